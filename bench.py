@@ -1,0 +1,298 @@
+"""Benchmark of the MI355X attention hot path on one GPU.
+
+Headline (`value`): config 1 -- Gated DeltaNet chunked prefill, one layer,
+batch 1, T = 4096, chunk 64 -- in tokens/s, inputs resident in HBM. The same
+JSON line carries the other configurations' figures under "configs", the
+roofline of the headline's dominant kernel (timed live with HIP events on the
+launch stream through qff_profile_*) and the CPU baseline (the fp32 oracle,
+one thread, on a bounded sample).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen-fieldfare_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+
+# Canonical work per unit ("Measurement")
+C0_BYTES = 4_424_448           # DeltaNet decode, one layer-step at B=1
+C0_FLOPS = 3_670_016
+C1_FLOPS = 23_622_320_128      # DeltaNet chunked prefill T=4096
+C1_BYTES = 137_428_992
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _ctypes_profile(ctx, enable):
+    from qff._lib import check, lib
+    check("qff_profile_enable", lib().qff_profile_enable(ctx.handle, int(enable)))
+
+
+def _profile_read(ctx):
+    import ctypes
+    from qff._lib import check, lib
+    cap = 4096
+    names = (ctypes.c_char_p * cap)()
+    ms = (ctypes.c_float * cap)()
+    n = ctypes.c_int()
+    check("qff_profile_read", lib().qff_profile_read(ctx.handle, names, ms, cap, ctypes.byref(n)))
+    out = {}
+    for i in range(n.value):
+        out.setdefault(names[i].decode(), []).append(ms[i])
+    return out
+
+
+def timed(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def kernel_times(ctx, fn, steps):
+    """Per-kernel average durations (ms) over `steps` calls, from the
+    library's own hipEvent brackets on the launch stream."""
+    import torch
+    torch.cuda.synchronize()
+    _ctypes_profile(ctx, True)
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    rec = _profile_read(ctx)
+    _ctypes_profile(ctx, False)
+    return {k: sum(v) / len(v) for k, v in rec.items()}, {k: len(v) for k, v in rec.items()}
+
+
+def bf16_randn(shape, gen, std=1.0):
+    import torch
+    return (torch.randn(shape, generator=gen, device="cuda") * std).to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ configs
+def bench_c1(ctx, steps, warmup):
+    """Config 1: DeltaNet prefill T=4096 from zero state."""
+    import torch
+    import qff
+    from qff import synth
+    T = 4096
+    g = torch.Generator(device="cuda").manual_seed(1)
+    p = {k: torch.from_numpy(v).cuda() for k, v in synth.deltanet_params().items()}
+    qkv = bf16_randn((T, 8192), g)
+    z = bf16_randn((T, 4096), g)
+    a = torch.randn(T, 32, generator=g, device="cuda")
+    b = torch.randn(T, 32, generator=g, device="cuda")
+    conv = torch.zeros(8192, 4, device="cuda")
+    ssm = torch.zeros(32, 128, 128, device="cuda")
+    out = torch.empty(T, 4096, dtype=torch.bfloat16, device="cuda")
+
+    def step(i):
+        # every step starts from zero state, as the workload defines
+        conv.zero_()
+        ssm.zero_()
+        qff.deltanet_prefill(ctx, p, qkv, z, a, b, conv, ssm, out=out)
+
+    stream = torch.cuda.current_stream()
+    ms = timed(step, steps, warmup, stream)
+    kt, _ = kernel_times(ctx, step, max(3, min(steps, 10)))
+    return {"ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "kernels_ms": kt}
+
+
+def bench_c0(ctx, steps, warmup, sets=128):
+    """Config 0: DeltaNet decode B=1, one layer-step, rotating over `sets`
+    distinct state/input sets so the 4.4 MB working set comes from HBM."""
+    import torch
+    import qff
+    from qff import synth
+    g = torch.Generator(device="cuda").manual_seed(0)
+    p = {k: torch.from_numpy(v).cuda() for k, v in synth.deltanet_params().items()}
+    qkv = bf16_randn((sets, 1, 8192), g)
+    z = bf16_randn((sets, 1, 4096), g)
+    a = torch.randn(sets, 1, 32, generator=g, device="cuda")
+    b = torch.randn(sets, 1, 32, generator=g, device="cuda")
+    conv = torch.randn(sets, 1, 8192, 4, generator=g, device="cuda")
+    ssm = torch.randn(sets, 1, 32, 128, 128, generator=g, device="cuda") * 0.02
+    out = torch.empty(sets, 1, 4096, dtype=torch.bfloat16, device="cuda")
+
+    def step(i):
+        j = i % sets
+        qff.deltanet_decode(ctx, p, qkv[j], z[j], a[j], b[j], conv[j], ssm[j], out=out[j])
+
+    stream = torch.cuda.current_stream()
+    ms = timed(step, steps, warmup, stream)
+    kt, _ = kernel_times(ctx, step, min(steps, 256))
+    k = kt["deltanet_decode"]
+    return {"ms_per_step": ms, "tokens_per_s": 1.0 / (ms * 1e-3),
+            "kernel_us": k * 1e3, "kernel_GBps": C0_BYTES / (k * 1e-3) / 1e9,
+            "hbm_frac": C0_BYTES / (k * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_dn_decode_batch(ctx, B, steps, warmup):
+    """DeltaNet decode at batch B (the config-4 decode shape), one layer."""
+    import torch
+    import qff
+    from qff import synth
+    sets = max(1, 256 // B)
+    g = torch.Generator(device="cuda").manual_seed(B)
+    p = {k: torch.from_numpy(v).cuda() for k, v in synth.deltanet_params().items()}
+    qkv = bf16_randn((sets, B, 8192), g)
+    z = bf16_randn((sets, B, 4096), g)
+    a = torch.randn(sets, B, 32, generator=g, device="cuda")
+    b = torch.randn(sets, B, 32, generator=g, device="cuda")
+    conv = torch.randn(sets, B, 8192, 4, generator=g, device="cuda")
+    ssm = torch.randn(sets, B, 32, 128, 128, generator=g, device="cuda") * 0.02
+    out = torch.empty(sets, B, 4096, dtype=torch.bfloat16, device="cuda")
+
+    def step(i):
+        j = i % sets
+        qff.deltanet_decode(ctx, p, qkv[j], z[j], a[j], b[j], conv[j], ssm[j], out=out[j])
+
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    kt, _ = kernel_times(ctx, step, min(steps, 64))
+    k = kt["deltanet_decode"]
+    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "kernel_us": k * 1e3,
+            "kernel_GBps": B * C0_BYTES / (k * 1e-3) / 1e9,
+            "hbm_frac": B * C0_BYTES / (k * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_c2(ctx, B, steps, warmup, max_ctx=8192):
+    """Config 2: GQA decode at batch B, context 8192, random lengths."""
+    import numpy as np
+    import torch
+    import qff
+    from qff import synth
+    pools = max(2, 64 // B)
+    rng = np.random.default_rng(1000 + B)
+    lengths = rng.integers(1, max_ctx + 1, B)
+    g = torch.Generator(device="cuda").manual_seed(B)
+    p = {k: torch.from_numpy(v).cuda() for k, v in synth.gqa_params().items()}
+    kc = [bf16_randn((B, max_ctx, 2, 256), g) for _ in range(pools)]
+    vc = [bf16_randn((B, max_ctx, 2, 256), g) for _ in range(pools)]
+    qg = bf16_randn((B, 16, 512), g)
+    kn = bf16_randn((B, 2, 256), g)
+    vn = bf16_randn((B, 2, 256), g)
+    pos = torch.from_numpy((lengths - 1).astype(np.int32)).cuda()
+    out = torch.empty(B, 16, 256, dtype=torch.bfloat16, device="cuda")
+
+    def step(i):
+        j = i % pools
+        qff.gqa_decode(ctx, p, qg, kn, vn, kc[j], vc[j], pos, out=out)
+
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    kt, _ = kernel_times(ctx, step, min(steps, 64))
+    nbytes = int(np.sum(2048 * lengths.astype(np.int64) + 29_696))
+    flops = int(np.sum(16_384 * lengths.astype(np.int64)))
+    part = kt["gqa_decode_partial"] + kt.get("gqa_decode_combine", 0.0)
+    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "mean_len": float(lengths.mean()),
+            "kernels_us": {k: v * 1e3 for k, v in kt.items()},
+            "GBps": nbytes / (part * 1e-3) / 1e9, "hbm_frac": nbytes / (part * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "TFLOPs": flops / (part * 1e-3) / 1e12}
+
+
+def cpu_baseline_c1(budget_s=20.0):
+    """The fp32 reference-order oracle (sequential, one thread) on the
+    config-1 workload: as many tokens as fit in ~budget_s of CPU."""
+    import numpy as np
+    from oracle import oracle as O
+    from qff import synth
+    T = 4096
+    p = synth.deltanet_params()
+    inp = synth.deltanet_prefill_inputs(T)
+    qkv, z = O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"])
+    # calibrate on 64 tokens, then run a bounded prefix
+    t0 = time.perf_counter()
+    O.deltanet_sequence(qkv[:64], z[:64], inp["a"][:64], inp["b"][:64], p["a_log"], p["dt_bias"],
+                        p["conv_w"], p["norm_w"], inp["conv_state"], inp["ssm_state"])
+    per_tok = (time.perf_counter() - t0) / 64
+    n = int(min(T, max(64, budget_s / per_tok)))
+    t0 = time.perf_counter()
+    O.deltanet_sequence(qkv[:n], z[:n], inp["a"][:n], inp["b"][:n], p["a_log"], p["dt_bias"],
+                        p["conv_w"], p["norm_w"], inp["conv_state"], inp["ssm_state"])
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"first {n} of the 4096 config-1 tokens through the fp32 sequential oracle "
+                      f"(oracle/qff_oracle.c, gcc -O2), 1 thread, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,dnb")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    import qff
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "dnb"}
+    ctx = qff.Context(max_batch=32, max_ctx=8192, max_prefill_tokens=4096)
+    configs = {}
+    if "c0" in only:
+        log("config 0: DeltaNet decode B=1")
+        configs["c0_deltanet_decode_b1"] = bench_c0(ctx, max(args.steps * 50, 500), args.warmup * 10)
+    if "dnb" in only:
+        for B in (16, 32):
+            log(f"DeltaNet decode B={B}")
+            configs[f"deltanet_decode_b{B}"] = bench_dn_decode_batch(ctx, B, max(args.steps * 5, 100), args.warmup)
+    if "c2" in only:
+        for B in (1, 8, 32):
+            log(f"config 2: GQA decode B={B}")
+            configs[f"c2_gqa_decode_b{B}"] = bench_c2(ctx, B, max(args.steps * 10, 200), args.warmup)
+    c1 = None
+    if "c1" in only:
+        log("config 1: DeltaNet prefill T=4096")
+        c1 = bench_c1(ctx, args.steps, args.warmup)
+        configs["c1_deltanet_prefill_t4096"] = c1
+    cpu = None
+    if not args.skip_cpu and c1 is not None:
+        log("cpu baseline (oracle, 1 thread)")
+        cpu = cpu_baseline_c1()
+
+    roof = None
+    if c1 is not None:
+        kt = c1["kernels_ms"]
+        dom = max(kt, key=kt.get)
+        achieved = C1_FLOPS / (kt[dom] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None, "kernel": dom,
+                "kernel_ms": kt[dom],
+                "hbm_GBps": C1_BYTES / (kt[dom] * 1e-3) / 1e9}
+    value = c1["tokens_per_s"] if c1 else None
+    line = {
+        "metric": "attn tokens/s: DeltaNet+GQA decode (B=1..32) & 8K prefill; % HBM/MFMA roofline",
+        "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": c1["ms_per_step"] if c1 else None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 in/out, fp32 state+accum", "data": "synthetic",
+        "config": {"workload": "config 1: Gated DeltaNet chunked prefill, 1 layer, B=1, T=4096, C=64",
+                   "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)"},
+        "roofline": roof, "cpu_baseline": cpu, "configs": configs,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,107 @@
+// internal.hpp -- host-side context and the launchers each kernel file
+// provides. Not part of the public ABI (include/qff/qff.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "qff/qff.h"
+
+struct qff_prof_record {
+    const char* name;
+    hipEvent_t start, stop;
+};
+
+struct qff_ctx {
+    int device = 0;
+    qff_ctx_cfg cfg{};
+    // One device allocation, carved into the regions below.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // DeltaNet decode: one arrival counter per (sequence, key head), zero
+    // between calls, and the pre-norm per-row outputs.
+    int* dn_counters = nullptr;   // [max_batch * 16]
+    float* dn_o_raw = nullptr;    // [max_batch * 4096]
+    // Full-attention decode: split-KV partials per (sequence, kv head, chunk).
+    float* gqa_m = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8]
+    float* gqa_d = nullptr;       // same
+    float* gqa_o = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8 * 256]
+    // Prefill staging (DeltaNet): per-token prepared q, k, v, gates.
+    float* pf_q = nullptr;        // [T * 16 * 128]
+    float* pf_k = nullptr;        // [T * 16 * 128]
+    float* pf_v = nullptr;        // [T * 32 * 128]
+    float* pf_g = nullptr;        // [T * 32] log gate
+    float* pf_beta = nullptr;     // [T * 32]
+    float* pf_o = nullptr;        // [T * 32 * 128] pre-norm output
+    // Kernel timing (qff_profile_enable): a pool of event pairs.
+    bool prof = false;
+    std::vector<qff_prof_record> prof_pool;
+    int prof_n = 0;
+};
+
+namespace qff {
+
+constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head)
+
+struct WorkspaceLayout {
+    size_t dn_counters, dn_o_raw, gqa_m, gqa_d, gqa_o;
+    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o;
+    size_t total;
+};
+WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
+
+// Brackets the kernels launched in its scope with the context's profiling
+// events when profiling is on; costs one branch otherwise.
+struct ProfScope {
+    qff_ctx* ctx;
+    hipStream_t stream;
+    int idx = -1;
+    ProfScope(qff_ctx* c, hipStream_t s, const char* name) : ctx(c), stream(s) {
+        if (c && c->prof && c->prof_n < static_cast<int>(c->prof_pool.size())) {
+            idx = c->prof_n++;
+            c->prof_pool[idx].name = name;
+            (void)hipEventRecord(c->prof_pool[idx].start, s);
+        }
+    }
+    ~ProfScope() {
+        if (idx >= 0) (void)hipEventRecord(ctx->prof_pool[idx].stop, stream);
+    }
+};
+
+inline bool dtype_ok(qff_dtype d, bool allow_f16 = false) {
+    return d == QFF_F32 || d == QFF_BF16 || (allow_f16 && d == QFF_F16);
+}
+
+// Launchers: validate nothing (qff_api.cpp does), enqueue on `stream`,
+// return the HIP status of the launch.
+hipError_t launch_deltanet_decode(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
+                                  const void* qkv, const void* z, qff_dtype in_dtype,
+                                  const float* a, const float* b, float* conv_state,
+                                  float* ssm_state, void* out, qff_dtype out_dtype, int batch);
+hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
+                                   const void* qkv, const void* z, qff_dtype in_dtype,
+                                   const float* a, const float* b, float* conv_state,
+                                   float* ssm_state, void* out, qff_dtype out_dtype, int T);
+hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
+                             const void* q_gate, const void* k_new, const void* v_new,
+                             qff_dtype in_dtype, void* k_cache, void* v_cache,
+                             const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
+                             int max_ctx);
+hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
+                              const void* q_gate, const void* k, const void* v, qff_dtype in_dtype,
+                              void* k_cache, void* v_cache, int start_pos, void* out,
+                              qff_dtype out_dtype, int T, int max_ctx);
+hipError_t launch_q4_dequant(hipStream_t stream, const uint32_t* w, const void* scales,
+                             const void* biases, qff_dtype sb_dtype, float* out, int rows, int cols);
+hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
+                            const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
+                            void* y, qff_dtype y_dtype, int rows, int cols, int batch);
+hipError_t launch_kv_append(hipStream_t stream, const float* k, const float* v, void* k_cache,
+                            void* v_cache, qff_dtype cache_dtype, int pos, int max_seq);
+hipError_t launch_attention_gate(hipStream_t stream, const uint16_t* attn, const float* gate,
+                                 float* out, int count);
+
+}  // namespace qff

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports every entry point include/qff/qff.h
+declares, and the host-side argument checks that need no GPU behave. No
+compute call runs here (this container has no GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qff", "qff.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(qff_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_expected_surface():
+    fns = declared_functions()
+    for name in ("qff_ctx_create", "qff_ctx_destroy", "qff_workspace_size", "qff_status_string",
+                 "qff_version", "qff_q4_dequant", "qff_q4_matmul", "qff_deltanet_decode",
+                 "qff_deltanet_prefill", "qff_gqa_decode", "qff_gqa_prefill", "qff_kv_append",
+                 "qff_attention_gate"):
+        assert name in fns
+
+
+def test_library_exports_every_declared_symbol():
+    import qff
+    from qff._lib import SIGNATURES
+    L = qff.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), f"{name} missing from {qff.LIB_PATH}"
+        assert name in SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_strings_and_version():
+    import qff
+    L = qff.lib()
+    assert L.qff_status_string(0) == b"ok"
+    assert L.qff_status_string(-4) == b"request exceeds the context workspace"
+    assert L.qff_status_string(12345) == b"unknown status"
+    assert L.qff_version() >= 1
+
+
+def test_workspace_size_and_argument_checks_without_gpu():
+    import qff
+    from qff._lib import CtxCfg
+    L = qff.lib()
+    n = ctypes.c_size_t()
+    assert L.qff_workspace_size(None, ctypes.byref(n)) == 0 and n.value > 0
+    small = CtxCfg(1, 1024, 1)
+    m = ctypes.c_size_t()
+    assert L.qff_workspace_size(ctypes.byref(small), ctypes.byref(m)) == 0
+    assert 0 < m.value < n.value
+    assert L.qff_workspace_size(ctypes.byref(CtxCfg(-1, 0, 0)), ctypes.byref(m)) == -1
+    assert L.qff_workspace_size(None, None) == -1
+    # null context / outputs are rejected before any HIP call
+    assert L.qff_ctx_create(None, 0, None) == -1
+    assert L.qff_ctx_destroy(None) == -1
+    N = None
+    assert L.qff_deltanet_decode(N, N, N, N, N, 1, N, N, N, N, N, 1, 1) == -1
+    assert L.qff_gqa_decode(N, N, N, N, N, N, 1, N, N, N, N, 1, 1, 16) == -1
+    assert L.qff_q4_matmul(N, N, N, N, N, 2, N, 1, N, 0, 64, 64, 1) == -1
+
+
+def test_product_has_no_cpu_fallback():
+    """The product package never imports the oracle."""
+    pkg = os.path.join(ROOT, "qwen-fieldfare_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                src = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"(from|import)\s+oracle|qff_oracle|libqff_oracle", src), f

@@ -1,0 +1,156 @@
+"""GPU parity of the DeltaNet entry points (qff_deltanet_decode / _prefill)
+against the fp32 reference-order oracle (QwenDeltaNetKernel.swift:39-151 fed
+token by token, QwenQ4ActiveExpertStreamingRunner.swift:1545-1561).
+
+Tolerances (stated by the workload): outputs max-abs <= 2e-2 (bf16 outputs
+may also be one bf16 ulp off where that exceeds 2e-2), fp32 state per-head
+Frobenius relative error <= 1e-4. The conv state only shifts stored values,
+so it must match bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import (DEV, assert_bf16_output_close, assert_f32_output_close, bf16_tensor,
+                      f32_tensor, state_rel_err, to_np)
+from oracle import oracle as O
+from qff import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _params_gpu(p):
+    return {k: f32_tensor(v) for k, v in p.items()}
+
+
+def _oracle_decode(p, inp, in_f32=False):
+    B = inp["qkv"].shape[0]
+    outs, convs, ssms = [], [], []
+    for s in range(B):
+        qkv = inp["qkv_f32"][s] if in_f32 else O.bf16_to_f32(inp["qkv"][s])
+        z = inp["z_f32"][s] if in_f32 else O.bf16_to_f32(inp["z"][s])
+        o, c, st = O.deltanet_sequence(qkv[None], z[None], inp["a"][s][None], inp["b"][s][None],
+                                       p["a_log"], p["dt_bias"], p["conv_w"], p["norm_w"],
+                                       inp["conv_state"][s], inp["ssm_state"][s])
+        outs.append(o[0]); convs.append(c); ssms.append(st)
+    return np.stack(outs), np.stack(convs), np.stack(ssms)
+
+
+@pytest.mark.parametrize("B", [1, 3, 16])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
+    import qff
+    print(f"deltanet_decode B={B} out={out_dtype}", flush=True)
+    p = synth.deltanet_params()
+    inp = synth.deltanet_decode_inputs(B, seed=100 + B)
+    ref_o, ref_c, ref_s = _oracle_decode(p, inp)
+    ctx = qff.Context(max_batch=32, max_prefill_tokens=1)
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = qff.deltanet_decode(ctx, _params_gpu(p), bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"]),
+                              f32_tensor(inp["a"]), f32_tensor(inp["b"]), conv, ssm,
+                              out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    if out_dtype == torch.bfloat16:
+        assert_bf16_output_close(to_np(out), ref_o)
+    else:
+        assert_f32_output_close(to_np(out), ref_o)
+    assert np.array_equal(to_np(conv), ref_c)
+    assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+
+
+def test_deltanet_decode_f32_inputs_and_repeat(hip):
+    """fp32 activations, and three steps in a row on the same context: the
+    arrival counters must be back at zero after every call."""
+    import qff
+    p = synth.deltanet_params()
+    B = 4
+    inp = synth.deltanet_decode_inputs(B, seed=7)
+    ctx = qff.Context(max_batch=8, max_prefill_tokens=1)
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    pg = _params_gpu(p)
+    rng = np.random.default_rng(8)
+    for step in range(3):
+        inp["qkv_f32"] = rng.standard_normal((B, 8192)).astype(np.float32)
+        inp["z_f32"] = rng.standard_normal((B, 4096)).astype(np.float32)
+        inp["a"] = rng.standard_normal((B, 32)).astype(np.float32)
+        inp["b"] = rng.standard_normal((B, 32)).astype(np.float32)
+        ref_o, ref_c, ref_s = _oracle_decode(p, inp, in_f32=True)
+        out = qff.deltanet_decode(ctx, pg, f32_tensor(inp["qkv_f32"]), f32_tensor(inp["z_f32"]),
+                                  f32_tensor(inp["a"]), f32_tensor(inp["b"]), conv, ssm,
+                                  out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert_f32_output_close(to_np(out), ref_o)
+        assert np.array_equal(to_np(conv), ref_c)
+        assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+        inp["conv_state"], inp["ssm_state"] = ref_c, ref_s
+
+
+@pytest.mark.parametrize("T", [1, 3, 64, 200])
+def test_deltanet_prefill_matches_sequential_oracle(hip, T):
+    import qff
+    print(f"deltanet_prefill T={T}", flush=True)
+    p = synth.deltanet_params()
+    inp = synth.deltanet_prefill_inputs(T, seed=300 + T)
+    rng = np.random.default_rng(T)
+    # a non-zero starting state exercises the conv history and state carry-in
+    inp["conv_state"][:, 1:] = rng.standard_normal((8192, 3)).astype(np.float32)
+    inp["ssm_state"] = (rng.standard_normal((32, 128, 128)) * 0.02).astype(np.float32)
+    ref_o, ref_c, ref_s = O.deltanet_sequence(O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"]),
+                                              inp["a"], inp["b"], p["a_log"], p["dt_bias"],
+                                              p["conv_w"], p["norm_w"], inp["conv_state"],
+                                              inp["ssm_state"])
+    ctx = qff.Context(max_batch=1, max_prefill_tokens=256)
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = qff.deltanet_prefill(ctx, _params_gpu(p), bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"]),
+                               f32_tensor(inp["a"]), f32_tensor(inp["b"]), conv, ssm)
+    torch.cuda.synchronize()
+    assert_bf16_output_close(to_np(out), ref_o)
+    assert np.array_equal(to_np(conv), ref_c)
+    assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+
+
+def test_deltanet_prefill_config1_full_length(hip):
+    """Config 1 at its full size: T = 4096 from zero state, against the
+    4096-step sequential fp32 oracle (a few seconds of CPU)."""
+    import qff
+    p = synth.deltanet_params()
+    inp = synth.deltanet_prefill_inputs(4096)
+    print("deltanet_prefill T=4096 (oracle running)", flush=True)
+    ref_o, ref_c, ref_s = O.deltanet_sequence(O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"]),
+                                              inp["a"], inp["b"], p["a_log"], p["dt_bias"],
+                                              p["conv_w"], p["norm_w"], inp["conv_state"],
+                                              inp["ssm_state"])
+    ctx = qff.Context(max_batch=1, max_prefill_tokens=4096)
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = qff.deltanet_prefill(ctx, _params_gpu(p), bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"]),
+                               f32_tensor(inp["a"]), f32_tensor(inp["b"]), conv, ssm)
+    torch.cuda.synchronize()
+    assert_bf16_output_close(to_np(out), ref_o)
+    assert np.array_equal(to_np(conv), ref_c)
+    assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+
+
+def test_deltanet_rejects_bad_arguments(hip):
+    import qff
+    p = _params_gpu(synth.deltanet_params())
+    ctx = qff.Context(max_batch=2, max_prefill_tokens=16)
+    x = torch.zeros(4, 8192, dtype=torch.bfloat16, device=DEV)
+    z = torch.zeros(4, 4096, dtype=torch.bfloat16, device=DEV)
+    ab = torch.zeros(4, 32, device=DEV)
+    conv = torch.zeros(4, 8192, 4, device=DEV)
+    ssm = torch.zeros(4, 32, 128, 128, device=DEV)
+    with pytest.raises(qff.QffError) as e:           # batch above the context's max
+        qff.deltanet_decode(ctx, p, x, z, ab, ab, conv, ssm)
+    assert e.value.status == -4
+    with pytest.raises(qff.QffError) as e:           # chunk other than 64
+        qff.deltanet_prefill(ctx, p, x, z, ab, ab, conv[0], ssm[0], chunk=32)
+    assert e.value.status == -2
+    with pytest.raises(qff.QffError) as e:           # T above max_prefill_tokens
+        qff.deltanet_prefill(ctx, p, torch.zeros(17, 8192, dtype=torch.bfloat16, device=DEV),
+                             torch.zeros(17, 4096, dtype=torch.bfloat16, device=DEV),
+                             torch.zeros(17, 32, device=DEV), torch.zeros(17, 32, device=DEV),
+                             conv[0], ssm[0])
+    assert e.value.status == -4

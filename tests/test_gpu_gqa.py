@@ -1,0 +1,121 @@
+"""GPU parity of qff_gqa_decode against the fp32 reference-order oracle
+(deltanet.metal:599-708, attention.metal:134-377, Attention.swift:129-157,
+QwenQ4ActiveExpertStreamingRunner.swift:1076-1150, with the reference's
+half rounding of q and of the attention output).
+
+Tolerance: outputs max-abs <= 2e-2 (bf16 outputs may also be one bf16 ulp
+off where that exceeds 2e-2). The appended cache entries are the bf16
+rounding of fp32 values that the two sides compute in a different order, so
+they must agree to one bf16 ulp; every other cache entry must be untouched."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import (DEV, assert_bf16_output_close, assert_f32_output_close, bf16_tensor,
+                      bf16_ulp, f32_tensor, to_np)
+from oracle import oracle as O
+from qff import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_case(hip, lengths, max_ctx, out_dtype=torch.float32, seed=11):
+    import qff
+    B = len(lengths)
+    print(f"gqa_decode B={B} max_ctx={max_ctx} lengths={list(lengths)[:8]}", flush=True)
+    p = synth.gqa_params()
+    inp = synth.gqa_decode_inputs(B, max_ctx, seed=seed, lengths=lengths)
+    ctx = qff.Context(max_batch=max(B, 1), max_ctx=max_ctx, max_prefill_tokens=1)
+    kc = bf16_tensor(inp["k_cache"])
+    vc = bf16_tensor(inp["v_cache"])
+    pg = {k: f32_tensor(v) for k, v in p.items()}
+    pos_t = torch.from_numpy(inp["positions"]).to(DEV)
+    out = qff.gqa_decode(ctx, pg, bf16_tensor(inp["q_gate"]), bf16_tensor(inp["k_new"]),
+                         bf16_tensor(inp["v_new"]), kc, vc, pos_t, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    kc_g = kc.cpu().view(torch.int16).numpy().view(np.uint16)
+    vc_g = vc.cpu().view(torch.int16).numpy().view(np.uint16)
+    for s in range(B):
+        pos = int(inp["positions"][s])
+        kref = inp["k_cache"][s].copy()
+        vref = inp["v_cache"][s].copy()
+        O.gqa_append_kv_seq(O.bf16_to_f32(inp["k_new"][s])[None], O.bf16_to_f32(inp["v_new"][s])[None],
+                            p["k_norm_w"], kref, vref, O.BF16, start_pos=pos)
+        ref = O.gqa_attend(O.bf16_to_f32(inp["q_gate"][s]), p["q_norm_w"], kref, vref, O.BF16, pos)
+        if out_dtype == torch.bfloat16:
+            assert_bf16_output_close(got[s], ref)
+        else:
+            assert_f32_output_close(got[s], ref)
+        # cache: only row `pos` changed, and to within one bf16 ulp
+        mask = np.ones(max_ctx, bool)
+        mask[pos] = False
+        assert np.array_equal(kc_g[s][mask], inp["k_cache"][s][mask])
+        assert np.array_equal(vc_g[s][mask], inp["v_cache"][s][mask])
+        assert np.array_equal(vc_g[s][pos], vref[pos])
+        kr = O.bf16_to_f32(kref[pos])
+        assert np.all(np.abs(O.bf16_to_f32(kc_g[s][pos]) - kr) <= bf16_ulp(kr))
+
+
+def test_gqa_decode_batch1_full_context(hip):
+    _run_case(hip, [8192], 8192)
+
+
+def test_gqa_decode_edges(hip):
+    # L = 1 (pos 0), chunk boundaries of the split, and odd lengths
+    _run_case(hip, [1, 2, 15, 16, 17, 63, 64, 65, 127, 128, 129, 1000, 2047, 2048], 2048)
+
+
+@pytest.mark.parametrize("B", [8, 32])
+def test_gqa_decode_batch_random_lengths(hip, B):
+    rng = np.random.default_rng(B)
+    _run_case(hip, rng.integers(1, 8193, B), 8192, out_dtype=torch.bfloat16, seed=B)
+
+
+def test_gqa_decode_long_context(hip):
+    # 64K context (config 4's single-sequence decode) at two positions
+    _run_case(hip, [65536, 40000], 65536)
+
+
+def test_kv_append_and_gate_kats(hip):
+    """The reference's own GPU KATs (QwenFP16AttentionBridgeTests.swift:8-86)
+    through qff_kv_append and qff_attention_gate."""
+    import ctypes
+    import json
+    import os
+    import qff
+    from qff._lib import check, lib
+    kats = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+    k = kats["kv_writer"]
+    ctx = qff.Context(max_batch=1, max_ctx=16, max_prefill_tokens=1)
+    kin = f32_tensor(np.array(k["k"], np.float32))
+    vin = f32_tensor(np.array(k["v"], np.float32))
+    for dt, code in ((torch.float16, 2), (torch.bfloat16, 1)):
+        kc = torch.zeros(k["max_seq"], 2, 256, dtype=dt, device=DEV)
+        vc = torch.zeros_like(kc)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check("qff_kv_append", lib().qff_kv_append(ctx.handle, st, ctypes.c_void_p(kin.data_ptr()),
+                                                   ctypes.c_void_p(vin.data_ptr()),
+                                                   ctypes.c_void_p(kc.data_ptr()),
+                                                   ctypes.c_void_p(vc.data_ptr()), code,
+                                                   k["position"], k["max_seq"]))
+        torch.cuda.synchronize()
+        kb = kc.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+        vb = vc.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+        off = k["token_offset"]
+        assert np.all(kb[:off] == 0) and np.all(vb[:off] == 0) and np.all(kb[off + 512:] == 0)
+        if code == 2:
+            assert kb[off:off + 512].tolist() == k["k_f16_bits"]
+            assert vb[off:off + 512].tolist() == k["v_f16_bits"]
+        else:
+            assert np.array_equal(kb[off:off + 512], O.f32_to_bf16(np.array(k["k"], np.float32)))
+    g = kats["attention_gate"]
+    att = torch.from_numpy(np.array(g["attention_f16_bits"], np.uint16).view(np.int16)).to(DEV)
+    gate = f32_tensor(np.array(g["gate"], np.float32))
+    out = torch.empty(4, device=DEV)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    check("qff_attention_gate", lib().qff_attention_gate(ctx.handle, st, ctypes.c_void_p(att.data_ptr()),
+                                                         ctypes.c_void_p(gate.data_ptr()),
+                                                         ctypes.c_void_p(out.data_ptr()), 4))
+    torch.cuda.synchronize()
+    assert np.all(np.abs(to_np(out) - np.array(g["expected"])) < g["tol"])

@@ -1,0 +1,82 @@
+"""GPU parity of the affine-Q4 entry points.
+
+qff_q4_dequant must be bit-exact with the closed form
+(QwenQ4ActiveExpertStreamingRunner.swift:899-922) for f16 and bf16 scales.
+qff_q4_matmul is checked against an fp64 product of the dequantized matrix:
+with bf16 activations (exact MFMA operands) the relative Frobenius error must
+stay <= 1e-5 (fp32 accumulation order only); with fp32 activations, which the
+matrix cores take rounded to bf16, <= 1e-2 against the reference's own fp32
+factored order (deltanet.metal:816-861)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, bf16_tensor, f16_tensor, f32_tensor, to_np
+from oracle import oracle as O
+from qff import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _w_gpu(w, s, b, sb):
+    wt = torch.from_numpy(w.view(np.int32)).to(DEV)
+    conv = f16_tensor if sb == "f16" else bf16_tensor
+    return wt, conv(s), conv(b)
+
+
+@pytest.mark.parametrize("rows,cols,sb", [(512, 2048, "f16"), (2048, 4096, "bf16"), (17, 64, "f16"),
+                                          (8192, 2048, "bf16")])
+def test_q4_dequant_bit_exact(hip, rows, cols, sb):
+    import qff
+    print(f"q4_dequant {rows}x{cols} {sb}", flush=True)
+    w, s, b = synth.q4_weight(rows, cols, seed=rows + cols, sb_dtype=sb)
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    out = qff.q4_dequant(ctx, *_w_gpu(w, s, b, sb))
+    torch.cuda.synchronize()
+    ref = O.q4_dequant(w, s, b, O.F16 if sb == "f16" else O.BF16)
+    assert np.array_equal(to_np(out).view(np.uint32), ref.view(np.uint32))
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(8192, 2048, 1), (512, 2048, 5), (4096, 2048, 16),
+                                             (2048, 4096, 32), (100, 2048, 33), (32, 2048, 1)])
+def test_q4_matmul_bf16_activations(hip, rows, cols, batch):
+    import qff
+    print(f"q4_matmul {rows}x{cols} batch={batch}", flush=True)
+    w, s, b = synth.q4_weight(rows, cols, seed=rows * 3 + batch)
+    rng = np.random.default_rng(batch)
+    xb = O.f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32))
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    y = qff.q4_matmul(ctx, *_w_gpu(w, s, b, "f16"), bf16_tensor(xb))
+    torch.cuda.synchronize()
+    dense = O.q4_dequant(w, s, b, O.F16).astype(np.float64)
+    ref = O.bf16_to_f32(xb).astype(np.float64) @ dense.T
+    assert _rel(to_np(y), ref) <= 1e-5
+
+
+def test_q4_matmul_f32_activations_vs_reference_order(hip):
+    import qff
+    rows, cols = 2048, 4096
+    w, s, b = synth.q4_weight(rows, cols, seed=99)
+    x = np.random.default_rng(5).standard_normal((2, cols)).astype(np.float32)
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    y = qff.q4_matmul(ctx, *_w_gpu(w, s, b, "f16"), f32_tensor(x))
+    yb = qff.q4_matmul(ctx, *_w_gpu(w, s, b, "f16"), f32_tensor(x), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    for m in range(2):
+        ref = O.q4_matvec(w, s, b, x[m])
+        assert _rel(to_np(y)[m], ref) <= 1e-2
+        assert _rel(to_np(yb)[m], ref) <= 1e-2
+
+
+def test_q4_rejects_bad_shapes(hip):
+    import qff
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    w = torch.zeros(4, 12, dtype=torch.int32, device=DEV)          # cols = 96: not a multiple of 64
+    s = torch.zeros(4, 1, dtype=torch.float16, device=DEV)
+    with pytest.raises(qff.QffError) as e:
+        qff.q4_dequant(ctx, w, s, s)
+    assert e.value.status == -2
