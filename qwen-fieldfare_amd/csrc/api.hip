@@ -1,6 +1,7 @@
 // api.hip -- the extern "C" entry points of include/qff/qff.h: argument
 // validation, the context and its workspace, and the two small kernels
 // (raw KV append, f16 attention gate) that do not belong to a larger file.
+#include <math.h>
 #include <string.h>
 
 #include <new>
@@ -40,6 +41,12 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.pf_o = take(T * 4096 * sizeof(float));
     L.total = off;
     return L;
+}
+
+RopeFreqs rope_freqs(float theta) {
+    RopeFreqs r;
+    for (int i = 0; i < 32; ++i) r.f[i] = 1.0f / powf(theta, static_cast<float>(2 * i) / 64.0f);
+    return r;
 }
 
 // out = float(attn_f16) * sigmoid(gate): deltanet.metal:700-708.

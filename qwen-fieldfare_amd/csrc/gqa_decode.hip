@@ -35,7 +35,7 @@ constexpr int kVtStride = 20;  // bf16 per transposed V row: 16 positions + pad
 template <int IN_DT>
 __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
-    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, float theta, float scale,
+    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
     const int32_t* __restrict__ positions, int max_ctx, int chunk_len, float* __restrict__ pm,
     float* __restrict__ pd, float* __restrict__ po) {
@@ -57,9 +57,9 @@ __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
     __shared__ float wm[4][8], wd[4][8];
 
     // RoPE table for this position: QwenQ4ActiveExpertStreamingRunner.swift:1090-1099
+    // (the inverse frequencies come from the host, computed there in fp32)
     if (t < 32) {
-        const float freq = 1.0f / powf(theta, static_cast<float>(2 * t) / 64.0f);
-        const float ang = static_cast<float>(pos) * freq;
+        const float ang = static_cast<float>(pos) * rf.f[t];
         rcos[t] = cosf(ang);
         rsin[t] = sinf(ang);
     }
@@ -293,6 +293,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              int max_ctx) {
     const int ch = gqa_chunk_len(max_ctx);
     const int nc = (max_ctx + ch - 1) / ch;
+    const RopeFreqs rf = rope_freqs(p->rope_theta);
     const dim3 pgrid(nc, 2, batch);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
@@ -300,11 +301,11 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
     ProfScope prof(ctx, stream, "gqa_decode_partial");
     if (in_dtype == QFF_BF16)
         gqa_decode_partial_kernel<1><<<pgrid, 256, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
-                                                                p->rope_theta, p->scale, p->eps, kc, vc, positions,
+                                                                rf, p->scale, p->eps, kc, vc, positions,
                                                                 max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o);
     else
         gqa_decode_partial_kernel<0><<<pgrid, 256, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
-                                                                p->rope_theta, p->scale, p->eps, kc, vc, positions,
+                                                                rf, p->scale, p->eps, kc, vc, positions,
                                                                 max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o);
     }
     const dim3 cgrid(16, batch);

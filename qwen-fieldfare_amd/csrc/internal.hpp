@@ -71,6 +71,15 @@ struct ProfScope {
     }
 };
 
+// Inverse RoPE frequencies 1 / theta^(2i/64), i < 32, computed on the host
+// in fp32 as the reference does (QwenQ4ActiveExpertStreamingRunner.swift
+// :1090-1099) and passed to kernels by value; kernels form pos * f[i] and
+// its cos / sin themselves, so no table travels per token.
+struct RopeFreqs {
+    float f[32];
+};
+RopeFreqs rope_freqs(float theta);
+
 inline bool dtype_ok(qff_dtype d, bool allow_f16 = false) {
     return d == QFF_F32 || d == QFF_BF16 || (allow_f16 && d == QFF_F16);
 }
