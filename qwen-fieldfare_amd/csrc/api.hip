@@ -28,8 +28,6 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
     const size_t B = static_cast<size_t>(cfg.max_batch);
     const size_t T = static_cast<size_t>(cfg.max_prefill_tokens);
-    L.dn_counters = take(B * 16 * sizeof(int));
-    L.dn_o_raw = take(B * 4096 * sizeof(float));
     L.gqa_m = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
     L.gqa_d = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
     L.gqa_o = take(B * 2 * kGqaMaxChunks * 8 * 256 * sizeof(float));
@@ -141,8 +139,6 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     }
     c->ws_bytes = L.total;
     char* base = static_cast<char*>(c->ws);
-    c->dn_counters = reinterpret_cast<int*>(base + L.dn_counters);
-    c->dn_o_raw = reinterpret_cast<float*>(base + L.dn_o_raw);
     c->gqa_m = reinterpret_cast<float*>(base + L.gqa_m);
     c->gqa_d = reinterpret_cast<float*>(base + L.gqa_d);
     c->gqa_o = reinterpret_cast<float*>(base + L.gqa_o);
@@ -152,15 +148,6 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->pf_g = reinterpret_cast<float*>(base + L.pf_g);
     c->pf_beta = reinterpret_cast<float*>(base + L.pf_beta);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
-    // The arrival counters must start at zero; every decode call leaves them
-    // at zero again.
-    if (hipMemset(c->dn_counters, 0, static_cast<size_t>(c->cfg.max_batch) * 16 * sizeof(int)) != hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
-        (void)hipFree(c->ws);
-        delete c;
-        (void)hipSetDevice(prev);
-        return QFF_ERR_HIP;
-    }
     (void)hipSetDevice(prev);
     *out = c;
     return QFF_OK;

@@ -130,29 +130,41 @@ __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
     const uint16_t* Kb = k_cache + seq_base;
     const uint16_t* Vb = v_cache + seq_base;
 
-    for (int p0 = p_start + wave * 16; p0 < p_end; p0 += 64) {
-        // S^T = K Q^T: A = K rows p0 + n, dims 32jj + 8kb .. +7; rows past the
-        // chunk end re-read its last row (masked below) so no lane reads
-        // outside the chunk.
-        const int pr = min(p0 + n, p_end - 1);
-        const uint16_t* krow = Kb + static_cast<size_t>(pr) * 512;
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // K operand rows (A of 16x16x32: position p0 + n, dims 32jj + 8kb .. +7)
+    // and V rows (positions p0 + 4kb + i, dims 8(n + 16it) .. +7) of one tile.
+    // K rows past the chunk end re-read its last row (masked below) and V
+    // rows past it read as zero (their probability is 0, and the cache
+    // beyond the sequence may hold any bit pattern, NaN included), so no
+    // lane reads outside the chunk.
+    auto load_tile = [&](int p0, u32x4_t (&ka)[8], u32x4_t (&va)[2][4]) {
+        const uint16_t* krow = Kb + static_cast<size_t>(min(p0 + n, p_end - 1)) * 512;
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-            s = mfma_16x16x32_bf16(*reinterpret_cast<const u32x4_t*>(krow + 32 * jj + 8 * kb), qreg[jj], s);
-        // V rows for this tile: lane holds positions 4kb..4kb+3, dims 8dg..+7.
-        // Rows past the chunk end are zero (their probability is 0, and the
-        // cache beyond the sequence may hold any bit pattern, NaN included).
-        u32x4_t vr[2][4];
+        for (int jj = 0; jj < 8; ++jj) ka[jj] = *reinterpret_cast<const u32x4_t*>(krow + 32 * jj + 8 * kb);
 #pragma unroll
         for (int it = 0; it < 2; ++it)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int pp = p0 + 4 * kb + i;
-                vr[it][i] = pp < p_end
+                va[it][i] = pp < p_end
                     ? *reinterpret_cast<const u32x4_t*>(Vb + static_cast<size_t>(pp) * 512 + 8 * (n + 16 * it))
                     : u32x4_t{0u, 0u, 0u, 0u};
             }
+    };
+    u32x4_t kn[8], vn[2][4];
+    if (p_start + wave * 16 < p_end) load_tile(p_start + wave * 16, kn, vn);
+    for (int p0 = p_start + wave * 16; p0 < p_end; p0 += 64) {
+        u32x4_t kcur[8], vr[2][4];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) kcur[jj] = kn[jj];
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vr[it][i] = vn[it][i];
+        if (p0 + 64 < p_end) load_tile(p0 + 64, kn, vn);   // next tile in flight
+        // S^T = K Q^T
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) s = mfma_16x16x32_bf16(kcur[jj], qreg[jj], s);
         // online softmax: lane holds head n, positions p0 + 4kb + i
         float sv[4], tmax = -INFINITY;
 #pragma unroll
@@ -250,14 +262,18 @@ __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
     }
 }
 
-// grid (16 q heads, batch), 256 threads (one dim each): attention.metal:342-377
-// merge, then the gate of deltanet.metal:700-708.
+// grid (16 q heads, batch), 256 threads: attention.metal:342-377 merge, then
+// the gate of deltanet.metal:700-708. Chunk weights are formed in parallel
+// (one thread per chunk) and the dim loop issues 8 independent loads at a
+// time.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(
     const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int max_ctx, int chunk_len,
     const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
+    __shared__ float es[kGqaMaxChunks], red[8];
     const int h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
     const int kvh = h >> 3, hl = h & 7;
     const size_t qi = (static_cast<size_t>(seq) * 16 + h);
     const int pos = positions[seq];
@@ -268,21 +284,41 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(
     const int L = pos + 1;
     const int nc = (L + chunk_len - 1) / chunk_len;
     const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * kGqaMaxChunks;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pm[(base + c) * 8 + hl]);
-    float D = 0.0f, O = 0.0f;
-    for (int c = 0; c < nc; ++c) {
-        const float e = expf(pm[(base + c) * 8 + hl] - M);
-        D += pd[(base + c) * 8 + hl] * e;
-        O += po[((base + c) * 8 + hl) * 256 + t] * e;
+    const float m = t < nc ? pm[(base + t) * 8 + hl] : -INFINITY;
+    const float d = t < nc ? pd[(base + t) * 8 + hl] : 0.0f;
+    const float wmax = group_max<64>(m);
+    if (lane == 0) red[wave] = wmax;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float e = t < nc ? expf(m - M) : 0.0f;
+    if (t < kGqaMaxChunks) es[t] = e;
+    const float wd = group_sum<64>(d * e);
+    if (lane == 0) red[4 + wave] = wd;
+    __syncthreads();
+    const float D = red[4] + red[5] + red[6] + red[7];
+    const float* pr = po + (base * 8 + hl) * 256 + t;   // chunk c at pr[c * 8 * 256]
+    float O = 0.0f;
+    int c = 0;
+    for (; c + 8 <= nc; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = pr[static_cast<size_t>(c + u) * 2048];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) O += v[u] * es[c + u];
     }
+    for (; c < nc; ++c) O += pr[static_cast<size_t>(c) * 2048] * es[c];
     const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + t);
     elem<OUT_DT>::store(out, qi * 256 + t, (O / D) * sigmoid(gate));
 }
 
-int gqa_chunk_len(int max_ctx) {
-    int per = (max_ctx + kGqaMaxChunks - 1) / kGqaMaxChunks;
-    int ch = ((per + 63) / 64) * 64;
+// Chunk length: aim for ~2048 partial workgroups over the batch (8 per CU),
+// at most kGqaMaxChunks chunks per sequence, multiples of 64 positions.
+int gqa_chunk_len(int max_ctx, int batch) {
+    int target = 2048 / (2 * batch);
+    if (target < 1) target = 1;
+    if (target > kGqaMaxChunks) target = kGqaMaxChunks;
+    const int per = (max_ctx + target - 1) / target;
+    const int ch = ((per + 63) / 64) * 64;
     return ch < 64 ? 64 : ch;
 }
 
@@ -291,7 +327,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              qff_dtype in_dtype, void* k_cache, void* v_cache,
                              const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                              int max_ctx) {
-    const int ch = gqa_chunk_len(max_ctx);
+    const int ch = gqa_chunk_len(max_ctx, batch);
     const int nc = (max_ctx + ch - 1) / ch;
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     const dim3 pgrid(nc, 2, batch);

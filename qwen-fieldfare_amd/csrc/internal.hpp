@@ -21,10 +21,6 @@ struct qff_ctx {
     // One device allocation, carved into the regions below.
     void* ws = nullptr;
     size_t ws_bytes = 0;
-    // DeltaNet decode: one arrival counter per (sequence, key head), zero
-    // between calls, and the pre-norm per-row outputs.
-    int* dn_counters = nullptr;   // [max_batch * 16]
-    float* dn_o_raw = nullptr;    // [max_batch * 4096]
     // Full-attention decode: split-KV partials per (sequence, kv head, chunk).
     float* gqa_m = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8]
     float* gqa_d = nullptr;       // same
@@ -47,7 +43,7 @@ namespace qff {
 constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head)
 
 struct WorkspaceLayout {
-    size_t dn_counters, dn_o_raw, gqa_m, gqa_d, gqa_o;
+    size_t gqa_m, gqa_d, gqa_o;
     size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o;
     size_t total;
 };

@@ -59,8 +59,8 @@ def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
 
 
 def test_deltanet_decode_f32_inputs_and_repeat(hip):
-    """fp32 activations, and three steps in a row on the same context: the
-    arrival counters must be back at zero after every call."""
+    """fp32 activations, and three steps in a row on the same context and
+    state buffers."""
     import qff
     p = synth.deltanet_params()
     B = 4

@@ -119,3 +119,52 @@ def test_kv_append_and_gate_kats(hip):
                                                          ctypes.c_void_p(out.data_ptr()), 4))
     torch.cuda.synchronize()
     assert np.all(np.abs(to_np(out) - np.array(g["expected"])) < g["tol"])
+
+
+def _prefill_case(hip, T, start, max_ctx, rows=None, out_dtype=torch.bfloat16, seed=21):
+    import qff
+    print(f"gqa_prefill T={T} start={start} max_ctx={max_ctx}", flush=True)
+    rng = np.random.default_rng(seed)
+    p = synth.gqa_params()
+    qg = O.f32_to_bf16(rng.standard_normal((T, 16, 512)).astype(np.float32))
+    kk = O.f32_to_bf16(rng.standard_normal((T, 2, 256)).astype(np.float32))
+    vv = O.f32_to_bf16(rng.standard_normal((T, 2, 256)).astype(np.float32))
+    kc0 = O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32))
+    vc0 = O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32))
+    ctx = qff.Context(max_batch=1, max_ctx=max_ctx, max_prefill_tokens=T)
+    kc, vc = bf16_tensor(kc0), bf16_tensor(vc0)
+    pg = {k: f32_tensor(v) for k, v in p.items()}
+    out = qff.gqa_prefill(ctx, pg, bf16_tensor(qg), bf16_tensor(kk), bf16_tensor(vv), kc, vc,
+                          start_pos=start, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    kref, vref = kc0.copy(), vc0.copy()
+    O.gqa_append_kv_seq(O.bf16_to_f32(kk), O.bf16_to_f32(vv), p["k_norm_w"], kref, vref, O.BF16,
+                        start_pos=start)
+    kc_g = kc.cpu().view(torch.int16).numpy().view(np.uint16)
+    vc_g = vc.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(vc_g, vref)
+    outside = np.ones(max_ctx, bool)
+    outside[start:start + T] = False
+    assert np.array_equal(kc_g[outside], kc0[outside])
+    kr = O.bf16_to_f32(kref[start:start + T])
+    assert np.all(np.abs(O.bf16_to_f32(kc_g[start:start + T]) - kr) <= bf16_ulp(kr))
+    for t in (range(T) if rows is None else rows):
+        ref = O.gqa_attend(O.bf16_to_f32(qg[t]), p["q_norm_w"], kref, vref, O.BF16, start + t)
+        if out_dtype == torch.bfloat16:
+            assert_bf16_output_close(got[t], ref)
+        else:
+            assert_f32_output_close(got[t], ref)
+
+
+@pytest.mark.parametrize("T,start", [(1, 0), (17, 0), (100, 0), (64, 37), (300, 1000)])
+def test_gqa_prefill_matches_token_by_token(hip, T, start):
+    _prefill_case(hip, T, start, max_ctx=2048, out_dtype=torch.float32 if T == 17 else torch.bfloat16)
+
+
+def test_gqa_prefill_config3_full_length_sampled_rows(hip):
+    """T = 8192 from position 0: every appended K/V entry, and a sample of
+    output rows (first, last, tile and block boundaries, random)."""
+    rows = sorted({0, 1, 15, 16, 31, 32, 33, 1000, 4095, 4096, 8190, 8191} |
+                  set(np.random.default_rng(3).integers(0, 8192, 6).tolist()))
+    _prefill_case(hip, 8192, 0, max_ctx=8192, rows=rows)
