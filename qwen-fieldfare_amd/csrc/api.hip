@@ -37,6 +37,14 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.pf_g = take(T * 32 * sizeof(float));
     L.pf_beta = take(T * 32 * sizeof(float));
     L.pf_o = take(T * 4096 * sizeof(float));
+    const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
+    L.pf_wh = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_wl = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_uh = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_ul = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_ph = take(TC * 32 * 64 * sizeof(uint16_t));
+    L.pf_pl = take(TC * 32 * 64 * sizeof(uint16_t));
+    L.pf_G = take(TC * 32 * sizeof(float));
     L.total = off;
     return L;
 }
@@ -148,6 +156,13 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->pf_g = reinterpret_cast<float*>(base + L.pf_g);
     c->pf_beta = reinterpret_cast<float*>(base + L.pf_beta);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
+    c->pf_wh = reinterpret_cast<uint16_t*>(base + L.pf_wh);
+    c->pf_wl = reinterpret_cast<uint16_t*>(base + L.pf_wl);
+    c->pf_uh = reinterpret_cast<uint16_t*>(base + L.pf_uh);
+    c->pf_ul = reinterpret_cast<uint16_t*>(base + L.pf_ul);
+    c->pf_ph = reinterpret_cast<uint16_t*>(base + L.pf_ph);
+    c->pf_pl = reinterpret_cast<uint16_t*>(base + L.pf_pl);
+    c->pf_G = reinterpret_cast<float*>(base + L.pf_G);
     (void)hipSetDevice(prev);
     *out = c;
     return QFF_OK;

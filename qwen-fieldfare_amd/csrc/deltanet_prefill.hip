@@ -3,15 +3,13 @@
 //
 // The reference has no prefill kernel: prompts go token by token through the
 // decode path (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561). This file
-// computes the same recurrence for a whole sequence in four launches:
+// computes the same result for a whole sequence:
 //   prep       conv1d + SiLU over time for all 8192 channels (each token only
 //              needs the 3 previous inputs, so tokens run in parallel), L2
 //              norms of q (then / sqrt(128)) and k per key head, and the
-//              per-token gates g and beta of every value head;
-//   recurrent  one workgroup per (16-row block, value head) keeps its slice
-//              of the fp32 state in registers for the whole sequence and
-//              walks the tokens in order (the data for token t+1 is loaded
-//              while token t computes);
+//              per-token log gate and beta of every value head;
+//   chunked    the chunked WY form of the gated delta rule
+//              (deltanet_chunked.hip), pre-norm outputs to workspace;
 //   norm       gated RMSNorm of every (token, value head) output row;
 //   conv state the conv state after the last token.
 #include "common.hpp"
@@ -55,59 +53,9 @@ __global__ __launch_bounds__(128) void dn_prefill_prep_kernel(
     }
     if (blk == 0 && t < 32) {
         const int i = tok * 32 + t;
-        pg[i] = expf(-expf(a_log[t]) * softplus(a[i] + dt_bias[t]));
+        pg[i] = -expf(a_log[t]) * softplus(a[i] + dt_bias[t]);   // log g
         pbeta[i] = sigmoid(b[i]);
     }
-}
-
-// grid (8 row blocks, 32 value heads), 256 threads: 4 waves x 4 rows.
-__global__ __launch_bounds__(256) void dn_prefill_recurrent_kernel(
-    int T, const float* __restrict__ pq, const float* __restrict__ pk, const float* __restrict__ pv,
-    const float* __restrict__ pg, const float* __restrict__ pbeta, float* __restrict__ ssm_state,
-    float* __restrict__ po) {
-    const int rb = blockIdx.x, h = blockIdx.y, kh = h >> 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int col4 = lane & 31;
-    const int r0 = rb * 16 + wave * 4 + (lane >> 5);  // rows r0 and r0 + 2
-    float4* S = reinterpret_cast<float4*>(ssm_state) + static_cast<size_t>(h) * (128 * 32);
-    float4 s0 = S[r0 * 32 + col4];
-    float4 s1 = S[(r0 + 2) * 32 + col4];
-    const float4* q4p = reinterpret_cast<const float4*>(pq) + kh * 32 + col4;
-    const float4* k4p = reinterpret_cast<const float4*>(pk) + kh * 32 + col4;
-    float4 qn = q4p[0], kn = k4p[0];
-    float vn0 = pv[h * 128 + r0], vn1 = pv[h * 128 + r0 + 2];
-    float gn = pg[h], bn = pbeta[h];
-    for (int tok = 0; tok < T; ++tok) {
-        const float4 q4 = qn, k4 = kn;
-        const float v0 = vn0, v1 = vn1, g = gn, beta = bn;
-        if (tok + 1 < T) {
-            const size_t nx = static_cast<size_t>(tok + 1);
-            qn = q4p[nx * 512];
-            kn = k4p[nx * 512];
-            vn0 = pv[nx * 4096 + h * 128 + r0];
-            vn1 = pv[nx * 4096 + h * 128 + r0 + 2];
-            gn = pg[nx * 32 + h];
-            bn = pbeta[nx * 32 + h];
-        }
-        s0.x *= g; s0.y *= g; s0.z *= g; s0.w *= g;
-        s1.x *= g; s1.y *= g; s1.z *= g; s1.w *= g;
-        const float kv0 = group_sum<32>(dot4(s0, k4));
-        const float kv1 = group_sum<32>(dot4(s1, k4));
-        const float d0 = (v0 - kv0) * beta, d1 = (v1 - kv1) * beta;
-        s0.x = fmaf(k4.x, d0, s0.x); s0.y = fmaf(k4.y, d0, s0.y);
-        s0.z = fmaf(k4.z, d0, s0.z); s0.w = fmaf(k4.w, d0, s0.w);
-        s1.x = fmaf(k4.x, d1, s1.x); s1.y = fmaf(k4.y, d1, s1.y);
-        s1.z = fmaf(k4.z, d1, s1.z); s1.w = fmaf(k4.w, d1, s1.w);
-        const float o0 = group_sum<32>(dot4(s0, q4));
-        const float o1 = group_sum<32>(dot4(s1, q4));
-        if (col4 == 0) {
-            float* orow = po + static_cast<size_t>(tok) * 4096 + h * 128;
-            orow[r0] = o0;
-            orow[r0 + 2] = o1;
-        }
-    }
-    S[r0 * 32 + col4] = s0;
-    S[(r0 + 2) * 32 + col4] = s1;
 }
 
 // grid (T, 16), 256 threads: value heads 2*blockIdx.y (waves 0-1) and +1.
@@ -158,9 +106,8 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
                                                                   ctx->pf_g, ctx->pf_beta);
     }
     {
-    ProfScope prof(ctx, stream, "dn_prefill_recurrent");
-    dn_prefill_recurrent_kernel<<<dim3(8, 32), 256, 0, stream>>>(T, ctx->pf_q, ctx->pf_k, ctx->pf_v, ctx->pf_g,
-                                                                 ctx->pf_beta, ssm_state, ctx->pf_o);
+        hipError_t e = launch_deltanet_chunked(ctx, stream, T, ssm_state);
+        if (e != hipSuccess) return e;
     }
     const dim3 ng(T, 16);
     {

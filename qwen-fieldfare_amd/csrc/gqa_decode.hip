@@ -7,19 +7,18 @@
 // attention.metal:134-224, 342-377; geometry Attention.swift:129-157) and the
 // gate (deltanet.metal:700-708), one q head per threadgroup.
 //
-// Here the eight q heads that share a kv head run in the same workgroup, so
-// every K/V byte is read from HBM once, and both products run on the matrix
-// cores:
-//   partial  grid (chunk, kv head, sequence), 4 waves. Each workgroup
+// Here the eight q heads that share a kv head run in the same wave, so every
+// K/V byte is read from HBM once, and both products run on the matrix cores:
+//   partial  grid (chunk, kv head, sequence), one wave each. The wave
 //            normalises and rotates its 8 q heads into LDS (bf16, softmax
-//            scale folded in); the workgroup whose chunk holds the new token
-//            also normalises/rotates k, appends k and v to the cache and
-//            fences them before the chunk is read. Each wave then walks
-//            16-position tiles: S^T = K Q^T with 8 MFMA 16x16x32 (K rows
-//            straight from HBM, 16 B per lane), online softmax per head in
-//            registers, V transposed through a per-wave LDS tile, and
-//            O += P V with 16 MFMA 16x16x16. The 4 waves merge in LDS and the
-//            workgroup writes one (m, d, o[8][256]) partial.
+//            scale folded in); the wave whose chunk holds the new token also
+//            normalises/rotates k, appends k and v to the cache and keeps both
+//            in LDS for its own use. It then walks 16-position tiles:
+//            S^T = K Q^T with 8 MFMA 16x16x32 (K rows straight from HBM, 16 B
+//            per lane), online softmax per head in registers, the V tile
+//            copied row-major into LDS and read back as MFMA B operands with
+//            the gfx950 transpose read (ds_read_b64_tr_b16), O += P V with 16
+//            MFMA 16x16x16, and one (m, d, o[8][256]) partial per chunk.
 //   combine  grid (q head, sequence): merges the chunk partials and applies
 //            out = attn * sigmoid(gate).
 // Lengths come from the device `positions` array, so no host sync is needed;
@@ -30,17 +29,19 @@
 
 namespace qff {
 
-constexpr int kVtStride = 20;  // bf16 per transposed V row: 16 positions + pad
+constexpr int kDecTile = 16;          // positions per MFMA tile
+constexpr int kVRowStride = 264;      // bf16 per V row in LDS: 256 + 8 pad (528 B)
 
+// One wave per (chunk, kv head, sequence).
 template <int IN_DT>
-__global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
+__global__ __launch_bounds__(64, 3) void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
     const int32_t* __restrict__ positions, int max_ctx, int chunk_len, float* __restrict__ pm,
     float* __restrict__ pd, float* __restrict__ po) {
     const int c = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lane = threadIdx.x;
     const int pos = positions[seq];
     // a position outside the cache is the caller's error: skip the sequence
     // (the combine writes NaN for it) rather than touch memory past the cache
@@ -50,122 +51,138 @@ __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
     const int p_start = c * chunk_len;
     const int p_end = min(L, p_start + chunk_len);
 
-    __shared__ float qf[8][256];
-    __shared__ __attribute__((aligned(16))) uint16_t qb[8][256];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[4][256 * kVtStride];
-    __shared__ float rcos[32], rsin[32], kf[256], red[4];
-    __shared__ float wm[4][8], wd[4][8];
+    __shared__ __attribute__((aligned(16))) uint16_t qs[8][256];               // 4 KB
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kDecTile * kVRowStride];  // 8.25 KB
+    __shared__ __attribute__((aligned(16))) uint16_t knew[256], vnew[256];
 
-    // RoPE table for this position: QwenQ4ActiveExpertStreamingRunner.swift:1090-1099
-    // (the inverse frequencies come from the host, computed there in fp32)
-    if (t < 32) {
-        const float ang = static_cast<float>(pos) * rf.f[t];
-        rcos[t] = cosf(ang);
-        rsin[t] = sinf(ang);
-    }
-    // head RMSNorm of the 8 q heads: thread -> head t/32, dims 8*(t%32)..+7
-    // (deltanet.metal:599-632)
+    // ---- q: head RMSNorm + partial RoPE + scale, bf16 into LDS ---------------
+    // (deltanet.metal:599-651; RoPE angles as QwenQ4ActiveExpertStreamingRunner
+    // .swift:1090-1099 with host-computed inverse frequencies). Lane -> head
+    // lane/8, dims 8*(lane%8) + 64*pass .. +7 over 4 passes; the RoPE pair
+    // (i, i+32) of pass 0 sits in lanes 8h+jj and 8h+jj+4.
     {
-        const int hl = t >> 5, j = t & 31;
+        const int hl = lane >> 3, j = lane & 7;
         const size_t qbase = (static_cast<size_t>(seq) * 16 + kvh * 8 + hl) * 512 + 8 * j;
-        float x[8], ss = 0.0f;
+        float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[i] = elem<IN_DT>::load(q_gate, qbase + i);
-            ss += x[i] * x[i];
-        }
-        ss = group_sum<32>(ss);
+        for (int ps = 0; ps < 4; ++ps)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = elem<IN_DT>::load(q_gate, qbase + 64 * ps + i);
+                ss += x * x;
+            }
+        ss = group_sum<8>(ss);
         const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[hl][8 * j + i] = x[i] * inv * q_norm_w[8 * j + i];
-    }
-    __syncthreads();
-    // partial RoPE (deltanet.metal:634-651), softmax scale, bf16
-    {
-        const int hl = t >> 5, j = t & 31;
+        for (int ps = 0; ps < 4; ++ps) {
+            float x[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int d = 8 * j + i;
-            float v = qf[hl][d];
-            if (d < 32) v = v * rcos[d] + (-qf[hl][d + 32]) * rsin[d];
-            else if (d < 64) v = v * rcos[d - 32] + qf[hl][d - 32] * rsin[d - 32];
-            qb[hl][d] = f32_to_bf16(v * scale);
+            for (int i = 0; i < 8; ++i) {
+                const int d = 64 * ps + 8 * j + i;
+                x[i] = elem<IN_DT>::load(q_gate, qbase + 64 * ps + i) * inv * q_norm_w[d];
+            }
+            if (ps == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int d = 8 * j + i;                          // 0..63
+                    const float partner = __shfl_xor(x[i], 4, 64);    // d +- 32
+                    const float ang = static_cast<float>(pos) * rf.f[d & 31];
+                    const float cs = cosf(ang), sn = sinf(ang);
+                    x[i] = (d < 32) ? x[i] * cs + (-partner) * sn : x[i] * cs + partner * sn;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i += 2)
+                *reinterpret_cast<uint32_t*>(&qs[hl][64 * ps + 8 * j + i]) = pack_bf16x2(x[i] * scale, x[i + 1] * scale);
         }
     }
+    // ---- the new token (only the chunk that holds it): k norm + RoPE, append
+    // k and v to the cache (deltanet.metal:670-689), keep both in LDS so this
+    // wave never reads back its own global stores.
+    const bool has_new = pos >= p_start && pos < p_end;
     const size_t seq_base = static_cast<size_t>(seq) * max_ctx * 512 + kvh * 256;
-    // the new token: k norm + RoPE, append k and v (deltanet.metal:670-689)
-    if (pos >= p_start && pos < p_end) {
-        const size_t kb0 = (static_cast<size_t>(seq) * 2 + kvh) * 256;
-        const float kx = elem<IN_DT>::load(k_new, kb0 + t);
-        const float kss = group_sum<64>(kx * kx);
-        if (lane == 0) red[wave] = kss;
-        __syncthreads();
-        const float kinv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / 256.0f + eps);
-        kf[t] = kx * kinv * k_norm_w[t];
-        __syncthreads();
-        float kr = kf[t];
-        if (t < 32) kr = kr * rcos[t] + (-kf[t + 32]) * rsin[t];
-        else if (t < 64) kr = kr * rcos[t - 32] + kf[t - 32] * rsin[t - 32];
-        const size_t off = seq_base + static_cast<size_t>(pos) * 512 + t;
-        k_cache[off] = f32_to_bf16(kr);
-        v_cache[off] = f32_to_bf16(elem<IN_DT>::load(v_new, kb0 + t));
-        __threadfence();
+    if (has_new) {
+        const size_t kb0 = (static_cast<size_t>(seq) * 2 + kvh) * 256 + 4 * lane;
+        float kx[4], vx[4], ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            kx[i] = elem<IN_DT>::load(k_new, kb0 + i);
+            vx[i] = elem<IN_DT>::load(v_new, kb0 + i);
+            ss += kx[i] * kx[i];
+        }
+        ss = group_sum<64>(ss);
+        const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kx[i] = kx[i] * inv * k_norm_w[4 * lane + i];
+        // dims 4*lane .. +3; RoPE partner of dim d < 32 is d + 32 = lane + 8
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float up = __shfl_down(kx[i], 8, 64), dn = __shfl_up(kx[i], 8, 64);
+            const int d = 4 * lane + i;
+            if (d < 64) {
+                const float ang = static_cast<float>(pos) * rf.f[d & 31];
+                const float cs = cosf(ang), sn = sinf(ang);
+                kx[i] = (d < 32) ? kx[i] * cs + (-up) * sn : kx[i] * cs + dn * sn;
+            }
+        }
+        const uint32_t k01 = pack_bf16x2(kx[0], kx[1]), k23 = pack_bf16x2(kx[2], kx[3]);
+        const uint32_t v01 = pack_bf16x2(vx[0], vx[1]), v23 = pack_bf16x2(vx[2], vx[3]);
+        *reinterpret_cast<u32x2_t*>(&knew[4 * lane]) = u32x2_t{k01, k23};
+        *reinterpret_cast<u32x2_t*>(&vnew[4 * lane]) = u32x2_t{v01, v23};
+        const size_t off = seq_base + static_cast<size_t>(pos) * 512 + 4 * lane;
+        *reinterpret_cast<u32x2_t*>(k_cache + off) = u32x2_t{k01, k23};
+        *reinterpret_cast<u32x2_t*>(v_cache + off) = u32x2_t{v01, v23};
     }
     __syncthreads();
 
-    // q^T operands (B of 16x16x32): col = head n (< 8 real), k = dims
     const int n = lane & 15, kb = lane >> 4;
-    u32x4_t qreg[8];
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        if (n < 8) qreg[jj] = *reinterpret_cast<const u32x4_t*>(&qb[n][32 * jj + 8 * kb]);
-        else qreg[jj] = u32x4_t{0u, 0u, 0u, 0u};
-    }
+    // q^T (B of 16x16x32): col = head n (< 8 real), k = dims 32jj + 8kb .. +7,
+    // read from LDS per tile (registers are kept for occupancy)
+    const uint16_t* qrow = &qs[n & 7][8 * kb];
 
     float m_run = -INFINITY, d_run = 0.0f;
     f32x4_t oacc[16];
 #pragma unroll
     for (int jd = 0; jd < 16; ++jd) oacc[jd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    uint16_t* vtw = vt[wave];
     const uint16_t* Kb = k_cache + seq_base;
     const uint16_t* Vb = v_cache + seq_base;
 
-    // K operand rows (A of 16x16x32: position p0 + n, dims 32jj + 8kb .. +7)
-    // and V rows (positions p0 + 4kb + i, dims 8(n + 16it) .. +7) of one tile.
-    // K rows past the chunk end re-read its last row (masked below) and V
-    // rows past it read as zero (their probability is 0, and the cache
-    // beyond the sequence may hold any bit pattern, NaN included), so no
-    // lane reads outside the chunk.
-    auto load_tile = [&](int p0, u32x4_t (&ka)[8], u32x4_t (&va)[2][4]) {
-        const uint16_t* krow = Kb + static_cast<size_t>(min(p0 + n, p_end - 1)) * 512;
+    for (int p0 = p_start; p0 < p_end; p0 += kDecTile) {
+        // K rows p0 + n (A of 16x16x32) and V rows p0 + 2i + lane/32 (dims
+        // 8*(lane%32) .. +7). Rows past the chunk end re-read its last row:
+        // their scores are masked to -inf, so they enter P V with probability
+        // 0 times finite data (the cache past the sequence may hold any bit
+        // pattern, NaN included, and is never read).
+        u32x4_t ka[8], vr[8];
+        const int kp = min(p0 + n, p_end - 1);
+        const uint16_t* krow = Kb + static_cast<size_t>(kp) * 512;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) ka[jj] = *reinterpret_cast<const u32x4_t*>(krow + 32 * jj + 8 * kb);
 #pragma unroll
-        for (int it = 0; it < 2; ++it)
+        for (int i = 0; i < 8; ++i) {
+            const int vp = min(p0 + 2 * i + (lane >> 5), p_end - 1);
+            vr[i] = *reinterpret_cast<const u32x4_t*>(Vb + static_cast<size_t>(vp) * 512 + 8 * (lane & 31));
+        }
+        if (has_new && kp == pos) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int pp = p0 + 4 * kb + i;
-                va[it][i] = pp < p_end
-                    ? *reinterpret_cast<const u32x4_t*>(Vb + static_cast<size_t>(pp) * 512 + 8 * (n + 16 * it))
-                    : u32x4_t{0u, 0u, 0u, 0u};
-            }
-    };
-    u32x4_t kn[8], vn[2][4];
-    if (p_start + wave * 16 < p_end) load_tile(p_start + wave * 16, kn, vn);
-    for (int p0 = p_start + wave * 16; p0 < p_end; p0 += 64) {
-        u32x4_t kcur[8], vr[2][4];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) kcur[jj] = kn[jj];
-#pragma unroll
-        for (int it = 0; it < 2; ++it)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vr[it][i] = vn[it][i];
-        if (p0 + 64 < p_end) load_tile(p0 + 64, kn, vn);   // next tile in flight
+            for (int jj = 0; jj < 8; ++jj) ka[jj] = *reinterpret_cast<const u32x4_t*>(&knew[32 * jj + 8 * kb]);
+        }
         // S^T = K Q^T
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) s = mfma_16x16x32_bf16(kcur[jj], qreg[jj], s);
-        // online softmax: lane holds head n, positions p0 + 4kb + i
+        for (int jj = 0; jj < 8; ++jj) {
+            const u32x4_t qv = n < 8 ? *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj) : u32x4_t{0u, 0u, 0u, 0u};
+            s = mfma_16x16x32_bf16(ka[jj], qv, s);
+        }
+        // V tile row-major into LDS (the new token's row from LDS as well)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 2 * i + (lane >> 5);
+            u32x4_t v = vr[i];
+            if (has_new && p0 + r == pos) v = *reinterpret_cast<const u32x4_t*>(&vnew[8 * (lane & 31)]);
+            *reinterpret_cast<u32x4_t*>(&vs[r * kVRowStride + 8 * (lane & 31)]) = v;
+        }
+        // online softmax; lane holds head n, positions p0 + 4kb + i
         float sv[4], tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -193,92 +210,53 @@ __global__ __launch_bounds__(256) void gqa_decode_partial_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) oacc[jd][i] *= al[i];
         }
+        // A of O += P V (16x16x16): row = head n, k = positions 4kb .. +3
         const u32x2_t pa = u32x2_t{pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])};
-        // transpose V (4 positions x 8 dims per lane) into vt[dim][position]
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int dg = n + 16 * it;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int w = e >> 1;
-                uint32_t lo, hi;
-                if (e & 1) {
-                    lo = (vr[it][0][w] >> 16) | (vr[it][1][w] & 0xffff0000u);
-                    hi = (vr[it][2][w] >> 16) | (vr[it][3][w] & 0xffff0000u);
-                } else {
-                    lo = (vr[it][0][w] & 0xffffu) | (vr[it][1][w] << 16);
-                    hi = (vr[it][2][w] & 0xffffu) | (vr[it][3][w] << 16);
-                }
-                *reinterpret_cast<u32x2_t*>(&vtw[(8 * dg + e) * kVtStride + 4 * kb]) = u32x2_t{lo, hi};
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        // B = V^T block straight from the row-major tile with a transpose read:
+        // source lane (group kb, s = n) points at row 4kb + n/4, dims
+        // 16jd + 4(n%4) .. +3, and receives V[4kb + k][16jd + n], k = 0..3.
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O += P V: A = P (head n, positions 4kb..), B = V^T tile (dim 16jd + n)
+        const uint16_t* vsrc = &vs[(4 * kb + (n >> 2)) * kVRowStride + 4 * (n & 3)];
 #pragma unroll
-        for (int jd = 0; jd < 16; ++jd) {
-            const u32x2_t vb = *reinterpret_cast<const u32x2_t*>(&vtw[(16 * jd + n) * kVtStride + 4 * kb]);
-            oacc[jd] = mfma_16x16x16_bf16(pa, vb, oacc[jd]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        for (int jd = 0; jd < 16; ++jd) oacc[jd] = mfma_16x16x16_bf16(pa, lds_read_tr16(vsrc + 16 * jd), oacc[jd]);
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    // ---- partial (m, d, o) of this chunk; oacc[jd][i] = O[head 4kb+i][dim 16jd+n]
     d_run += __shfl_xor(d_run, 16, 64);
     d_run += __shfl_xor(d_run, 32, 64);
+    const size_t pbase = (static_cast<size_t>(seq) * 2 + kvh) * kGqaMaxChunks + c;
     if (lane < 8) {
-        wm[wave][lane] = m_run;
-        wd[wave][lane] = d_run;
+        pm[pbase * 8 + lane] = m_run;
+        pd[pbase * 8 + lane] = d_run;
     }
-    __syncthreads();
-    // merge the 4 waves (the vt tiles are free now): om[wave][head][dim]
-    float* om = reinterpret_cast<float*>(&vt[0][0]);
     if (kb < 2) {
+        float* orow = po + pbase * 8 * 256;
 #pragma unroll
         for (int jd = 0; jd < 16; ++jd)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) om[(wave * 8 + 4 * kb + i) * 256 + 16 * jd + n] = oacc[jd][i];
-    }
-    __syncthreads();
-    const size_t pbase = (static_cast<size_t>(seq) * 2 + kvh) * kGqaMaxChunks + c;
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][h]);
-        float D = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float e = expf(wm[w][h] - M);
-            D += wd[w][h] * e;
-            O += om[(w * 8 + h) * 256 + t] * e;
-        }
-        po[(pbase * 8 + h) * 256 + t] = O;
-        if (t == 0) {
-            pm[pbase * 8 + h] = M;
-            pd[pbase * 8 + h] = D;
-        }
+            for (int i = 0; i < 4; ++i) orow[(4 * kb + i) * 256 + 16 * jd + n] = oacc[jd][i];
     }
 }
 
-// grid (16 q heads, batch), 256 threads: attention.metal:342-377 merge, then
-// the gate of deltanet.metal:700-708. Chunk weights are formed in parallel
-// (one thread per chunk) and the dim loop issues 8 independent loads at a
-// time.
+// grid (16 q heads, batch), 512 threads: attention.metal:342-377 merge, then
+// the gate of deltanet.metal:700-708. Chunk weights are formed one thread per
+// chunk; then wave w sums chunks w, w+8, ... for all 256 dims (a float4 per
+// lane) so each lane has few dependent loads in flight, and the 8 wave sums
+// are added in LDS in a fixed order.
 template <int IN_DT, int OUT_DT>
-__global__ __launch_bounds__(256) void gqa_decode_combine_kernel(
+__global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int max_ctx, int chunk_len,
     const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
-    __shared__ float es[kGqaMaxChunks], red[8];
+    __shared__ float es[kGqaMaxChunks], red[16];
+    __shared__ __attribute__((aligned(16))) float osum[8][256];
     const int h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int kvh = h >> 3, hl = h & 7;
     const size_t qi = (static_cast<size_t>(seq) * 16 + h);
     const int pos = positions[seq];
     if (pos < 0 || pos >= max_ctx) {
-        elem<OUT_DT>::store(out, qi * 256 + t, __builtin_nanf(""));
+        if (t < 256) elem<OUT_DT>::store(out, qi * 256 + t, __builtin_nanf(""));
         return;
     }
     const int L = pos + 1;
@@ -289,32 +267,51 @@ __global__ __launch_bounds__(256) void gqa_decode_combine_kernel(
     const float wmax = group_max<64>(m);
     if (lane == 0) red[wave] = wmax;
     __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) M = fmaxf(M, red[w]);
     const float e = t < nc ? expf(m - M) : 0.0f;
     if (t < kGqaMaxChunks) es[t] = e;
     const float wd = group_sum<64>(d * e);
-    if (lane == 0) red[4 + wave] = wd;
+    if (lane == 0) red[8 + wave] = wd;
     __syncthreads();
-    const float D = red[4] + red[5] + red[6] + red[7];
-    const float* pr = po + (base * 8 + hl) * 256 + t;   // chunk c at pr[c * 8 * 256]
-    float O = 0.0f;
-    int c = 0;
-    for (; c + 8 <= nc; c += 8) {
-        float v[8];
+    const float4* pr = reinterpret_cast<const float4*>(po + (base * 8 + hl) * 256) + lane;  // chunk c at pr[c*512]
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int c = wave;
+    for (; c + 24 < nc; c += 32) {
+        float4 v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = pr[static_cast<size_t>(c + u) * 2048];
+        for (int u = 0; u < 4; ++u) v[u] = pr[static_cast<size_t>(c + 8 * u) * 512];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) O += v[u] * es[c + u];
+        for (int u = 0; u < 4; ++u) {
+            const float w = es[c + 8 * u];
+            acc.x += v[u].x * w; acc.y += v[u].y * w; acc.z += v[u].z * w; acc.w += v[u].w * w;
+        }
     }
-    for (; c < nc; ++c) O += pr[static_cast<size_t>(c) * 2048] * es[c];
-    const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + t);
-    elem<OUT_DT>::store(out, qi * 256 + t, (O / D) * sigmoid(gate));
+    for (; c < nc; c += 8) {
+        const float4 v = pr[static_cast<size_t>(c) * 512];
+        const float w = es[c];
+        acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
+    }
+    reinterpret_cast<float4*>(osum[wave])[lane] = acc;
+    __syncthreads();
+    if (t < 256) {
+        float D = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            D += red[8 + w];
+            O += osum[w][t];
+        }
+        const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + t);
+        elem<OUT_DT>::store(out, qi * 256 + t, (O / D) * sigmoid(gate));
+    }
 }
 
-// Chunk length: aim for ~2048 partial workgroups over the batch (8 per CU),
-// at most kGqaMaxChunks chunks per sequence, multiples of 64 positions.
+// Chunk length: aim for ~4096 one-wave partial workgroups over the batch
+// (16 per CU), at most kGqaMaxChunks chunks per sequence, multiples of 64
+// positions (4 MFMA tiles).
 int gqa_chunk_len(int max_ctx, int batch) {
-    int target = 2048 / (2 * batch);
+    int target = 4096 / (2 * batch);
     if (target < 1) target = 1;
     if (target > kGqaMaxChunks) target = kGqaMaxChunks;
     const int per = (max_ctx + target - 1) / target;
@@ -336,18 +333,18 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
     {
     ProfScope prof(ctx, stream, "gqa_decode_partial");
     if (in_dtype == QFF_BF16)
-        gqa_decode_partial_kernel<1><<<pgrid, 256, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
+        gqa_decode_partial_kernel<1><<<pgrid, 64, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
                                                                 rf, p->scale, p->eps, kc, vc, positions,
                                                                 max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o);
     else
-        gqa_decode_partial_kernel<0><<<pgrid, 256, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
+        gqa_decode_partial_kernel<0><<<pgrid, 64, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w,
                                                                 rf, p->scale, p->eps, kc, vc, positions,
                                                                 max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o);
     }
     const dim3 cgrid(16, batch);
     ProfScope prof(ctx, stream, "gqa_decode_combine");
 #define QFF_COMB(I, O) \
-    gqa_decode_combine_kernel<I, O><<<cgrid, 256, 0, stream>>>(q_gate, positions, max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
+    gqa_decode_combine_kernel<I, O><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
     if (in_dtype == QFF_BF16) {
         if (out_dtype == QFF_BF16) QFF_COMB(1, 1); else QFF_COMB(1, 0);
     } else {

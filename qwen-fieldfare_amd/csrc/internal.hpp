@@ -32,6 +32,15 @@ struct qff_ctx {
     float* pf_g = nullptr;        // [T * 32] log gate
     float* pf_beta = nullptr;     // [T * 32]
     float* pf_o = nullptr;        // [T * 32 * 128] pre-norm output
+    // Chunked DeltaNet prefill: per (chunk, value head) W, U~ [64][128] and
+    // P [64][64] as bf16 hi/lo pairs, and the cumulative log gates G [64].
+    uint16_t* pf_wh = nullptr;
+    uint16_t* pf_wl = nullptr;
+    uint16_t* pf_uh = nullptr;
+    uint16_t* pf_ul = nullptr;
+    uint16_t* pf_ph = nullptr;
+    uint16_t* pf_pl = nullptr;
+    float* pf_G = nullptr;
     // Kernel timing (qff_profile_enable): a pool of event pairs.
     bool prof = false;
     std::vector<qff_prof_record> prof_pool;
@@ -44,7 +53,7 @@ constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o;
+    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o, pf_wh, pf_wl, pf_uh, pf_ul, pf_ph, pf_pl, pf_G;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
@@ -90,6 +99,7 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
                                    const void* qkv, const void* z, qff_dtype in_dtype,
                                    const float* a, const float* b, float* conv_state,
                                    float* ssm_state, void* out, qff_dtype out_dtype, int T);
+hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, int T, float* ssm_state);
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
                              const void* q_gate, const void* k_new, const void* v_new,
                              qff_dtype in_dtype, void* k_cache, void* v_cache,

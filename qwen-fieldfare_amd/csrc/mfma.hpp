@@ -30,12 +30,98 @@ __device__ __forceinline__ f32x4_t mfma_16x16x16_bf16(u32x2_t a, u32x2_t b, f32x
                                                      __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
 }
 
+// LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each group of 16
+// lanes, lane s reads 4 consecutive 16-bit elements D[s][0..3] at its own
+// address; lane i receives R[i][k] = D[4k + i/4][i % 4], k = 0..3. With a
+// row-major [position][dim] tile in LDS, source lane s of group g pointing at
+// row 4g + s/4, dims d0 + 4(s%4) .. +3 yields R[i][k] = tile[4g + k][d0 + i]:
+// the B operand of a 16x16x16 MFMA whose k runs over positions.
+__device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
+    typedef short s16x4_lds __attribute__((ext_vector_type(4)));
+    const s16x4_lds v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s16x4_lds __attribute__((address_space(3)))*)(p));
+    return __builtin_bit_cast(u32x2_t, v);
+}
+
+// fp32 -> (hi, lo) bf16 pair with hi + lo == x to ~2^-16 relative: the
+// operands of the three-product "bf16x3" MFMA scheme
+//   a b ~= a_hi b_hi + a_hi b_lo + a_lo b_hi
+// which keeps fp32-class accuracy (~2^-16 relative per product) on the
+// bf16 matrix cores. Inputs are finite.
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    uint32_t u = __float_as_uint(x);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    hi = static_cast<uint16_t>(u >> 16);
+    const float r = x - __uint_as_float(static_cast<uint32_t>(hi) << 16);
+    uint32_t v = __float_as_uint(r);
+    v += 0x7fffu + ((v >> 16) & 1u);
+    lo = static_cast<uint16_t>(v >> 16);
+}
+
 // Two floats -> packed bf16 pair (round to nearest even), low half = lo.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     uint32_t a = __float_as_uint(lo), b = __float_as_uint(hi);
     a += 0x7fffu + ((a >> 16) & 1u);
     b += 0x7fffu + ((b >> 16) & 1u);
     return (a >> 16) | (b & 0xffff0000u);
+}
+
+}  // namespace qff
+
+namespace qff {
+
+// 16x16 output tile, C += A B, bf16x3 on 16x16x32 MFMAs. A is row-major
+// [16 rows][K] (hi/lo arrays, row stride lda elements, K contiguous).
+// "NT": B is given as its transpose, row-major [16 cols][K] (stride ldb).
+// "NN": B is row-major [K][16 cols] (stride ldb) and is read with the LDS
+// transpose read, two per MFMA (k = 8kb .. 8kb+3 and 8kb+4 .. 8kb+7).
+// All pointers are LDS addresses of the tile's first element; strides keep
+// 16-byte (NT) / 8-byte (NN) alignment.
+template <int K>
+__device__ __forceinline__ f32x4_t mma_nt_x3(f32x4_t acc, const uint16_t* ah, const uint16_t* al, int lda,
+                                             const uint16_t* bh, const uint16_t* bl, int ldb, int lane) {
+    const int n = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        const int ao = n * lda + k0 + 8 * kb, bo = n * ldb + k0 + 8 * kb;
+        const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(ah + ao);
+        const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(al + ao);
+        const u32x4_t b_h = *reinterpret_cast<const u32x4_t*>(bh + bo);
+        const u32x4_t b_l = *reinterpret_cast<const u32x4_t*>(bl + bo);
+        acc = mfma_16x16x32_bf16(a_l, b_h, acc);
+        acc = mfma_16x16x32_bf16(a_h, b_l, acc);
+        acc = mfma_16x16x32_bf16(a_h, b_h, acc);
+    }
+    return acc;
+}
+
+template <int K>
+__device__ __forceinline__ f32x4_t mma_nn_x3(f32x4_t acc, const uint16_t* ah, const uint16_t* al, int lda,
+                                             const uint16_t* bh, const uint16_t* bl, int ldb, int lane) {
+    const int n = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        const int ao = n * lda + k0 + 8 * kb;
+        const int bo = (k0 + 8 * kb + (n >> 2)) * ldb + 4 * (n & 3);
+        const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(ah + ao);
+        const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(al + ao);
+        const u32x2_t h0 = lds_read_tr16(bh + bo), h1 = lds_read_tr16(bh + bo + 4 * ldb);
+        const u32x2_t l0 = lds_read_tr16(bl + bo), l1 = lds_read_tr16(bl + bo + 4 * ldb);
+        const u32x4_t b_h = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+        const u32x4_t b_l = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+        acc = mfma_16x16x32_bf16(a_l, b_h, acc);
+        acc = mfma_16x16x32_bf16(a_h, b_l, acc);
+        acc = mfma_16x16x32_bf16(a_h, b_h, acc);
+    }
+    return acc;
+}
+
+// Store 4 fp32 values as hi/lo bf16 at hi[i..i+3], lo[i..i+3] (8-byte aligned).
+__device__ __forceinline__ void store_split4(uint16_t* hi, uint16_t* lo, int i, float a, float b, float c, float d) {
+    uint16_t h0, h1, h2, h3, l0, l1, l2, l3;
+    split_bf16(a, h0, l0); split_bf16(b, h1, l1); split_bf16(c, h2, l2); split_bf16(d, h3, l3);
+    *reinterpret_cast<u32x2_t*>(hi + i) = u32x2_t{h0 | (static_cast<uint32_t>(h1) << 16), h2 | (static_cast<uint32_t>(h3) << 16)};
+    *reinterpret_cast<u32x2_t*>(lo + i) = u32x2_t{l0 | (static_cast<uint32_t>(l1) << 16), l2 | (static_cast<uint32_t>(l3) << 16)};
 }
 
 }  // namespace qff
