@@ -44,6 +44,10 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.pf_ul = take(TC * 32 * 128 * sizeof(uint16_t));
     L.pf_ph = take(TC * 32 * 64 * sizeof(uint16_t));
     L.pf_pl = take(TC * 32 * 64 * sizeof(uint16_t));
+    L.pf_qth = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_qtl = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_kth = take(TC * 32 * 128 * sizeof(uint16_t));
+    L.pf_ktl = take(TC * 32 * 128 * sizeof(uint16_t));
     L.pf_G = take(TC * 32 * sizeof(float));
     L.total = off;
     return L;
@@ -162,6 +166,10 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->pf_ul = reinterpret_cast<uint16_t*>(base + L.pf_ul);
     c->pf_ph = reinterpret_cast<uint16_t*>(base + L.pf_ph);
     c->pf_pl = reinterpret_cast<uint16_t*>(base + L.pf_pl);
+    c->pf_qth = reinterpret_cast<uint16_t*>(base + L.pf_qth);
+    c->pf_qtl = reinterpret_cast<uint16_t*>(base + L.pf_qtl);
+    c->pf_kth = reinterpret_cast<uint16_t*>(base + L.pf_kth);
+    c->pf_ktl = reinterpret_cast<uint16_t*>(base + L.pf_ktl);
     c->pf_G = reinterpret_cast<float*>(base + L.pf_G);
     (void)hipSetDevice(prev);
     *out = c;

@@ -17,9 +17,11 @@
 //
 // Two kernels:
 //   dn_chunk_local_kernel  one workgroup per (chunk, value head), all chunks
-//       at once: A from K K^T, P = e^{G_i-G_j}[j<=i] Q K^T, T by forward
-//       substitution (one wave, fp32), then W and U~; W, U~, P and G go to
-//       workspace.
+//       at once: A from K K^T, P = e^{G_i-G_j}[j<=i] Q K^T, T = (I + A)^-1
+//       in 16x16 blocks (diagonal blocks by substitution, the rest on fp32
+//       MFMAs, four waves in parallel), then W and U~; W, U~, P, the scaled
+//       Q~ = e^G Q and K~ = e^{G_C - G} K (all split into bf16 hi/lo) and G
+//       go to workspace.
 //   dn_chunk_state_kernel  one workgroup per (32-row block of the state,
 //       value head) walks the chunks in order with its state slice in
 //       registers: U = U~ - W S^T, O = Q~ S^T + P U, S = e^{G_C} S + U^T K~.
@@ -42,7 +44,8 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
     int T, const float* __restrict__ pq, const float* __restrict__ pk, const float* __restrict__ pv,
     const float* __restrict__ plg, const float* __restrict__ pbeta, uint16_t* __restrict__ wh,
     uint16_t* __restrict__ wl, uint16_t* __restrict__ uh, uint16_t* __restrict__ ul, uint16_t* __restrict__ ph,
-    uint16_t* __restrict__ pl, float* __restrict__ gout) {
+    uint16_t* __restrict__ pl, float* __restrict__ gout, uint16_t* __restrict__ qth, uint16_t* __restrict__ qtl,
+    uint16_t* __restrict__ kth, uint16_t* __restrict__ ktl) {
     const int c = blockIdx.x, h = blockIdx.y, kh = h >> 1;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
@@ -115,34 +118,70 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
-    if (wave == 0) {
-        // T = (I + A)^-1, lower unitriangular, by forward substitution:
-        // lane = column c, T[i][c] = [i == c] - sum_{j<i} A[i][j] T[j][c]
-        float Tc[kC];
+    // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
+    //   diagonal blocks by forward substitution, one wave each;
+    //   T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i > j, wave j walking
+    //   column block j downwards (fp32 MFMA 16x16x4).
+    float* Tm = reinterpret_cast<float*>(Qh);          // [64][65] fp32 (Q is consumed)
+    float* scr = reinterpret_cast<float*>(Ql) + wave * (16 * 17);
+    {
+        const int bi = wave;
+        if (lane < 16) {
+            float tc[16];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            float acc = 0.0f;
+            for (int i = 0; i < 16; ++i) {
+                float acc = 0.0f;
 #pragma unroll
-            for (int jj = 0; jj < i; ++jj) acc = fmaf(Am[i * 65 + jj], Tc[jj], acc);
-            Tc[i] = (i == lane ? 1.0f : 0.0f) - acc;
+                for (int j = 0; j < i; ++j) acc = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], acc);
+                tc[i] = (i == lane ? 1.0f : 0.0f) - acc;
+                Tm[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
+            }
         }
+        // blocks right of the diagonal are zero
+        for (int idx = lane; idx < 16 * (48 - 16 * bi); idx += 64) {
+            const int i = idx / (48 - 16 * bi), j = 16 * (bi + 1) + idx % (48 - 16 * bi);
+            Tm[(16 * bi + i) * 65 + j] = 0.0f;
+        }
+    }
+    __syncthreads();
+    if (wave < 3) {
+        const int bj = wave;
+        for (int bi = bj + 1; bi < 4; ++bi) {
+            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int bk = bj; bk < bi; ++bk)
+                acc = mm16_f32(Am + (16 * bi) * 65 + 16 * bk, 65, Tm + (16 * bk) * 65 + 16 * bj, 65, acc, lane);
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            uint16_t hh, ll;
-            split_bf16(Tc[i], hh, ll);
-            Th[i * kLT + lane] = hh;
-            Tl[i * kLT + lane] = ll;
+            for (int ii = 0; ii < 4; ++ii) scr[(4 * kb + ii) * 17 + n] = acc[ii];
+            __builtin_amdgcn_wave_barrier();
+            const f32x4_t res = mm16_f32(Tm + (16 * bi) * 65 + 16 * bi, 65, scr, 17,
+                                         f32x4_t{0.f, 0.f, 0.f, 0.f}, lane);
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) Tm[(16 * bi + 4 * kb + ii) * 65 + 16 * bj + n] = -res[ii];
+            __builtin_amdgcn_wave_barrier();
         }
-    } else {
-        // X = beta e^G K (fp32 K re-read, scaled, split) into the Q buffers
-        for (int idx = t - 64; idx < kC * 32; idx += 192) {
-            const int rr = idx >> 5, q4 = idx & 31;
-            const float sc = Bt[rr] * expf(G[rr]);
-            const float4 kv = rr < nv
-                ? reinterpret_cast<const float4*>(pk + (static_cast<size_t>(t0 + rr) * 16 + kh) * 128)[q4]
-                : make_float4(0.f, 0.f, 0.f, 0.f);
-            store_split4(Qh, Ql, rr * kLD + 4 * q4, sc * kv.x, sc * kv.y, sc * kv.z, sc * kv.w);
-        }
+    }
+    __syncthreads();
+    for (int idx = t; idx < kC * kC; idx += 256) {
+        const int i = idx >> 6, j = idx & 63;
+        uint16_t hh, ll;
+        split_bf16(Tm[i * 65 + j], hh, ll);
+        Th[i * kLT + j] = hh;
+        Tl[i * kLT + j] = ll;
+    }
+    __syncthreads();
+    // X = beta e^G K into the Q buffers; Q~ = e^G Q and K~ = e^{G_C - G} K to
+    // workspace (split) for the state pass
+    for (int idx = t; idx < kC * 32; idx += 256) {
+        const int rr = idx >> 5, q4 = idx & 31;
+        const float eg = expf(G[rr]);
+        const float sx = Bt[rr] * eg, sk = expf(G[kC - 1] - G[rr]);
+        const size_t src = (static_cast<size_t>(t0 + rr) * 16 + kh) * 128;
+        const float4 kv = rr < nv ? reinterpret_cast<const float4*>(pk + src)[q4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 qv = rr < nv ? reinterpret_cast<const float4*>(pq + src)[q4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        store_split4(Qh, Ql, rr * kLD + 4 * q4, sx * kv.x, sx * kv.y, sx * kv.z, sx * kv.w);
+        const size_t o = (ch * kC + rr) * 128 + 4 * q4;
+        store_split4(qth + o, qtl + o, 0, eg * qv.x, eg * qv.y, eg * qv.z, eg * qv.w);
+        store_split4(kth + o, ktl + o, 0, sk * kv.x, sk * kv.y, sk * kv.z, sk * kv.w);
     }
     __syncthreads();
     // W = T X and U~ = T (beta V): wave -> row tile, 8 column tiles of 16 dims
@@ -171,11 +210,12 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
 // grid (4 row blocks of 32, 32 value heads), 256 threads. Wave w keeps the
 // state tiles (row tile 0/1) x (column tiles 2w, 2w+1) in registers.
 __global__ __launch_bounds__(256) void dn_chunk_state_kernel(
-    int T, const float* __restrict__ pq, const float* __restrict__ pk, const uint16_t* __restrict__ wh,
-    const uint16_t* __restrict__ wl, const uint16_t* __restrict__ uh, const uint16_t* __restrict__ ul,
-    const uint16_t* __restrict__ ph, const uint16_t* __restrict__ pl, const float* __restrict__ gin,
-    float* __restrict__ ssm_state, float* __restrict__ po) {
-    const int rb = blockIdx.x, h = blockIdx.y, kh = h >> 1;
+    int T, const uint16_t* __restrict__ qth, const uint16_t* __restrict__ qtl, const uint16_t* __restrict__ kth,
+    const uint16_t* __restrict__ ktl, const uint16_t* __restrict__ wh, const uint16_t* __restrict__ wl,
+    const uint16_t* __restrict__ uh, const uint16_t* __restrict__ ul, const uint16_t* __restrict__ ph,
+    const uint16_t* __restrict__ pl, const float* __restrict__ gin, float* __restrict__ ssm_state,
+    float* __restrict__ po) {
+    const int rb = blockIdx.x, h = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
 
@@ -199,12 +239,71 @@ __global__ __launch_bounds__(256) void dn_chunk_state_kernel(
                 sacc[rt][cc][ii] = Sg[(16 * rt + 4 * kb + ii) * 128 + 16 * (2 * wave + cc) + n];
 
     const int nch = (T + kC - 1) / kC;
-    const int r = t >> 2, d0 = 32 * (t & 3);
+    // Chunk inputs travel global -> registers -> LDS; the registers for chunk
+    // c+1 are loaded while chunk c computes. Per thread: 4 x 16 B of each of
+    // W, Q~, K~ (hi and lo), 2 x 16 B of P hi and lo, and the 16 U~ values
+    // (hi, lo) its Y1 outputs need.
+    u32x4_t pre[6][4], prep_[2][2];
+    uint16_t preu[2][2][4][2];
+    float preg = 0.0f;
+    auto fetch = [&](int c) {
+        const size_t ch = static_cast<size_t>(c) * 32 + h;
+        // the small loads first: vmcnt retires in issue order, so consuming
+        // them early must not wait on the bulk copies behind them
+        const int rt = wave & 1;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int i = 16 * (2 * (wave >> 1) + cc) + n;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const size_t gu = (ch * kC + i) * 128 + 32 * rb + 16 * rt + 4 * kb + ii;
+                preu[cc][0][ii][0] = uh[gu];
+                preu[cc][0][ii][1] = ul[gu];
+            }
+        }
+        if (t < kC) preg = gin[ch * kC + t];
+        const size_t o = ch * kC * 128;
+        const uint16_t* srcs[6] = {wh + o, wl + o, qth + o, qtl + o, kth + o, ktl + o};
+#pragma unroll
+        for (int a = 0; a < 6; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pre[a][i] = reinterpret_cast<const u32x4_t*>(srcs[a])[t + 256 * i];
+        const u32x4_t* gp_h = reinterpret_cast<const u32x4_t*>(ph + ch * kC * kC);
+        const u32x4_t* gp_l = reinterpret_cast<const u32x4_t*>(pl + ch * kC * kC);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            prep_[0][i] = gp_h[t + 256 * i];
+            prep_[1][i] = gp_l[t + 256 * i];
+        }
+    };
+    fetch(0);
     for (int c = 0; c < nch; ++c) {
         const int t0 = c * kC;
         const int nv = min(kC, T - t0);
-        const size_t ch = static_cast<size_t>(c) * 32 + h;
-        if (t < kC) G[t] = gin[ch * kC + t];
+        // registers -> LDS
+        {
+            uint16_t* dst[6] = {Wh, Wl, Qh, Ql, Kh, Kl};
+#pragma unroll
+            for (int a = 0; a < 6; ++a)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int q = t + 256 * i;
+                    *reinterpret_cast<u32x4_t*>(&dst[a][(q >> 4) * kLD + 8 * (q & 15)]) = pre[a][i];
+                }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int q = t + 256 * i;
+                *reinterpret_cast<u32x4_t*>(&Ph[(q >> 3) * kLT + 8 * (q & 7)]) = prep_[0][i];
+                *reinterpret_cast<u32x4_t*>(&Pl[(q >> 3) * kLT + 8 * (q & 7)]) = prep_[1][i];
+            }
+            if (t < kC) G[t] = preg;
+        }
+        float ucur[2][4];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                ucur[cc][ii] = bf16_to_f32(preu[cc][0][ii][0]) + bf16_to_f32(preu[cc][0][ii][1]);
         // state -> LDS as the A operand (rows of this block)
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
@@ -218,74 +317,40 @@ __global__ __launch_bounds__(256) void dn_chunk_state_kernel(
                     Sh[o] = hh;
                     Sl[o] = ll;
                 }
-        // W and P (already split) -> LDS
-        {
-            const u32x4_t* gw_h = reinterpret_cast<const u32x4_t*>(wh + ch * kC * 128);
-            const u32x4_t* gw_l = reinterpret_cast<const u32x4_t*>(wl + ch * kC * 128);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = t + 256 * i;          // 1024 x 16 B per array
-                const int rr = q >> 4, cq = q & 15;
-                *reinterpret_cast<u32x4_t*>(&Wh[rr * kLD + 8 * cq]) = gw_h[q];
-                *reinterpret_cast<u32x4_t*>(&Wl[rr * kLD + 8 * cq]) = gw_l[q];
-            }
-            const u32x4_t* gp_h = reinterpret_cast<const u32x4_t*>(ph + ch * kC * kC);
-            const u32x4_t* gp_l = reinterpret_cast<const u32x4_t*>(pl + ch * kC * kC);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int q = t + 256 * i;          // 512 x 16 B per array
-                const int rr = q >> 3, cq = q & 7;
-                *reinterpret_cast<u32x4_t*>(&Ph[rr * kLT + 8 * cq]) = gp_h[q];
-                *reinterpret_cast<u32x4_t*>(&Pl[rr * kLT + 8 * cq]) = gp_l[q];
-            }
-        }
         __syncthreads();
-        // Q~ and K~ (key head rows, scaled by the chunk's gates), split
-        {
-            const float gq = expf(G[r]), gk = expf(G[kC - 1] - G[r]);
-            const float4* ks = reinterpret_cast<const float4*>(pk + (static_cast<size_t>(t0 + r) * 16 + kh) * 128 + d0);
-            const float4* qs = reinterpret_cast<const float4*>(pq + (static_cast<size_t>(t0 + r) * 16 + kh) * 128 + d0);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 kv = r < nv ? ks[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float4 qv = r < nv ? qs[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                store_split4(Kh, Kl, r * kLD + d0 + 4 * i, gk * kv.x, gk * kv.y, gk * kv.z, gk * kv.w);
-                store_split4(Qh, Ql, r * kLD + d0 + 4 * i, gq * qv.x, gq * qv.y, gq * qv.z, gq * qv.w);
-            }
-        }
+        if (c + 1 < nch) fetch(c + 1);
         const float gamma = expf(G[kC - 1]);
         // U^T[r][i] = U~[i][r] - sum_d S[r][d] W[i][d]: wave -> row tile w&1,
         // token tiles 2(w>>1), +1
-        const int rt = wave & 1;
+        const int rt = wave & 1, ci0 = 2 * (wave >> 1);
+        {
+            f32x4_t sw[1][2] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}}};
+            mma_block_x3<128, 1, 2, false>(sw, Sh, Sl, kLD, 16 * rt, Wh, Wl, kLD, 16 * ci0, lane);
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int ci = 2 * (wave >> 1) + cc;
-            const f32x4_t sw = mma_nt_x3<128>(f32x4_t{0.f, 0.f, 0.f, 0.f}, Sh + 16 * rt * kLD, Sl + 16 * rt * kLD,
-                                              kLD, Wh + 16 * ci * kLD, Wl + 16 * ci * kLD, kLD, lane);
-            const int i = 16 * ci + n;
+            for (int cc = 0; cc < 2; ++cc) {
+                const int i = 16 * (ci0 + cc) + n;
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int rr = 16 * rt + 4 * kb + ii;
-                const size_t gu = (ch * kC + i) * 128 + 32 * rb + rr;
-                const float ut = bf16_to_f32(uh[gu]) + bf16_to_f32(ul[gu]) - sw[ii];
-                uint16_t hh, ll;
-                split_bf16(ut, hh, ll);
-                Uh[rr * kLT + i] = hh;
-                Ul[rr * kLT + i] = ll;
+                for (int ii = 0; ii < 4; ++ii) {
+                    const int rr = 16 * rt + 4 * kb + ii;
+                    uint16_t hh, ll;
+                    split_bf16(ucur[cc][ii] - sw[0][cc][ii], hh, ll);
+                    Uh[rr * kLT + i] = hh;
+                    Ul[rr * kLT + i] = ll;
+                }
             }
         }
         __syncthreads();
         // O^T[r][i] = sum_d S[r][d] Q~[i][d] + sum_j U^T[r][j] P[i][j]
+        {
+            f32x4_t o[1][2] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}}};
+            mma_block_x3<128, 1, 2, false>(o, Sh, Sl, kLD, 16 * rt, Qh, Ql, kLD, 16 * ci0, lane);
+            mma_block_x3<kC, 1, 2, false>(o, Uh, Ul, kLT, 16 * rt, Ph, Pl, kLT, 16 * ci0, lane);
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int ci = 2 * (wave >> 1) + cc;
-            f32x4_t o = mma_nt_x3<128>(f32x4_t{0.f, 0.f, 0.f, 0.f}, Sh + 16 * rt * kLD, Sl + 16 * rt * kLD, kLD,
-                                       Qh + 16 * ci * kLD, Ql + 16 * ci * kLD, kLD, lane);
-            o = mma_nt_x3<kC>(o, Uh + 16 * rt * kLT, Ul + 16 * rt * kLT, kLT, Ph + 16 * ci * kLT, Pl + 16 * ci * kLT,
-                              kLT, lane);
-            const int i = 16 * ci + n;
+            for (int cc = 0; cc < 2; ++cc) {
+                const int i = 16 * (ci0 + cc) + n;
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) Os[i * 33 + 16 * rt + 4 * kb + ii] = o[ii];
+                for (int ii = 0; ii < 4; ++ii) Os[i * 33 + 16 * rt + 4 * kb + ii] = o[0][cc][ii];
+            }
         }
         __syncthreads();
         // pre-norm outputs of this block's 32 rows, token-major
@@ -301,14 +366,10 @@ __global__ __launch_bounds__(256) void dn_chunk_state_kernel(
 #pragma unroll
         for (int rt2 = 0; rt2 < 2; ++rt2)
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                f32x4_t s = sacc[rt2][cc];
+            for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) s[ii] *= gamma;
-                const int ct = 2 * wave + cc;
-                sacc[rt2][cc] = mma_nn_x3<kC>(s, Uh + 16 * rt2 * kLT, Ul + 16 * rt2 * kLT, kLT, Kh + 16 * ct,
-                                              Kl + 16 * ct, kLD, lane);
-            }
+                for (int ii = 0; ii < 4; ++ii) sacc[rt2][cc][ii] *= gamma;
+        mma_block_x3<kC, 2, 2, true>(sacc, Uh, Ul, kLT, 0, Kh, Kl, kLD, 32 * wave, lane);
         __syncthreads();
     }
 #pragma unroll
@@ -324,14 +385,14 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, int T, floa
     const int nch = (T + kC - 1) / kC;
     {
         ProfScope prof(ctx, stream, "dn_chunk_local");
-        dn_chunk_local_kernel<<<dim3(nch, 32), 256, 0, stream>>>(T, ctx->pf_q, ctx->pf_k, ctx->pf_v, ctx->pf_g,
-                                                                 ctx->pf_beta, ctx->pf_wh, ctx->pf_wl, ctx->pf_uh,
-                                                                 ctx->pf_ul, ctx->pf_ph, ctx->pf_pl, ctx->pf_G);
+        dn_chunk_local_kernel<<<dim3(nch, 32), 256, 0, stream>>>(
+            T, ctx->pf_q, ctx->pf_k, ctx->pf_v, ctx->pf_g, ctx->pf_beta, ctx->pf_wh, ctx->pf_wl, ctx->pf_uh,
+            ctx->pf_ul, ctx->pf_ph, ctx->pf_pl, ctx->pf_G, ctx->pf_qth, ctx->pf_qtl, ctx->pf_kth, ctx->pf_ktl);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
-    dn_chunk_state_kernel<<<dim3(4, 32), 256, 0, stream>>>(T, ctx->pf_q, ctx->pf_k, ctx->pf_wh, ctx->pf_wl, ctx->pf_uh,
-                                                           ctx->pf_ul, ctx->pf_ph, ctx->pf_pl, ctx->pf_G, ssm_state,
-                                                           ctx->pf_o);
+    dn_chunk_state_kernel<<<dim3(4, 32), 256, 0, stream>>>(T, ctx->pf_qth, ctx->pf_qtl, ctx->pf_kth, ctx->pf_ktl,
+                                                           ctx->pf_wh, ctx->pf_wl, ctx->pf_uh, ctx->pf_ul, ctx->pf_ph,
+                                                           ctx->pf_pl, ctx->pf_G, ssm_state, ctx->pf_o);
     return hipGetLastError();
 }
 

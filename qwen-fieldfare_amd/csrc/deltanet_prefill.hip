@@ -24,57 +24,93 @@ __device__ __forceinline__ float conv_ext(const float* __restrict__ conv_state, 
     return i < 4 ? conv_state[c * 4 + i] : elem<IN_DT>::load(qkv, static_cast<size_t>(i - 4) * 8192 + c);
 }
 
-// grid (T, 64 channel blocks of 128), 128 threads.
+constexpr int kPrepTokens = 16;   // tokens per prep workgroup
+
+// grid (ceil(T/16), 32 channel blocks of 256), 256 threads: thread = channel,
+// walking 16 tokens with a sliding 4-tap window (one new input per token).
+// Channel blocks 0-7 hold q (two key heads each), 8-15 k, 16-31 v. Block 0
+// also forms the 16 tokens' log gates and betas.
 template <int IN_DT>
-__global__ __launch_bounds__(128) void dn_prefill_prep_kernel(
-    const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
+__global__ __launch_bounds__(256) void dn_prefill_prep_kernel(
+    int T, const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ a_log, const float* __restrict__ dt_bias, const float* __restrict__ conv_w,
     const float* __restrict__ conv_state, float* __restrict__ pq, float* __restrict__ pk,
-    float* __restrict__ pv, float* __restrict__ pg, float* __restrict__ pbeta) {
-    const int tok = blockIdx.x, blk = blockIdx.y, t = threadIdx.x;
-    const int c = blk * 128 + t;
+    float* __restrict__ pv, float* __restrict__ plg, float* __restrict__ pbeta) {
+    __shared__ float red[kPrepTokens][4];
+    const int tb = blockIdx.x * kPrepTokens, blk = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int c = blk * 256 + t;
+    const int nt = min(kPrepTokens, T - tb);
     const float4 w = reinterpret_cast<const float4*>(conv_w)[c];
     // token tok uses e[tok+1 .. tok+4] (deltanet.metal:120-137 after the shift)
-    const float e0 = conv_ext<IN_DT>(conv_state, qkv, c, tok + 1);
-    const float e1 = conv_ext<IN_DT>(conv_state, qkv, c, tok + 2);
-    const float e2 = conv_ext<IN_DT>(conv_state, qkv, c, tok + 3);
-    const float e3 = conv_ext<IN_DT>(conv_state, qkv, c, tok + 4);
-    const float y = silu(e0 * w.x + e1 * w.y + e2 * w.z + e3 * w.w);
-    if (blk < 32) {
-        __shared__ float red[2];
-        const float ss = group_sum<64>(y * y);
-        if ((t & 63) == 0) red[t >> 6] = ss;
-        __syncthreads();
-        const float inv = 1.0f / sqrtf(red[0] + red[1] + 1e-6f);
-        if (blk < 16) pq[static_cast<size_t>(tok) * 2048 + c] = (y * inv) * (1.0f / sqrtf(128.0f));
-        else pk[static_cast<size_t>(tok) * 2048 + (c - 2048)] = y * inv;
-    } else {
-        pv[static_cast<size_t>(tok) * 4096 + (c - 4096)] = y;
+    float e1 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 1);
+    float e2 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 2);
+    float e3 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 3);
+    float y[kPrepTokens];
+#pragma unroll
+    for (int i = 0; i < kPrepTokens; ++i) {
+        const float e4 = i < nt ? elem<IN_DT>::load(qkv, static_cast<size_t>(tb + i) * 8192 + c) : 0.0f;
+        y[i] = silu(e1 * w.x + e2 * w.y + e3 * w.z + e4 * w.w);
+        e1 = e2; e2 = e3; e3 = e4;
     }
-    if (blk == 0 && t < 32) {
-        const int i = tok * 32 + t;
-        pg[i] = -expf(a_log[t]) * softplus(a[i] + dt_bias[t]);   // log g
-        pbeta[i] = sigmoid(b[i]);
+    if (blk < 16) {
+        // L2 norm per key head: waves 0-1 one head, waves 2-3 the other
+#pragma unroll
+        for (int i = 0; i < kPrepTokens; ++i) {
+            const float ss = group_sum<64>(y[i] * y[i]);
+            if (lane == 0) red[i][wave] = ss;
+        }
+        __syncthreads();
+        const int hw = wave & 2;
+        float* dst = blk < 8 ? pq : pk;
+        const int cc = blk < 8 ? c : c - 2048;
+#pragma unroll
+        for (int i = 0; i < kPrepTokens; ++i) {
+            if (i >= nt) break;
+            const float inv = 1.0f / sqrtf(red[i][hw] + red[i][hw + 1] + 1e-6f);
+            const float v = blk < 8 ? (y[i] * inv) * (1.0f / sqrtf(128.0f)) : y[i] * inv;
+            dst[static_cast<size_t>(tb + i) * 2048 + cc] = v;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kPrepTokens; ++i) {
+            if (i >= nt) break;
+            pv[static_cast<size_t>(tb + i) * 4096 + (c - 4096)] = y[i];
+        }
+    }
+    if (blk == 0) {
+        for (int idx = t; idx < nt * 32; idx += 256) {
+            const int hh = idx & 31;
+            const size_t gi = static_cast<size_t>(tb) * 32 + idx;
+            plg[gi] = -expf(a_log[hh]) * softplus(a[gi] + dt_bias[hh]);   // log g
+            pbeta[gi] = sigmoid(b[gi]);
+        }
     }
 }
 
-// grid (T, 16), 256 threads: value heads 2*blockIdx.y (waves 0-1) and +1.
+// grid (T), 256 threads: thread -> value head t/8, rows 16*(t%8) .. +15.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __restrict__ po,
                                                               const void* __restrict__ z,
                                                               const float* __restrict__ norm_w, float eps,
                                                               void* __restrict__ out) {
-    __shared__ float red[4];
     const int tok = blockIdx.x, t = threadIdx.x;
-    const int hh = blockIdx.y * 2 + (t >> 7), r = t & 127;
-    const size_t i = static_cast<size_t>(tok) * 4096 + hh * 128 + r;
-    const float o = po[i];
-    const float ss = group_sum<64>(o * o);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    const float tot = (t < 128) ? (red[0] + red[1]) : (red[2] + red[3]);
-    const float inv = 1.0f / sqrtf(tot / 128.0f + eps);
-    elem<OUT_DT>::store(out, i, o * inv * norm_w[r] * silu(elem<IN_DT>::load(z, i)));
+    const int r0 = 16 * (t & 7);
+    const size_t base = static_cast<size_t>(tok) * 4096 + (t >> 3) * 128 + r0;
+    const float4* src = reinterpret_cast<const float4*>(po + base);
+    float o[16], ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = src[i];
+        o[4 * i] = v.x; o[4 * i + 1] = v.y; o[4 * i + 2] = v.z; o[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss += o[i] * o[i];
+    ss = group_sum<8>(ss);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        elem<OUT_DT>::store(out, base + i, o[i] * inv * norm_w[r0 + i] * silu(elem<IN_DT>::load(z, base + i)));
 }
 
 // conv state after the last token: slots = e[T .. T+3]. grid 32 x 256.
@@ -97,11 +133,11 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
     {
     ProfScope prof(ctx, stream, "dn_prefill_prep");
     if (bf)
-        dn_prefill_prep_kernel<1><<<dim3(T, 64), 128, 0, stream>>>(qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
+        dn_prefill_prep_kernel<1><<<dim3((T + kPrepTokens - 1) / kPrepTokens, 32), 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
                                                                   conv_state, ctx->pf_q, ctx->pf_k, ctx->pf_v,
                                                                   ctx->pf_g, ctx->pf_beta);
     else
-        dn_prefill_prep_kernel<0><<<dim3(T, 64), 128, 0, stream>>>(qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
+        dn_prefill_prep_kernel<0><<<dim3((T + kPrepTokens - 1) / kPrepTokens, 32), 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
                                                                   conv_state, ctx->pf_q, ctx->pf_k, ctx->pf_v,
                                                                   ctx->pf_g, ctx->pf_beta);
     }
@@ -109,7 +145,7 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
         hipError_t e = launch_deltanet_chunked(ctx, stream, T, ssm_state);
         if (e != hipSuccess) return e;
     }
-    const dim3 ng(T, 16);
+    const dim3 ng(T);
     {
     ProfScope prof(ctx, stream, "dn_prefill_norm");
 #define QFF_NORM(I, O) dn_prefill_norm_kernel<I, O><<<ng, 256, 0, stream>>>(ctx->pf_o, z, p->norm_w, p->eps, out)

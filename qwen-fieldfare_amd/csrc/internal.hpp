@@ -40,6 +40,10 @@ struct qff_ctx {
     uint16_t* pf_ul = nullptr;
     uint16_t* pf_ph = nullptr;
     uint16_t* pf_pl = nullptr;
+    uint16_t* pf_qth = nullptr;   // Q~ [64][128] per (chunk, value head)
+    uint16_t* pf_qtl = nullptr;
+    uint16_t* pf_kth = nullptr;   // K~ [64][128] per (chunk, value head)
+    uint16_t* pf_ktl = nullptr;
     float* pf_G = nullptr;
     // Kernel timing (qff_profile_enable): a pool of event pairs.
     bool prof = false;
@@ -53,7 +57,7 @@ constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o, pf_wh, pf_wl, pf_uh, pf_ul, pf_ph, pf_pl, pf_G;
+    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o, pf_wh, pf_wl, pf_uh, pf_ul, pf_ph, pf_pl, pf_qth, pf_qtl, pf_kth, pf_ktl, pf_G;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

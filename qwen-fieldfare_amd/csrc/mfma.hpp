@@ -116,6 +116,66 @@ __device__ __forceinline__ f32x4_t mma_nn_x3(f32x4_t acc, const uint16_t* ah, co
     return acc;
 }
 
+// acc += A[16x16] B[16x16] in fp32 on v_mfma_f32_16x16x4_f32 (A row-major
+// stride lda, B row-major stride ldb; LDS or global).
+// Layout: A lane l holds A[l%16][k = l/16], B lane l holds B[k = l/16][l%16].
+__device__ __forceinline__ f32x4_t mm16_f32(const float* A, int lda, const float* B, int ldb, f32x4_t acc,
+                                            int lane) {
+    const int n = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[n * lda + 4 * kk + kq], B[(4 * kk + kq) * ldb + n], acc, 0, 0, 0);
+    return acc;
+}
+
+// MR x NC block of 16x16 tiles, C[r][c] += A_r B_c with bf16x3, sharing each
+// operand read across the block: A row tile r starts at row ar + 16 r of a
+// row-major [rows][K] array; B column tile c starts at column bc + 16 c,
+// given as its transpose (NT: row-major [cols][K]) or as row-major [K][cols]
+// (NN, read with the LDS transpose read).
+template <int K, int MR, int NC, bool NN>
+__device__ __forceinline__ void mma_block_x3(f32x4_t (&acc)[MR][NC], const uint16_t* ah, const uint16_t* al,
+                                             int lda, int ar, const uint16_t* bh, const uint16_t* bl, int ldb,
+                                             int bc, int lane) {
+    const int n = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        u32x4_t a_h[MR], a_l[MR], b_h[NC], b_l[NC];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const int ao = (ar + 16 * r + n) * lda + k0 + 8 * kb;
+            a_h[r] = *reinterpret_cast<const u32x4_t*>(ah + ao);
+            a_l[r] = *reinterpret_cast<const u32x4_t*>(al + ao);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (NN) {
+                const int bo = (k0 + 8 * kb + (n >> 2)) * ldb + bc + 16 * c + 4 * (n & 3);
+                const u32x2_t h0 = lds_read_tr16(bh + bo), h1 = lds_read_tr16(bh + bo + 4 * ldb);
+                const u32x2_t l0 = lds_read_tr16(bl + bo), l1 = lds_read_tr16(bl + bo + 4 * ldb);
+                b_h[c] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+                b_l[c] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+            } else {
+                const int bo = (bc + 16 * c + n) * ldb + k0 + 8 * kb;
+                b_h[c] = *reinterpret_cast<const u32x4_t*>(bh + bo);
+                b_l[c] = *reinterpret_cast<const u32x4_t*>(bl + bo);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[r][c] = mfma_16x16x32_bf16(a_l[r], b_h[c], acc[r][c]);
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[r][c] = mfma_16x16x32_bf16(a_h[r], b_l[c], acc[r][c]);
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[r][c] = mfma_16x16x32_bf16(a_h[r], b_h[c], acc[r][c]);
+    }
+}
+
 // Store 4 fp32 values as hi/lo bf16 at hi[i..i+3], lo[i..i+3] (8-byte aligned).
 __device__ __forceinline__ void store_split4(uint16_t* hi, uint16_t* lo, int i, float a, float b, float c, float d) {
     uint16_t h0, h1, h2, h3, l0, l1, l2, l3;
