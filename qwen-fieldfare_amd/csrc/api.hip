@@ -31,24 +31,16 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_m = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
     L.gqa_d = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
     L.gqa_o = take(B * 2 * kGqaMaxChunks * 8 * 256 * sizeof(float));
-    L.pf_q = take(T * 2048 * sizeof(float));
-    L.pf_k = take(T * 2048 * sizeof(float));
-    L.pf_v = take(T * 4096 * sizeof(float));
-    L.pf_g = take(T * 32 * sizeof(float));
-    L.pf_beta = take(T * 32 * sizeof(float));
-    L.pf_o = take(T * 4096 * sizeof(float));
+    L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
-    L.pf_wh = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_wl = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_uh = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_ul = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_ph = take(TC * 32 * 64 * sizeof(uint16_t));
-    L.pf_pl = take(TC * 32 * 64 * sizeof(uint16_t));
-    L.pf_qth = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_qtl = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_kth = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_ktl = take(TC * 32 * 128 * sizeof(uint16_t));
-    L.pf_G = take(TC * 32 * sizeof(float));
+    L.pf_o = take(TC * 4096 * sizeof(float));
+    const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
+    L.wh = take(big); L.wl = take(big);
+    L.qeh = take(big); L.qel = take(big);
+    L.kth = take(big); L.ktl = take(big);
+    L.uth = take(big); L.utl = take(big);
+    L.ph = take(small); L.pl = take(small);
+    L.gam = take(TC / 64 * 32 * sizeof(float));
     L.total = off;
     return L;
 }
@@ -154,23 +146,11 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_m = reinterpret_cast<float*>(base + L.gqa_m);
     c->gqa_d = reinterpret_cast<float*>(base + L.gqa_d);
     c->gqa_o = reinterpret_cast<float*>(base + L.gqa_o);
-    c->pf_q = reinterpret_cast<float*>(base + L.pf_q);
-    c->pf_k = reinterpret_cast<float*>(base + L.pf_k);
-    c->pf_v = reinterpret_cast<float*>(base + L.pf_v);
-    c->pf_g = reinterpret_cast<float*>(base + L.pf_g);
-    c->pf_beta = reinterpret_cast<float*>(base + L.pf_beta);
+    auto u16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
+    c->gqa_qb = u16(L.gqa_qb);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
-    c->pf_wh = reinterpret_cast<uint16_t*>(base + L.pf_wh);
-    c->pf_wl = reinterpret_cast<uint16_t*>(base + L.pf_wl);
-    c->pf_uh = reinterpret_cast<uint16_t*>(base + L.pf_uh);
-    c->pf_ul = reinterpret_cast<uint16_t*>(base + L.pf_ul);
-    c->pf_ph = reinterpret_cast<uint16_t*>(base + L.pf_ph);
-    c->pf_pl = reinterpret_cast<uint16_t*>(base + L.pf_pl);
-    c->pf_qth = reinterpret_cast<uint16_t*>(base + L.pf_qth);
-    c->pf_qtl = reinterpret_cast<uint16_t*>(base + L.pf_qtl);
-    c->pf_kth = reinterpret_cast<uint16_t*>(base + L.pf_kth);
-    c->pf_ktl = reinterpret_cast<uint16_t*>(base + L.pf_ktl);
-    c->pf_G = reinterpret_cast<float*>(base + L.pf_G);
+    c->dn = qff_dn_bufs{u16(L.wh),  u16(L.wl),  u16(L.qeh), u16(L.qel), u16(L.kth), u16(L.ktl),
+                        u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam)};
     (void)hipSetDevice(prev);
     *out = c;
     return QFF_OK;

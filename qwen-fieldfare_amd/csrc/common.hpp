@@ -50,6 +50,11 @@ template <> struct elem<2> {
 };
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// SiLU on the hardware exp2 and reciprocal (a few ulp) for bulk elementwise
+// work whose consumers tolerate it.
+__device__ __forceinline__ float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplus(float x) {
     if (x > 20.0f) return x;

@@ -10,21 +10,26 @@
 // unrolling gives the chunk identities this file evaluates:
 //   A_ij = beta_i e^{G_i - G_j} (k_i . k_j)  (j < i),     T = (I + A)^-1
 //   W = T (beta e^G K),  U~ = T (beta V),  U = U~ - W S0^T
-//   O = (e^G Q) S0^T + (e^{G_i - G_j} [j <= i] Q K^T) U
-//   S_C = e^{G_C} S0 + U^T (e^{G_C - G} K)
+//   P_ij = e^{G_i - G_j} (q_i . k_j)  (j <= i)
+//   O = (e^G Q) S0^T + P U = Qe S0^T + P U~,   Qe = e^G Q - P W
+//   S_C = e^{G_C} S0 + U^T K~,  K~ = e^{G_C - G} K
 // (tests/test_oracle_deltanet.py checks them against the sequential
-// recurrence in fp64).
+// recurrence in fp64). Writing O through Qe takes U out of it, so the
+// sequential pass forms U and O from the same S0 in one step.
 //
 // Two kernels:
 //   dn_chunk_local_kernel  one workgroup per (chunk, value head), all chunks
-//       at once: A from K K^T, P = e^{G_i-G_j}[j<=i] Q K^T, T = (I + A)^-1
-//       in 16x16 blocks (diagonal blocks by substitution, the rest on fp32
-//       MFMAs, four waves in parallel), then W and U~; W, U~, P, the scaled
-//       Q~ = e^G Q and K~ = e^{G_C - G} K (all split into bf16 hi/lo) and G
-//       go to workspace.
-//   dn_chunk_state_kernel  one workgroup per (32-row block of the state,
-//       value head) walks the chunks in order with its state slice in
-//       registers: U = U~ - W S^T, O = Q~ S^T + P U, S = e^{G_C} S + U^T K~.
+//       at once: conv1d + SiLU of the chunk's q, k, v channels straight from
+//       the projection (3 tokens of history from the input or the conv
+//       state), L2 norms, gates, then A, P, T (16x16 blocks: diagonal blocks
+//       by substitution, the rest on fp32 MFMAs), W, U~ and Qe; writes W, Qe,
+//       K~^T, U~^T, P (bf16 hi/lo) and e^{G_C}.
+//   dn_chunk_state_kernel  one workgroup per (block of RB state rows, value
+//       head) walks the chunks in order with its state rows in registers:
+//       U^T = U~^T - S W^T and O^T = S Qe^T + U~^T P^T in one pass over
+//       [S | U~^T], then S = e^{G_C} S + U^T K~. Its MFMA B operands are read
+//       from global memory straight into registers in operand layout, one
+//       chunk ahead.
 // Every product runs as bf16x3 on v_mfma_f32_16x16x32_bf16 (a b ~ a_hi b_hi
 // + a_hi b_lo + a_lo b_hi, ~2^-16 relative per product), which keeps the
 // fp32 state within 1e-4 of the sequential fp32 recurrence; plain bf16
@@ -38,92 +43,232 @@ namespace qff {
 constexpr int kC = 64;      // chunk length
 constexpr int kLD = 136;    // bf16 row stride of [64][128] LDS tiles (128 + 8)
 constexpr int kLT = 72;     // bf16 row stride of [64][64] LDS tiles (64 + 8)
+#ifndef QFF_DN_STATE_RB
+#define QFF_DN_STATE_RB 16
+#endif
+
+// ---- chunk-local pass --------------------------------------------------------
+
+// Conv input of 8 consecutive channels at stream position pos: the token's
+// projection for pos >= 0, conv-state slot pos + 4 for pos in [-3, -1].
+template <int IN_DT>
+__device__ __forceinline__ void load_e8(const void* __restrict__ qkv, const float* __restrict__ conv_state, int ch,
+                                        int pos, float (&e)[8], bool may_precede) {
+    if (!may_precede || pos >= 0) {
+        if (IN_DT == 1) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(qkv) +
+                                                                static_cast<size_t>(pos) * 8192 + ch);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                e[2 * k] = __uint_as_float(v[k] << 16);
+                e[2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
+            }
+        } else {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(qkv) +
+                                                              static_cast<size_t>(pos) * 8192 + ch);
+            const float4 v0 = p[0], v1 = p[1];
+            e[0] = v0.x; e[1] = v0.y; e[2] = v0.z; e[3] = v0.w;
+            e[4] = v1.x; e[5] = v1.y; e[6] = v1.z; e[7] = v1.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = conv_state[(ch + k) * 4 + pos + 4];
+    }
+}
+
+// y[i][k] = SiLU(conv1d) of channel ch + k at token tok0 + i (deltanet.metal
+// :120-137: taps w.x .. w.w over inputs tok-3 .. tok); 0 for tokens >= T.
+// EDGE: the window may reach before token 0 (conv state) or past T - 1;
+// chunks away from both ends take the branch-free path.
+template <int IN_DT, int NT, bool EDGE>
+__device__ __forceinline__ void conv8(const void* __restrict__ qkv, const float* __restrict__ conv_state,
+                                      const float* __restrict__ conv_w, int ch, int tok0, int T,
+                                      float (&y)[NT][8]) {
+    float e[NT + 3][8];
+#pragma unroll
+    for (int i = 0; i < NT + 3; ++i) {
+        const int pos = tok0 - 3 + i;
+        if (!EDGE || pos < T) {
+            load_e8<IN_DT>(qkv, conv_state, ch, pos, e[i], EDGE);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) e[i][k] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float4 w = reinterpret_cast<const float4*>(conv_w)[ch + k];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const float v = silu_fast(e[i][k] * w.x + e[i + 1][k] * w.y + e[i + 2][k] * w.z + e[i + 3][k] * w.w);
+            y[i][k] = !EDGE || tok0 + i < T ? v : 0.0f;
+        }
+    }
+}
+
+template <int IN_DT, int NT>
+__device__ __forceinline__ void conv8_any(bool edge, const void* __restrict__ qkv, const float* __restrict__ conv_state,
+                                          const float* __restrict__ conv_w, int ch, int tok0, int T,
+                                          float (&y)[NT][8]) {
+    if (edge)
+        conv8<IN_DT, NT, true>(qkv, conv_state, conv_w, ch, tok0, T, y);
+    else
+        conv8<IN_DT, NT, false>(qkv, conv_state, conv_w, ch, tok0, T, y);
+}
+
+// Splits 8 floats into bf16 hi / lo and stores 16 B of each.
+__device__ __forceinline__ void store_split8(uint16_t* hi, uint16_t* lo, const float (&x)[8]) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) split_bf16x2(x[2 * k], x[2 * k + 1], hw[k], lw[k]);
+    *reinterpret_cast<u32x4_t*>(hi) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<u32x4_t*>(lo) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+}
+
+// LDS carve-up of the chunk-local kernel (bytes)
+constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
+constexpr int kOffK = 0;                          // K hi, lo; then X = beta e^G K; then P W (fp32)
+constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T (fp32) + scratch; then W hi, lo
+constexpr int kOffV = 4 * kTile128;               // beta V hi, lo
+constexpr int kOffA = 6 * kTile128;               // A fp32 [64][65]
+constexpr int kOffT = kOffA + kC * 65 * 4;        // P hi, lo, then T hi, lo, then P again: [64][72]
+constexpr int kOffG = kOffT + 2 * kC * kLT * 2;   // G[64], beta[64]
+constexpr int kLocalSmem = kOffG + 2 * kC * 4;
 
 // grid (ceil(T/64), 32 value heads), 256 threads.
+template <int IN_DT>
 __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
-    int T, const float* __restrict__ pq, const float* __restrict__ pk, const float* __restrict__ pv,
-    const float* __restrict__ plg, const float* __restrict__ pbeta, uint16_t* __restrict__ wh,
-    uint16_t* __restrict__ wl, uint16_t* __restrict__ uh, uint16_t* __restrict__ ul, uint16_t* __restrict__ ph,
-    uint16_t* __restrict__ pl, float* __restrict__ gout, uint16_t* __restrict__ qth, uint16_t* __restrict__ qtl,
-    uint16_t* __restrict__ kth, uint16_t* __restrict__ ktl) {
+    int T, const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ a_log, const float* __restrict__ dt_bias, const float* __restrict__ conv_w,
+    const float* __restrict__ conv_state, qff_dn_bufs out) {
     const int c = blockIdx.x, h = blockIdx.y, kh = h >> 1;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
     const int t0 = c * kC;
     const int nv = min(kC, T - t0);
     const size_t ch = static_cast<size_t>(c) * 32 + h;
+    const bool edge = c == 0 || t0 + kC > T;   // conv window leaves [0, T)
 
-    __shared__ __attribute__((aligned(16))) uint16_t Kh[kC * kLD], Kl[kC * kLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Qh[kC * kLD], Ql[kC * kLD];   // Q, later X = beta e^G K
-    __shared__ __attribute__((aligned(16))) uint16_t Vh[kC * kLD], Vl[kC * kLD];   // beta V
-    __shared__ __attribute__((aligned(16))) uint16_t Th[kC * kLT], Tl[kC * kLT];
-    __shared__ float Am[kC * 65];
-    __shared__ float G[kC], Bt[kC];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kLocalSmem];
+    uint16_t* Kh = reinterpret_cast<uint16_t*>(smem + kOffK);
+    uint16_t* Kl = Kh + kC * kLD;
+    uint16_t* Qh = reinterpret_cast<uint16_t*>(smem + kOffQ);
+    uint16_t* Ql = Qh + kC * kLD;
+    uint16_t* Vh = reinterpret_cast<uint16_t*>(smem + kOffV);
+    uint16_t* Vl = Vh + kC * kLD;
+    float* Am = reinterpret_cast<float*>(smem + kOffA);
+    uint16_t* Th = reinterpret_cast<uint16_t*>(smem + kOffT);
+    uint16_t* Tl = Th + kC * kLT;
+    float* G = reinterpret_cast<float*>(smem + kOffG);
+    float* Bt = G + kC;
 
-    // gates: G = inclusive prefix sum of log g over the chunk; padded tokens
-    // have log g = 0 and beta = 0, so they change nothing
+    // gates (deltanet.metal:250-280): log g = -e^{A_log} softplus(a + dt_bias),
+    // beta = sigmoid(b); G = inclusive prefix sum over the chunk. Padded
+    // tokens have log g = 0 and beta = 0, so they change nothing.
     if (wave == 0) {
         const bool ok = lane < nv;
-        float x = ok ? plg[static_cast<size_t>(t0 + lane) * 32 + h] : 0.0f;
+        const size_t gi = static_cast<size_t>(t0 + lane) * 32 + h;
+        float x = ok ? -expf(a_log[h]) * softplus(a[gi] + dt_bias[h]) : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o, 64);
             if (lane >= o) x += y;
         }
         G[lane] = x;
-        Bt[lane] = ok ? pbeta[static_cast<size_t>(t0 + lane) * 32 + h] : 0.0f;
-        gout[ch * kC + lane] = x;
+        Bt[lane] = ok ? sigmoid(b[gi]) : 0.0f;
+        if (lane == 63) out.gam[ch] = expf(x);
     }
-    // K and Q rows of the key head: thread -> row t/4, dims 32*(t%4) .. +31
-    const int r = t >> 2, d0 = 32 * (t & 3);
+    __syncthreads();
+
+    // q and k of key head kh: thread -> 8 channels (lanes 0-15 of each 32
+    // q, 16-31 k) x tokens 8g .. 8g+7; L2 norm per token over the 16 lanes of
+    // its head (deltanet.metal:282-305), q then / sqrt(128).
     {
-        const float4* ks = reinterpret_cast<const float4*>(pk + (static_cast<size_t>(t0 + r) * 16 + kh) * 128 + d0);
-        const float4* qs = reinterpret_cast<const float4*>(pq + (static_cast<size_t>(t0 + r) * 16 + kh) * 128 + d0);
+        const bool isq = (t & 31) < 16;
+        const int oc = t & 15, g = t >> 5;
+        const int chn = (isq ? 0 : 2048) + kh * 128 + 8 * oc;
+        float y[8][8];
+        conv8_any<IN_DT, 8>(edge, qkv, conv_state, conv_w, chn, t0 + 8 * g, T, y);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float4 kv = r < nv ? ks[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 qv = r < nv ? qs[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            store_split4(Kh, Kl, r * kLD + d0 + 4 * i, kv.x, kv.y, kv.z, kv.w);
-            store_split4(Qh, Ql, r * kLD + d0 + 4 * i, qv.x, qv.y, qv.z, qv.w);
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
+            ss = group_sum<16>(ss);
+            const float inv = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) y[i][k] = isq ? (y[i][k] * inv) * (1.0f / sqrtf(128.0f)) : y[i][k] * inv;
+            const int row = 8 * g + i;
+            store_split8((isq ? Qh : Kh) + row * kLD + 8 * oc, (isq ? Ql : Kl) + row * kLD + 8 * oc, y[i]);
+        }
+        if (!isq) {
+            // K~^T rows 8oc .. 8oc+7, tokens 8g .. 8g+7
+            const float gc = G[kC - 1];
+            float sk[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sk[i] = expf(gc - G[8 * g + i]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = sk[i] * y[i][k];
+                const size_t o = (ch * 128 + 8 * oc + k) * kC + 8 * g;
+                store_split8(out.kth + o, out.ktl + o, x);
+            }
+        }
+    }
+    // beta v of value head h: thread -> 8 channels x tokens 4g .. 4g+3
+    {
+        const int oc = t & 15, g = t >> 4;
+        float y[4][8];
+        conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, 4096 + h * 128 + 8 * oc, t0 + 4 * g, T, y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * g + i;
+            const float bb = Bt[row];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) y[i][k] *= bb;
+            store_split8(Vh + row * kLD + 8 * oc, Vl + row * kLD + 8 * oc, y[i]);
         }
     }
     __syncthreads();
-    {
-        const float b = Bt[r];
-        const float4* vs = reinterpret_cast<const float4*>(pv + (static_cast<size_t>(t0 + r) * 32 + h) * 128 + d0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 vv = r < nv ? vs[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            store_split4(Vh, Vl, r * kLD + d0 + 4 * i, b * vv.x, b * vv.y, b * vv.z, b * vv.w);
-        }
-    }
+
     // K K^T -> A (strictly lower, scaled), Q K^T -> P (lower incl. diagonal)
+    {
+        f32x4_t kk[1][4], qk[1][4];
 #pragma unroll
-    for (int cj = 0; cj < 4; ++cj) {
-        const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const f32x4_t kk = mma_nt_x3<128>(zero, Kh + 16 * wave * kLD, Kl + 16 * wave * kLD, kLD,
-                                          Kh + 16 * cj * kLD, Kl + 16 * cj * kLD, kLD, lane);
-        const f32x4_t qk = mma_nt_x3<128>(zero, Qh + 16 * wave * kLD, Ql + 16 * wave * kLD, kLD,
-                                          Kh + 16 * cj * kLD, Kl + 16 * cj * kLD, kLD, lane);
-        const int j = 16 * cj + n;
+        for (int cj = 0; cj < 4; ++cj) kk[0][cj] = qk[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<128, 1, 4, false>(kk, Kh, Kl, kLD, 16 * wave, Kh, Kl, kLD, 0, lane);
+        mma_block_x3<128, 1, 4, false>(qk, Qh, Ql, kLD, 16 * wave, Kh, Kl, kLD, 0, lane);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const int i = 16 * wave + 4 * kb + ii;
-            const float decay = j <= i ? expf(G[i] - G[j]) : 0.0f;
-            Am[i * 65 + j] = j < i ? Bt[i] * decay * kk[ii] : 0.0f;
-            uint16_t hh, ll;
-            split_bf16(decay * qk[ii], hh, ll);
-            ph[(ch * kC + i) * kC + j] = hh;
-            pl[(ch * kC + i) * kC + j] = ll;
+        for (int cj = 0; cj < 4; ++cj) {
+            const int j = 16 * cj + n;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = 16 * wave + 4 * kb + ii;
+                const float decay = j <= i ? expf(G[i] - G[j]) : 0.0f;
+                Am[i * 65 + j] = j < i ? Bt[i] * decay * kk[0][cj][ii] : 0.0f;
+                uint16_t hh, ll;
+                split_bf16(decay * qk[0][cj][ii], hh, ll);
+                Th[i * kLT + j] = hh;
+                Tl[i * kLT + j] = ll;
+            }
         }
     }
     __syncthreads();
+    // P out, 16 B per thread and piece
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Tl : Th) + row * kLT + c8);
+        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + (ch * kC + row) * kC + c8) = v;
+    }
     // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
     //   diagonal blocks by forward substitution, one wave each;
     //   T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i > j, wave j walking
     //   column block j downwards (fp32 MFMA 16x16x4).
-    float* Tm = reinterpret_cast<float*>(Qh);          // [64][65] fp32 (Q is consumed)
-    float* scr = reinterpret_cast<float*>(Ql) + wave * (16 * 17);
+    float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [64][65] (Q is consumed)
+    float* scr = reinterpret_cast<float*>(smem + kOffQ + kTile128) + wave * (16 * 17);
     {
         const int bi = wave;
         if (lane < 16) {
@@ -161,6 +306,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
+    // T -> bf16 hi/lo; X = beta e^G K in place of K
     for (int idx = t; idx < kC * kC; idx += 256) {
         const int i = idx >> 6, j = idx & 63;
         uint16_t hh, ll;
@@ -168,231 +314,318 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         Th[i * kLT + j] = hh;
         Tl[i * kLT + j] = ll;
     }
-    __syncthreads();
-    // X = beta e^G K into the Q buffers; Q~ = e^G Q and K~ = e^{G_C - G} K to
-    // workspace (split) for the state pass
-    for (int idx = t; idx < kC * 32; idx += 256) {
-        const int rr = idx >> 5, q4 = idx & 31;
-        const float eg = expf(G[rr]);
-        const float sx = Bt[rr] * eg, sk = expf(G[kC - 1] - G[rr]);
-        const size_t src = (static_cast<size_t>(t0 + rr) * 16 + kh) * 128;
-        const float4 kv = rr < nv ? reinterpret_cast<const float4*>(pk + src)[q4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 qv = rr < nv ? reinterpret_cast<const float4*>(pq + src)[q4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        store_split4(Qh, Ql, rr * kLD + 4 * q4, sx * kv.x, sx * kv.y, sx * kv.z, sx * kv.w);
-        const size_t o = (ch * kC + rr) * 128 + 4 * q4;
-        store_split4(qth + o, qtl + o, 0, eg * qv.x, eg * qv.y, eg * qv.z, eg * qv.w);
-        store_split4(kth + o, ktl + o, 0, sk * kv.x, sk * kv.y, sk * kv.z, sk * kv.w);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q = t + 256 * k, row = q >> 4, c8 = 8 * (q & 15);
+        const float s = Bt[row] * expf(G[row]);
+        const u32x4_t hv = *reinterpret_cast<const u32x4_t*>(Kh + row * kLD + c8);
+        const u32x4_t lv = *reinterpret_cast<const u32x4_t*>(Kl + row * kLD + c8);
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = s * (__uint_as_float(hv[e] << 16) + __uint_as_float(lv[e] << 16));
+            x[2 * e + 1] = s * (__uint_as_float(hv[e] & 0xffff0000u) + __uint_as_float(lv[e] & 0xffff0000u));
+        }
+        store_split8(Kh + row * kLD + c8, Kl + row * kLD + c8, x);
     }
     __syncthreads();
-    // W = T X and U~ = T (beta V): wave -> row tile, 8 column tiles of 16 dims
-#pragma unroll 2
-    for (int cd = 0; cd < 8; ++cd) {
-        const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const f32x4_t w = mma_nn_x3<kC>(zero, Th + 16 * wave * kLT, Tl + 16 * wave * kLT, kLT, Qh + 16 * cd,
-                                        Ql + 16 * cd, kLD, lane);
-        const f32x4_t u = mma_nn_x3<kC>(zero, Th + 16 * wave * kLT, Tl + 16 * wave * kLT, kLT, Vh + 16 * cd,
-                                        Vl + 16 * cd, kLD, lane);
-        const int d = 16 * cd + n;
+    // W = T X -> LDS (Q region); U~ = T (beta V) -> U~^T out.
+    // Wave -> row tile (16 tokens), 8 column tiles of 16 dims in two halves.
+    uint16_t* Wh = Qh;
+    uint16_t* Wl = Ql;
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const size_t o = (ch * kC + 16 * wave + 4 * kb + ii) * 128 + d;
-            uint16_t hh, ll;
-            split_bf16(w[ii], hh, ll);
-            wh[o] = hh;
-            wl[o] = ll;
-            split_bf16(u[ii], hh, ll);
-            uh[o] = hh;
-            ul[o] = ll;
+    for (int half = 0; half < 2; ++half) {
+        f32x4_t w[1][4], u[1][4];
+#pragma unroll
+        for (int cd = 0; cd < 4; ++cd) w[0][cd] = u[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * wave, Kh, Kl, kLD, 64 * half, lane);
+        mma_block_x3<kC, 1, 4, true>(u, Th, Tl, kLT, 16 * wave, Vh, Vl, kLD, 64 * half, lane);
+#pragma unroll
+        for (int cd = 0; cd < 4; ++cd) {
+            const int d = 64 * half + 16 * cd + n;
+            uint16_t uh4[4], ul4[4];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = 16 * wave + 4 * kb + ii;
+                uint16_t hh, ll;
+                split_bf16(w[0][cd][ii], hh, ll);
+                Wh[i * kLD + d] = hh;
+                Wl[i * kLD + d] = ll;
+                split_bf16(u[0][cd][ii], uh4[ii], ul4[ii]);
+            }
+            const size_t o = (ch * 128 + d) * kC + 16 * wave + 4 * kb;
+            *reinterpret_cast<u32x2_t*>(out.uth + o) =
+                u32x2_t{uh4[0] | (static_cast<uint32_t>(uh4[1]) << 16), uh4[2] | (static_cast<uint32_t>(uh4[3]) << 16)};
+            *reinterpret_cast<u32x2_t*>(out.utl + o) =
+                u32x2_t{ul4[0] | (static_cast<uint32_t>(ul4[1]) << 16), ul4[2] | (static_cast<uint32_t>(ul4[3]) << 16)};
+        }
+    }
+    __syncthreads();
+    // W out; P back from global into the T region (T is consumed). The same
+    // workgroup wrote P above, and the barriers since make it visible.
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int q = t + 256 * k, arr = q >> 10, row = (q & 1023) >> 4, c8 = 8 * (q & 15);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Wl : Wh) + row * kLD + c8);
+        *reinterpret_cast<u32x4_t*>((arr ? out.wl : out.wh) + (ch * kC + row) * 128 + c8) = v;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
+        *reinterpret_cast<u32x4_t*>((arr ? Tl : Th) + row * kLT + c8) =
+            *reinterpret_cast<const u32x4_t*>((arr ? out.pl : out.ph) + (ch * kC + row) * kC + c8);
+    }
+    __syncthreads();
+    // P W -> fp32 [64][132] in the K region (X is consumed)
+    float* PW = reinterpret_cast<float*>(smem + kOffK);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        f32x4_t pw[1][4];
+#pragma unroll
+        for (int cd = 0; cd < 4; ++cd) pw[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<kC, 1, 4, true>(pw, Th, Tl, kLT, 16 * wave, Wh, Wl, kLD, 64 * half, lane);
+#pragma unroll
+        for (int cd = 0; cd < 4; ++cd)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                PW[(16 * wave + 4 * kb + ii) * 132 + 64 * half + 16 * cd + n] = pw[0][cd][ii];
+    }
+    __syncthreads();
+    // Qe = e^G q - P W with q recomputed (conv + norm): thread -> 8 channels
+    // x tokens 4g .. 4g+3
+    {
+        const int oc = t & 15, g = t >> 4;
+        float y[4][8];
+        conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, kh * 128 + 8 * oc, t0 + 4 * g, T, y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * g + i;
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
+            ss = group_sum<16>(ss);
+            const float inv = 1.0f / sqrtf(ss + 1e-6f);
+            const float eg = expf(G[row]);
+            const float4 p0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc);
+            const float4 p1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc + 4);
+            const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) y[i][k] = eg * ((y[i][k] * inv) * (1.0f / sqrtf(128.0f))) - pw[k];
+            const size_t o = (ch * kC + row) * 128 + 8 * oc;
+            store_split8(out.qeh + o, out.qel + o, y[i]);
         }
     }
 }
 
-// grid (4 row blocks of 32, 32 value heads), 256 threads. Wave w keeps the
-// state tiles (row tile 0/1) x (column tiles 2w, 2w+1) in registers.
-__global__ __launch_bounds__(256) void dn_chunk_state_kernel(
-    int T, const uint16_t* __restrict__ qth, const uint16_t* __restrict__ qtl, const uint16_t* __restrict__ kth,
-    const uint16_t* __restrict__ ktl, const uint16_t* __restrict__ wh, const uint16_t* __restrict__ wl,
-    const uint16_t* __restrict__ uh, const uint16_t* __restrict__ ul, const uint16_t* __restrict__ ph,
-    const uint16_t* __restrict__ pl, const float* __restrict__ gin, float* __restrict__ ssm_state,
-    float* __restrict__ po) {
-    const int rb = blockIdx.x, h = blockIdx.y;
+// ---- sequential state pass ---------------------------------------------------
+
+// One workgroup per (RB-row block of the state, value head), 256 threads;
+// a 1-D grid of 32 * (128 / RB) workgroups. Workgroups are dispatched to the
+// 8 XCDs round-robin by linear id, so the id -> (head, row block) map puts
+// all row blocks of a head on one XCD, whose L2 then serves the chunk
+// inputs they share.
+// Wave w: U^T / O^T columns = tokens 16w .. 16w+15 (all RB rows), state
+// columns 32w .. 32w+31 (all RB rows).
+template <int RB>
+__global__ __launch_bounds__(256) void dn_chunk_state_kernel(int T, qff_dn_bufs in, float* __restrict__ ssm_state,
+                                                             float* __restrict__ po) {
+    constexpr int RT = RB / 16;                // row tiles per block
+    constexpr int NRB = 128 / RB;              // row blocks per head
+    constexpr int HPX = 32 / 8;                // heads per XCD
+    constexpr int LA = 200;                    // [S | U~^T] row stride: 128 + 64 + 8
+    constexpr int NU = RB * 16 / 256;          // 16-B pieces of U~^T per thread
+    const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
+    const int h = xcd * HPX + slot / NRB, rb = slot % NRB;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
 
-    __shared__ __attribute__((aligned(16))) uint16_t Sh[32 * kLD], Sl[32 * kLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Wh[kC * kLD], Wl[kC * kLD];   // W, then O staging
-    __shared__ __attribute__((aligned(16))) uint16_t Qh[kC * kLD], Ql[kC * kLD];   // Q~ = e^G Q
-    __shared__ __attribute__((aligned(16))) uint16_t Kh[kC * kLD], Kl[kC * kLD];   // K~ = e^{G_C - G} K
-    __shared__ __attribute__((aligned(16))) uint16_t Ph[kC * kLT], Pl[kC * kLT];
-    __shared__ __attribute__((aligned(16))) uint16_t Uh[32 * kLT], Ul[32 * kLT];   // U^T rows of this block
-    __shared__ float G[kC];
-    float* Os = reinterpret_cast<float*>(Wh);   // [64][33] fp32, after W is consumed
+    __shared__ __attribute__((aligned(16))) uint16_t Ah[RB * LA], Al[RB * LA];
+    __shared__ __attribute__((aligned(16))) uint16_t Uh[RB * kLT], Ul[RB * kLT];
 
-    float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 32 * rb) * 128;
-    f32x4_t sacc[2][2];
+    float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + RB * rb) * 128;
+    f32x4_t sacc[RT][2];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii)
-                sacc[rt][cc][ii] = Sg[(16 * rt + 4 * kb + ii) * 128 + 16 * (2 * wave + cc) + n];
+                sacc[r][cc][ii] = Sg[(16 * r + 4 * kb + ii) * 128 + 32 * wave + 16 * cc + n];
 
     const int nch = (T + kC - 1) / kC;
-    // Chunk inputs travel global -> registers -> LDS; the registers for chunk
-    // c+1 are loaded while chunk c computes. Per thread: 4 x 16 B of each of
-    // W, Q~, K~ (hi and lo), 2 x 16 B of P hi and lo, and the 16 U~ values
-    // (hi, lo) its Y1 outputs need.
-    u32x4_t pre[6][4], prep_[2][2];
-    uint16_t preu[2][2][4][2];
-    float preg = 0.0f;
-    auto fetch = [&](int c) {
+    // B operands, one chunk ahead: W and Qe rows 16w + n (k = d), P row
+    // 16w + n (k = j), K~^T rows 32w + 16ct + n (k = i); and this thread's
+    // pieces of the block's U~^T rows.
+    u32x4_t wr[4][2], qr[4][2], pr[2][2], kr[2][2][2], ur[NU];
+    float gam = 0.0f;
+    auto fetch_u = [&](int c) {
         const size_t ch = static_cast<size_t>(c) * 32 + h;
-        // the small loads first: vmcnt retires in issue order, so consuming
-        // them early must not wait on the bulk copies behind them
-        const int rt = wave & 1;
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int i = 16 * (2 * (wave >> 1) + cc) + n;
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const size_t gu = (ch * kC + i) * 128 + 32 * rb + 16 * rt + 4 * kb + ii;
-                preu[cc][0][ii][0] = uh[gu];
-                preu[cc][0][ii][1] = ul[gu];
-            }
+        for (int j = 0; j < NU; ++j) {
+            const int q = t + 256 * j, arr = q / (RB * 8), rem = q % (RB * 8);
+            ur[j] = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) + (ch * 128 + RB * rb + (rem >> 3)) * kC +
+                                                      8 * (rem & 7));
         }
-        if (t < kC) preg = gin[ch * kC + t];
-        const size_t o = ch * kC * 128;
-        const uint16_t* srcs[6] = {wh + o, wl + o, qth + o, qtl + o, kth + o, ktl + o};
+        gam = in.gam[ch];
+    };
+    auto fetch_wqp = [&](int c) {
+        const size_t ch = static_cast<size_t>(c) * 32 + h;
+        const size_t ow = (ch * kC + 16 * wave + n) * 128 + 8 * kb;
 #pragma unroll
-        for (int a = 0; a < 6; ++a)
+        for (int ks = 0; ks < 4; ++ks) {
+            wr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.wh + ow + 32 * ks);
+            wr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.wl + ow + 32 * ks);
+            qr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.qeh + ow + 32 * ks);
+            qr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.qel + ow + 32 * ks);
+        }
+        const size_t op = (ch * kC + 16 * wave + n) * kC + 8 * kb;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pre[a][i] = reinterpret_cast<const u32x4_t*>(srcs[a])[t + 256 * i];
-        const u32x4_t* gp_h = reinterpret_cast<const u32x4_t*>(ph + ch * kC * kC);
-        const u32x4_t* gp_l = reinterpret_cast<const u32x4_t*>(pl + ch * kC * kC);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            prep_[0][i] = gp_h[t + 256 * i];
-            prep_[1][i] = gp_l[t + 256 * i];
+        for (int ks = 0; ks < 2; ++ks) {
+            pr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.ph + op + 32 * ks);
+            pr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.pl + op + 32 * ks);
         }
     };
-    fetch(0);
+    auto fetch_k = [&](int c) {
+        const size_t ch = static_cast<size_t>(c) * 32 + h;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const size_t ok = (ch * 128 + 32 * wave + 16 * ct + n) * kC + 8 * kb;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                kr[ct][ks][0] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 32 * ks);
+                kr[ct][ks][1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 32 * ks);
+            }
+        }
+    };
+    fetch_u(0);
+    fetch_wqp(0);
+    fetch_k(0);
     for (int c = 0; c < nch; ++c) {
-        const int t0 = c * kC;
-        const int nv = min(kC, T - t0);
-        // registers -> LDS
-        {
-            uint16_t* dst[6] = {Wh, Wl, Qh, Ql, Kh, Kl};
+        // [S | U~^T] -> LDS
 #pragma unroll
-            for (int a = 0; a < 6; ++a)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int q = t + 256 * i;
-                    *reinterpret_cast<u32x4_t*>(&dst[a][(q >> 4) * kLD + 8 * (q & 15)]) = pre[a][i];
-                }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int q = t + 256 * i;
-                *reinterpret_cast<u32x4_t*>(&Ph[(q >> 3) * kLT + 8 * (q & 7)]) = prep_[0][i];
-                *reinterpret_cast<u32x4_t*>(&Pl[(q >> 3) * kLT + 8 * (q & 7)]) = prep_[1][i];
-            }
-            if (t < kC) G[t] = preg;
-        }
-        float ucur[2][4];
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                ucur[cc][ii] = bf16_to_f32(preu[cc][0][ii][0]) + bf16_to_f32(preu[cc][0][ii][1]);
-        // state -> LDS as the A operand (rows of this block)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int r = 0; r < RT; ++r)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
                     uint16_t hh, ll;
-                    split_bf16(sacc[rt][cc][ii], hh, ll);
-                    const int o = (16 * rt + 4 * kb + ii) * kLD + 16 * (2 * wave + cc) + n;
-                    Sh[o] = hh;
-                    Sl[o] = ll;
+                    split_bf16(sacc[r][cc][ii], hh, ll);
+                    const int o = (16 * r + 4 * kb + ii) * LA + 32 * wave + 16 * cc + n;
+                    Ah[o] = hh;
+                    Al[o] = ll;
                 }
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int q = t + 256 * j, arr = q / (RB * 8), rem = q % (RB * 8);
+            *reinterpret_cast<u32x4_t*>((arr ? Al : Ah) + (rem >> 3) * LA + 128 + 8 * (rem & 7)) = ur[j];
+        }
+        const float g = gam;
+        // The next chunk's loads are issued unconditionally (the last
+        // iteration re-reads its own chunk) and so are the output stores
+        // (the output buffer holds whole chunks): with no branch around a
+        // memory instruction the compiler's vmcnt bookkeeping stays exact and
+        // each wait covers only the loads it needs.
+        const int cn = min(c + 1, nch - 1);
         __syncthreads();
-        if (c + 1 < nch) fetch(c + 1);
-        const float gamma = expf(G[kC - 1]);
-        // U^T[r][i] = U~[i][r] - sum_d S[r][d] W[i][d]: wave -> row tile w&1,
-        // token tiles 2(w>>1), +1
-        const int rt = wave & 1, ci0 = 2 * (wave >> 1);
-        {
-            f32x4_t sw[1][2] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}}};
-            mma_block_x3<128, 1, 2, false>(sw, Sh, Sl, kLD, 16 * rt, Wh, Wl, kLD, 16 * ci0, lane);
+        fetch_u(cn);
+        // U^T acc = S W^T (k = d, 4 steps), O^T = S Qe^T + U~^T P^T (6 steps)
+        f32x4_t au[RT], ao[RT];
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const int i = 16 * (ci0 + cc) + n;
+        for (int r = 0; r < RT; ++r) au[r] = ao[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    const int rr = 16 * rt + 4 * kb + ii;
-                    uint16_t hh, ll;
-                    split_bf16(ucur[cc][ii] - sw[0][cc][ii], hh, ll);
-                    Uh[rr * kLT + i] = hh;
-                    Ul[rr * kLT + i] = ll;
+        for (int ks = 0; ks < 6; ++ks) {
+            u32x4_t a_h[RT], a_l[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                a_h[r] = *reinterpret_cast<const u32x4_t*>(Ah + (16 * r + n) * LA + 32 * ks + 8 * kb);
+                a_l[r] = *reinterpret_cast<const u32x4_t*>(Al + (16 * r + n) * LA + 32 * ks + 8 * kb);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                if (ks < 4) {
+                    au[r] = mfma_16x16x32_bf16(a_l[r], wr[ks][0], au[r]);
+                    au[r] = mfma_16x16x32_bf16(a_h[r], wr[ks][1], au[r]);
+                    au[r] = mfma_16x16x32_bf16(a_h[r], wr[ks][0], au[r]);
+                    ao[r] = mfma_16x16x32_bf16(a_l[r], qr[ks][0], ao[r]);
+                    ao[r] = mfma_16x16x32_bf16(a_h[r], qr[ks][1], ao[r]);
+                    ao[r] = mfma_16x16x32_bf16(a_h[r], qr[ks][0], ao[r]);
+                } else {
+                    ao[r] = mfma_16x16x32_bf16(a_l[r], pr[ks - 4][0], ao[r]);
+                    ao[r] = mfma_16x16x32_bf16(a_h[r], pr[ks - 4][1], ao[r]);
+                    ao[r] = mfma_16x16x32_bf16(a_h[r], pr[ks - 4][0], ao[r]);
                 }
             }
         }
-        __syncthreads();
-        // O^T[r][i] = sum_d S[r][d] Q~[i][d] + sum_j U^T[r][j] P[i][j]
-        {
-            f32x4_t o[1][2] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}}};
-            mma_block_x3<128, 1, 2, false>(o, Sh, Sl, kLD, 16 * rt, Qh, Ql, kLD, 16 * ci0, lane);
-            mma_block_x3<kC, 1, 2, false>(o, Uh, Ul, kLT, 16 * rt, Ph, Pl, kLT, 16 * ci0, lane);
+        fetch_wqp(cn);
+        // U^T = U~^T - S W^T -> LDS; O^T -> pre-norm output (token-major)
+        const int i = 16 * wave + n;
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const int i = 16 * (ci0 + cc) + n;
+        for (int r = 0; r < RT; ++r) {
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) Os[i * 33 + 16 * rt + 4 * kb + ii] = o[0][cc][ii];
+            for (int ii = 0; ii < 4; ++ii) {
+                const int row = 16 * r + 4 * kb + ii;
+                const float ut = bf16_to_f32(Ah[row * LA + 128 + i]) + bf16_to_f32(Al[row * LA + 128 + i]) - au[r][ii];
+                uint16_t hh, ll;
+                split_bf16(ut, hh, ll);
+                Uh[row * kLT + i] = hh;
+                Ul[row * kLT + i] = ll;
             }
+            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + i) * 4096 + h * 128 + RB * rb + 16 * r +
+                                        4 * kb) = ao[r];
         }
         __syncthreads();
-        // pre-norm outputs of this block's 32 rows, token-major
-        {
-            const int i = t >> 2, r8 = 8 * (t & 3);
-            if (i < nv) {
-                float* dst = po + static_cast<size_t>(t0 + i) * 4096 + h * 128 + 32 * rb + r8;
+        // S = e^{G_C} S + U^T K~ (k = token, 2 steps)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) dst[e] = Os[i * 33 + r8 + e];
-            }
-        }
-        // S = e^{G_C} S + U^T K~
-#pragma unroll
-        for (int rt2 = 0; rt2 < 2; ++rt2)
+        for (int r = 0; r < RT; ++r)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) sacc[rt2][cc][ii] *= gamma;
-        mma_block_x3<kC, 2, 2, true>(sacc, Uh, Ul, kLT, 0, Kh, Kl, kLD, 32 * wave, lane);
-        __syncthreads();
+                for (int ii = 0; ii < 4; ++ii) sacc[r][cc][ii] *= g;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            u32x4_t a_h[RT], a_l[RT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                a_h[r] = *reinterpret_cast<const u32x4_t*>(Uh + (16 * r + n) * kLT + 32 * ks + 8 * kb);
+                a_l[r] = *reinterpret_cast<const u32x4_t*>(Ul + (16 * r + n) * kLT + 32 * ks + 8 * kb);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    sacc[r][ct] = mfma_16x16x32_bf16(a_l[r], kr[ct][ks][0], sacc[r][ct]);
+                    sacc[r][ct] = mfma_16x16x32_bf16(a_h[r], kr[ct][ks][1], sacc[r][ct]);
+                    sacc[r][ct] = mfma_16x16x32_bf16(a_h[r], kr[ct][ks][0], sacc[r][ct]);
+                }
+        }
+        fetch_k(cn);
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii)
-                Sg[(16 * rt + 4 * kb + ii) * 128 + 16 * (2 * wave + cc) + n] = sacc[rt][cc][ii];
+                Sg[(16 * r + 4 * kb + ii) * 128 + 32 * wave + 16 * cc + n] = sacc[r][cc][ii];
 }
 
-hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, int T, float* ssm_state) {
+hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
+                                   const void* qkv, qff_dtype in_dtype, const float* a, const float* b,
+                                   const float* conv_state, float* ssm_state, int T) {
     const int nch = (T + kC - 1) / kC;
     {
         ProfScope prof(ctx, stream, "dn_chunk_local");
-        dn_chunk_local_kernel<<<dim3(nch, 32), 256, 0, stream>>>(
-            T, ctx->pf_q, ctx->pf_k, ctx->pf_v, ctx->pf_g, ctx->pf_beta, ctx->pf_wh, ctx->pf_wl, ctx->pf_uh,
-            ctx->pf_ul, ctx->pf_ph, ctx->pf_pl, ctx->pf_G, ctx->pf_qth, ctx->pf_qtl, ctx->pf_kth, ctx->pf_ktl);
+        const dim3 grid(nch, 32);
+        if (in_dtype == QFF_BF16)
+            dn_chunk_local_kernel<1><<<grid, 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
+                                                               conv_state, ctx->dn);
+        else
+            dn_chunk_local_kernel<0><<<grid, 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
+                                                               conv_state, ctx->dn);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
-    dn_chunk_state_kernel<<<dim3(4, 32), 256, 0, stream>>>(T, ctx->pf_qth, ctx->pf_qtl, ctx->pf_kth, ctx->pf_ktl,
-                                                           ctx->pf_wh, ctx->pf_wl, ctx->pf_uh, ctx->pf_ul, ctx->pf_ph,
-                                                           ctx->pf_pl, ctx->pf_G, ssm_state, ctx->pf_o);
+    constexpr int kRB = QFF_DN_STATE_RB;
+    dn_chunk_state_kernel<kRB><<<32 * (128 / kRB), 256, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);
     return hipGetLastError();
 }
 

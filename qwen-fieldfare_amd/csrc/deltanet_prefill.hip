@@ -4,16 +4,14 @@
 // The reference has no prefill kernel: prompts go token by token through the
 // decode path (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561). This file
 // computes the same result for a whole sequence:
-//   prep       conv1d + SiLU over time for all 8192 channels (each token only
-//              needs the 3 previous inputs, so tokens run in parallel), L2
-//              norms of q (then / sqrt(128)) and k per key head, and the
-//              per-token log gate and beta of every value head;
-//   chunked    the chunked WY form of the gated delta rule
-//              (deltanet_chunked.hip), pre-norm outputs to workspace;
+//   chunked    conv1d + SiLU, L2 norms, gates and the chunked WY form of the
+//              gated delta rule (deltanet_chunked.hip), pre-norm outputs to
+//              workspace;
 //   norm       gated RMSNorm of every (token, value head) output row;
 //   conv state the conv state after the last token.
 #include "common.hpp"
 #include "internal.hpp"
+#include "mfma.hpp"
 
 namespace qff {
 
@@ -24,70 +22,36 @@ __device__ __forceinline__ float conv_ext(const float* __restrict__ conv_state, 
     return i < 4 ? conv_state[c * 4 + i] : elem<IN_DT>::load(qkv, static_cast<size_t>(i - 4) * 8192 + c);
 }
 
-constexpr int kPrepTokens = 16;   // tokens per prep workgroup
-
-// grid (ceil(T/16), 32 channel blocks of 256), 256 threads: thread = channel,
-// walking 16 tokens with a sliding 4-tap window (one new input per token).
-// Channel blocks 0-7 hold q (two key heads each), 8-15 k, 16-31 v. Block 0
-// also forms the 16 tokens' log gates and betas.
-template <int IN_DT>
-__global__ __launch_bounds__(256) void dn_prefill_prep_kernel(
-    int T, const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
-    const float* __restrict__ a_log, const float* __restrict__ dt_bias, const float* __restrict__ conv_w,
-    const float* __restrict__ conv_state, float* __restrict__ pq, float* __restrict__ pk,
-    float* __restrict__ pv, float* __restrict__ plg, float* __restrict__ pbeta) {
-    __shared__ float red[kPrepTokens][4];
-    const int tb = blockIdx.x * kPrepTokens, blk = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int c = blk * 256 + t;
-    const int nt = min(kPrepTokens, T - tb);
-    const float4 w = reinterpret_cast<const float4*>(conv_w)[c];
-    // token tok uses e[tok+1 .. tok+4] (deltanet.metal:120-137 after the shift)
-    float e1 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 1);
-    float e2 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 2);
-    float e3 = conv_ext<IN_DT>(conv_state, qkv, c, tb + 3);
-    float y[kPrepTokens];
+// grid (T), 256 threads: thread -> value head t/8, rows 16*(t%8) .. +15.
+// 8 consecutive elements of a dtype-DT row in one or two 16-B accesses.
+template <int DT> __device__ __forceinline__ void load8(const void* p, size_t i, float (&x)[8]) {
+    if (DT == 1) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
 #pragma unroll
-    for (int i = 0; i < kPrepTokens; ++i) {
-        const float e4 = i < nt ? elem<IN_DT>::load(qkv, static_cast<size_t>(tb + i) * 8192 + c) : 0.0f;
-        y[i] = silu(e1 * w.x + e2 * w.y + e3 * w.z + e4 * w.w);
-        e1 = e2; e2 = e3; e3 = e4;
-    }
-    if (blk < 16) {
-        // L2 norm per key head: waves 0-1 one head, waves 2-3 the other
-#pragma unroll
-        for (int i = 0; i < kPrepTokens; ++i) {
-            const float ss = group_sum<64>(y[i] * y[i]);
-            if (lane == 0) red[i][wave] = ss;
-        }
-        __syncthreads();
-        const int hw = wave & 2;
-        float* dst = blk < 8 ? pq : pk;
-        const int cc = blk < 8 ? c : c - 2048;
-#pragma unroll
-        for (int i = 0; i < kPrepTokens; ++i) {
-            if (i >= nt) break;
-            const float inv = 1.0f / sqrtf(red[i][hw] + red[i][hw + 1] + 1e-6f);
-            const float v = blk < 8 ? (y[i] * inv) * (1.0f / sqrtf(128.0f)) : y[i] * inv;
-            dst[static_cast<size_t>(tb + i) * 2048 + cc] = v;
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = __uint_as_float(v[k] << 16);
+            x[2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
         }
     } else {
-#pragma unroll
-        for (int i = 0; i < kPrepTokens; ++i) {
-            if (i >= nt) break;
-            pv[static_cast<size_t>(tb + i) * 4096 + (c - 4096)] = y[i];
-        }
+        const float4 a = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i)[0];
+        const float4 b = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i)[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     }
-    if (blk == 0) {
-        for (int idx = t; idx < nt * 32; idx += 256) {
-            const int hh = idx & 31;
-            const size_t gi = static_cast<size_t>(tb) * 32 + idx;
-            plg[gi] = -expf(a_log[hh]) * softplus(a[gi] + dt_bias[hh]);   // log g
-            pbeta[gi] = sigmoid(b[gi]);
-        }
+}
+template <int DT> __device__ __forceinline__ void store8(void* p, size_t i, const float (&x)[8]) {
+    if (DT == 1) {
+        u32x4_t v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v[k] = static_cast<uint32_t>(f32_to_bf16(x[2 * k])) | (static_cast<uint32_t>(f32_to_bf16(x[2 * k + 1])) << 16);
+        *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + i) = v;
+    } else {
+        reinterpret_cast<float4*>(static_cast<float*>(p) + i)[0] = make_float4(x[0], x[1], x[2], x[3]);
+        reinterpret_cast<float4*>(static_cast<float*>(p) + i)[1] = make_float4(x[4], x[5], x[6], x[7]);
     }
 }
 
+// Gated RMSNorm (QwenDeltaNetKernel.swift:127-151) of the pre-norm outputs.
 // grid (T), 256 threads: thread -> value head t/8, rows 16*(t%8) .. +15.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __restrict__ po,
@@ -97,20 +61,24 @@ __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __res
     const int tok = blockIdx.x, t = threadIdx.x;
     const int r0 = 16 * (t & 7);
     const size_t base = static_cast<size_t>(tok) * 4096 + (t >> 3) * 128 + r0;
-    const float4* src = reinterpret_cast<const float4*>(po + base);
-    float o[16], ss = 0.0f;
+    float o[2][8], zz[2][8], ss = 0.0f;
+    load8<0>(po, base, o[0]);
+    load8<0>(po, base + 8, o[1]);
+    load8<IN_DT>(z, base, zz[0]);
+    load8<IN_DT>(z, base + 8, zz[1]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 v = src[i];
-        o[4 * i] = v.x; o[4 * i + 1] = v.y; o[4 * i + 2] = v.z; o[4 * i + 3] = v.w;
-    }
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ss += o[i] * o[i];
+        for (int i = 0; i < 8; ++i) ss += o[h][i] * o[h][i];
     ss = group_sum<8>(ss);
     const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        elem<OUT_DT>::store(out, base + i, o[i] * inv * norm_w[r0 + i] * silu(elem<IN_DT>::load(z, base + i)));
+    for (int h = 0; h < 2; ++h) {
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = o[h][i] * inv * norm_w[r0 + 8 * h + i] * silu(zz[h][i]);
+        store8<OUT_DT>(out, base + 8 * h, y);
+    }
 }
 
 // conv state after the last token: slots = e[T .. T+3]. grid 32 x 256.
@@ -131,18 +99,7 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
                                    float* ssm_state, void* out, qff_dtype out_dtype, int T) {
     const bool bf = in_dtype == QFF_BF16;
     {
-    ProfScope prof(ctx, stream, "dn_prefill_prep");
-    if (bf)
-        dn_prefill_prep_kernel<1><<<dim3((T + kPrepTokens - 1) / kPrepTokens, 32), 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
-                                                                  conv_state, ctx->pf_q, ctx->pf_k, ctx->pf_v,
-                                                                  ctx->pf_g, ctx->pf_beta);
-    else
-        dn_prefill_prep_kernel<0><<<dim3((T + kPrepTokens - 1) / kPrepTokens, 32), 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
-                                                                  conv_state, ctx->pf_q, ctx->pf_k, ctx->pf_v,
-                                                                  ctx->pf_g, ctx->pf_beta);
-    }
-    {
-        hipError_t e = launch_deltanet_chunked(ctx, stream, T, ssm_state);
+        hipError_t e = launch_deltanet_chunked(ctx, stream, p, qkv, in_dtype, a, b, conv_state, ssm_state, T);
         if (e != hipSuccess) return e;
     }
     const dim3 ng(T);

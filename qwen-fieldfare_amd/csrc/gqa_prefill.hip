@@ -255,7 +255,7 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
                               void* k_cache, void* v_cache, int start_pos, void* out,
                               qff_dtype out_dtype, int T, int) {
     // the bf16 q rows [T][16][256] reuse the DeltaNet prefill staging buffer
-    uint16_t* qb = reinterpret_cast<uint16_t*>(ctx->pf_q);
+    uint16_t* qb = ctx->gqa_qb;
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     const RopeFreqs rf = rope_freqs(p->rope_theta);

@@ -15,6 +15,17 @@ struct qff_prof_record {
     hipEvent_t start, stop;
 };
 
+// Chunked DeltaNet prefill intermediates, one block per (chunk, value head),
+// each array split into bf16 hi / lo halves.
+struct qff_dn_bufs {
+    uint16_t *wh, *wl;      // W [64][128]
+    uint16_t *qeh, *qel;    // Qe = e^G Q - P W [64][128]
+    uint16_t *kth, *ktl;    // K~^T = (e^{G_C - G} K)^T [128][64]
+    uint16_t *uth, *utl;    // U~^T [128][64]
+    uint16_t *ph, *pl;      // P [64][64]
+    float* gam;             // e^{G_C}
+};
+
 struct qff_ctx {
     int device = 0;
     qff_ctx_cfg cfg{};
@@ -25,26 +36,12 @@ struct qff_ctx {
     float* gqa_m = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8]
     float* gqa_d = nullptr;       // same
     float* gqa_o = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8 * 256]
-    // Prefill staging (DeltaNet): per-token prepared q, k, v, gates.
-    float* pf_q = nullptr;        // [T * 16 * 128]
-    float* pf_k = nullptr;        // [T * 16 * 128]
-    float* pf_v = nullptr;        // [T * 32 * 128]
-    float* pf_g = nullptr;        // [T * 32] log gate
-    float* pf_beta = nullptr;     // [T * 32]
-    float* pf_o = nullptr;        // [T * 32 * 128] pre-norm output
-    // Chunked DeltaNet prefill: per (chunk, value head) W, U~ [64][128] and
-    // P [64][64] as bf16 hi/lo pairs, and the cumulative log gates G [64].
-    uint16_t* pf_wh = nullptr;
-    uint16_t* pf_wl = nullptr;
-    uint16_t* pf_uh = nullptr;
-    uint16_t* pf_ul = nullptr;
-    uint16_t* pf_ph = nullptr;
-    uint16_t* pf_pl = nullptr;
-    uint16_t* pf_qth = nullptr;   // Q~ [64][128] per (chunk, value head)
-    uint16_t* pf_qtl = nullptr;
-    uint16_t* pf_kth = nullptr;   // K~ [64][128] per (chunk, value head)
-    uint16_t* pf_ktl = nullptr;
-    float* pf_G = nullptr;
+    // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
+    uint16_t* gqa_qb = nullptr;
+    // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
+    // chunk intermediates.
+    float* pf_o = nullptr;
+    qff_dn_bufs dn{};
     // Kernel timing (qff_profile_enable): a pool of event pairs.
     bool prof = false;
     std::vector<qff_prof_record> prof_pool;
@@ -57,7 +54,7 @@ constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t pf_q, pf_k, pf_v, pf_g, pf_beta, pf_o, pf_wh, pf_wl, pf_uh, pf_ul, pf_ph, pf_pl, pf_qth, pf_qtl, pf_kth, pf_ktl, pf_G;
+    size_t gqa_qb, pf_o, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
@@ -103,7 +100,9 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
                                    const void* qkv, const void* z, qff_dtype in_dtype,
                                    const float* a, const float* b, float* conv_state,
                                    float* ssm_state, void* out, qff_dtype out_dtype, int T);
-hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, int T, float* ssm_state);
+hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
+                                   const void* qkv, qff_dtype in_dtype, const float* a, const float* b,
+                                   const float* conv_state, float* ssm_state, int T);
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
                              const void* q_gate, const void* k_new, const void* v_new,
                              qff_dtype in_dtype, void* k_cache, void* v_cache,

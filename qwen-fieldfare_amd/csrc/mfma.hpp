@@ -43,27 +43,30 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2_t, v);
 }
 
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32);
+// the low half holds lo.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // fp32 -> (hi, lo) bf16 pair with hi + lo == x to ~2^-16 relative: the
 // operands of the three-product "bf16x3" MFMA scheme
 //   a b ~= a_hi b_hi + a_hi b_lo + a_lo b_hi
 // which keeps fp32-class accuracy (~2^-16 relative per product) on the
 // bf16 matrix cores. Inputs are finite.
 __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-    uint32_t u = __float_as_uint(x);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    hi = static_cast<uint16_t>(u >> 16);
-    const float r = x - __uint_as_float(static_cast<uint32_t>(hi) << 16);
-    uint32_t v = __float_as_uint(r);
-    v += 0x7fffu + ((v >> 16) & 1u);
-    lo = static_cast<uint16_t>(v >> 16);
+    const uint32_t h = pack_bf16x2(x, 0.0f);
+    const float r = x - __uint_as_float(h << 16);
+    hi = static_cast<uint16_t>(h);
+    lo = static_cast<uint16_t>(pack_bf16x2(r, 0.0f));
 }
 
-// Two floats -> packed bf16 pair (round to nearest even), low half = lo.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    uint32_t a = __float_as_uint(lo), b = __float_as_uint(hi);
-    a += 0x7fffu + ((a >> 16) & 1u);
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (a >> 16) | (b & 0xffff0000u);
+// Two floats at once: packed hi pair and packed lo pair.
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16x2(x0, x1);
+    lo = pack_bf16x2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
 }
 
 }  // namespace qff
@@ -178,10 +181,11 @@ __device__ __forceinline__ void mma_block_x3(f32x4_t (&acc)[MR][NC], const uint1
 
 // Store 4 fp32 values as hi/lo bf16 at hi[i..i+3], lo[i..i+3] (8-byte aligned).
 __device__ __forceinline__ void store_split4(uint16_t* hi, uint16_t* lo, int i, float a, float b, float c, float d) {
-    uint16_t h0, h1, h2, h3, l0, l1, l2, l3;
-    split_bf16(a, h0, l0); split_bf16(b, h1, l1); split_bf16(c, h2, l2); split_bf16(d, h3, l3);
-    *reinterpret_cast<u32x2_t*>(hi + i) = u32x2_t{h0 | (static_cast<uint32_t>(h1) << 16), h2 | (static_cast<uint32_t>(h3) << 16)};
-    *reinterpret_cast<u32x2_t*>(lo + i) = u32x2_t{l0 | (static_cast<uint32_t>(l1) << 16), l2 | (static_cast<uint32_t>(l3) << 16)};
+    uint32_t h0, l0, h1, l1;
+    split_bf16x2(a, b, h0, l0);
+    split_bf16x2(c, d, h1, l1);
+    *reinterpret_cast<u32x2_t*>(hi + i) = u32x2_t{h0, h1};
+    *reinterpret_cast<u32x2_t*>(lo + i) = u32x2_t{l0, l1};
 }
 
 }  // namespace qff
