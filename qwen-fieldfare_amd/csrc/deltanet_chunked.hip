@@ -43,9 +43,6 @@ namespace qff {
 constexpr int kC = 64;      // chunk length
 constexpr int kLD = 136;    // bf16 row stride of [64][128] LDS tiles (128 + 8)
 constexpr int kLT = 72;     // bf16 row stride of [64][64] LDS tiles (64 + 8)
-#ifndef QFF_DN_STATE_RB
-#define QFF_DN_STATE_RB 16
-#endif
 
 // ---- chunk-local pass --------------------------------------------------------
 
@@ -123,6 +120,17 @@ __device__ __forceinline__ void store_split8(uint16_t* hi, uint16_t* lo, const f
     for (int k = 0; k < 4; ++k) split_bf16x2(x[2 * k], x[2 * k + 1], hw[k], lw[k]);
     *reinterpret_cast<u32x4_t*>(hi) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
     *reinterpret_cast<u32x4_t*>(lo) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+}
+
+// Operand-order layout of a row-major [rows][K] bf16 matrix that is read as
+// 16x16x32 MFMA operand tiles (row r of a tile in lane r % 16, k = 8 k8 ..
+// 8 k8 + 7 in lane group k8 % 4): the 8 elements (r, 8 k8 .. 8 k8 + 7) sit at
+// element offset 8 * swz<K>(r, k8), so the 64 lanes' pieces of each (row
+// tile, k step) are one contiguous 1 KB block and a wave's operand load is
+// fully coalesced.
+template <int K>
+__device__ __forceinline__ int swz(int r, int k8) {
+    return ((r >> 4) * (K / 32) + (k8 >> 2)) * 64 + (k8 & 3) * 16 + (r & 15);
 }
 
 // LDS carve-up of the chunk-local kernel (bytes)
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
                 float x[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) x[i] = sk[i] * y[i][k];
-                const size_t o = (ch * 128 + 8 * oc + k) * kC + 8 * g;
+                const size_t o = ch * 128 * kC + 8 * swz<kC>(8 * oc + k, g);
                 store_split8(out.kth + o, out.ktl + o, x);
             }
         }
@@ -261,7 +269,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
     for (int k = 0; k < 4; ++k) {
         const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Tl : Th) + row * kLT + c8);
-        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + (ch * kC + row) * kC + c8) = v;
+        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7)) = v;
     }
     // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
     //   diagonal blocks by forward substitution, one wave each;
@@ -367,13 +375,13 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
     for (int k = 0; k < 8; ++k) {
         const int q = t + 256 * k, arr = q >> 10, row = (q & 1023) >> 4, c8 = 8 * (q & 15);
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Wl : Wh) + row * kLD + c8);
-        *reinterpret_cast<u32x4_t*>((arr ? out.wl : out.wh) + (ch * kC + row) * 128 + c8) = v;
+        *reinterpret_cast<u32x4_t*>((arr ? out.wl : out.wh) + ch * kC * 128 + 8 * swz<128>(row, q & 15)) = v;
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
         *reinterpret_cast<u32x4_t*>((arr ? Tl : Th) + row * kLT + c8) =
-            *reinterpret_cast<const u32x4_t*>((arr ? out.pl : out.ph) + (ch * kC + row) * kC + c8);
+            *reinterpret_cast<const u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7));
     }
     __syncthreads();
     // P W -> fp32 [64][132] in the K region (X is consumed)
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
             const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
             for (int k = 0; k < 8; ++k) y[i][k] = eg * ((y[i][k] * inv) * (1.0f / sqrtf(128.0f))) - pw[k];
-            const size_t o = (ch * kC + row) * 128 + 8 * oc;
+            const size_t o = ch * kC * 128 + 8 * swz<128>(row, oc);
             store_split8(out.qeh + o, out.qel + o, y[i]);
         }
     }
@@ -419,194 +427,167 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
 
 // ---- sequential state pass ---------------------------------------------------
 
-// One workgroup per (RB-row block of the state, value head), 256 threads;
-// a 1-D grid of 32 * (128 / RB) workgroups. Workgroups are dispatched to the
-// 8 XCDs round-robin by linear id, so the id -> (head, row block) map puts
-// all row blocks of a head on one XCD, whose L2 then serves the chunk
-// inputs they share.
-// Wave w: U^T / O^T columns = tokens 16w .. 16w+15 (all RB rows), state
-// columns 32w .. 32w+31 (all RB rows).
-template <int RB>
-__global__ __launch_bounds__(256) void dn_chunk_state_kernel(int T, qff_dn_bufs in, float* __restrict__ ssm_state,
-                                                             float* __restrict__ po) {
-    constexpr int RT = RB / 16;                // row tiles per block
-    constexpr int NRB = 128 / RB;              // row blocks per head
-    constexpr int HPX = 32 / 8;                // heads per XCD
-    constexpr int LA = 200;                    // [S | U~^T] row stride: 128 + 64 + 8
-    constexpr int NU = RB * 16 / 256;          // 16-B pieces of U~^T per thread
+// One workgroup per (16-row block of the state, value head), 512 threads; a
+// 1-D grid of 256 workgroups. Workgroups are dispatched to the 8 XCDs
+// round-robin by linear id, so the id -> (head, row block) map puts all row
+// blocks of a head on one XCD, whose L2 then serves the chunk inputs they
+// share.
+// Waves 0-3 form U^T for tokens 16w .. 16w+15, waves 4-7 O^T for tokens
+// 16(w-4) .. +15; wave w keeps state columns 16w .. 16w+15. Two waves per
+// SIMD, each with short MFMA chains, so one wave's LDS and MFMA latencies
+// overlap the other's work.
+constexpr int kStateThreads = 512;
+constexpr int kLA = 200;   // [S | U~^T] row stride: 128 + 64 + 8
+
+__global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
+                                                                      float* __restrict__ ssm_state,
+                                                                      float* __restrict__ po) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
-    const int h = xcd * HPX + slot / NRB, rb = slot % NRB;
+    const int h = xcd * 4 + (slot >> 3), rb = slot & 7;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
+    const bool owave = wave >= 4;          // wave-uniform role
+    const int tt = wave & 3;               // token tile of U^T / O^T
 
-    __shared__ __attribute__((aligned(16))) uint16_t Ah[RB * LA], Al[RB * LA];
-    __shared__ __attribute__((aligned(16))) uint16_t Uh[RB * kLT], Ul[RB * kLT];
+    __shared__ __attribute__((aligned(16))) uint16_t Ah[16 * kLA], Al[16 * kLA];
+    __shared__ __attribute__((aligned(16))) uint16_t Uh[16 * kLT], Ul[16 * kLT];
 
-    float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + RB * rb) * 128;
-    f32x4_t sacc[RT][2];
+    float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * rb) * 128;
+    f32x4_t sacc;
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                sacc[r][cc][ii] = Sg[(16 * r + 4 * kb + ii) * 128 + 32 * wave + 16 * cc + n];
+    for (int ii = 0; ii < 4; ++ii) sacc[ii] = Sg[(4 * kb + ii) * 128 + 16 * wave + n];
 
     const int nch = (T + kC - 1) / kC;
-    // B operands, one chunk ahead: W and Qe rows 16w + n (k = d), P row
-    // 16w + n (k = j), K~^T rows 32w + 16ct + n (k = i); and this thread's
-    // pieces of the block's U~^T rows.
-    u32x4_t wr[4][2], qr[4][2], pr[2][2], kr[2][2][2], ur[NU];
-    float gam = 0.0f;
-    auto fetch_u = [&](int c) {
-        const size_t ch = static_cast<size_t>(c) * 32 + h;
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int q = t + 256 * j, arr = q / (RB * 8), rem = q % (RB * 8);
-            ur[j] = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) + (ch * 128 + RB * rb + (rem >> 3)) * kC +
-                                                      8 * (rem & 7));
-        }
-        gam = in.gam[ch];
+    // Operands of one chunk. op[0..7]: W (U waves) or Qe (O waves) token
+    // tile tt, [k step][hi, lo]; op[8..11]: P token tile tt (O waves; the U
+    // waves load W's first steps there again, an L1 hit, so that every wave
+    // runs the same loads). kr: K~^T column tile `wave`. ur: this thread's
+    // piece of the block's U~^T rows (threads < 256). Two stages: each is
+    // refilled with chunk c+2 as soon as its operands are consumed.
+    struct Stage {
+        u32x4_t op[12], kr[2][2], ur;
+        float gam;
     };
-    auto fetch_wqp = [&](int c) {
+    const uint16_t* oph = owave ? in.qeh : in.wh;
+    const uint16_t* opl = owave ? in.qel : in.wl;
+    const uint16_t* pph = owave ? in.ph : in.wh;
+    const uint16_t* ppl = owave ? in.pl : in.wl;
+    const int pstride = owave ? kC * kC : kC * 128;   // elements per (chunk, head) block
+    auto fetch_u = [&](Stage& S, int c) {
         const size_t ch = static_cast<size_t>(c) * 32 + h;
-        const size_t ow = (ch * kC + 16 * wave + n) * 128 + 8 * kb;
+        const int q = t & 255, arr = q >> 7, rem = q & 127;
+        S.ur = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) + (ch * 128 + 16 * rb + (rem >> 3)) * kC +
+                                                 8 * (rem & 7));
+        S.gam = in.gam[ch];
+    };
+    auto fetch_op = [&](Stage& S, int c) {
+        const size_t ch = static_cast<size_t>(c) * 32 + h;
+        const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            wr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.wh + ow + 32 * ks);
-            wr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.wl + ow + 32 * ks);
-            qr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.qeh + ow + 32 * ks);
-            qr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.qel + ow + 32 * ks);
+            S.op[2 * ks] = *reinterpret_cast<const u32x4_t*>(oph + ow + 512 * ks);
+            S.op[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(opl + ow + 512 * ks);
         }
-        const size_t op = (ch * kC + 16 * wave + n) * kC + 8 * kb;
+        const size_t op = ch * pstride + 8 * (tt * (owave ? 2 : 4) * 64 + lane);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            pr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.ph + op + 32 * ks);
-            pr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.pl + op + 32 * ks);
+            S.op[8 + 2 * ks] = *reinterpret_cast<const u32x4_t*>(pph + op + 512 * ks);
+            S.op[9 + 2 * ks] = *reinterpret_cast<const u32x4_t*>(ppl + op + 512 * ks);
         }
     };
-    auto fetch_k = [&](int c) {
+    auto fetch_k = [&](Stage& S, int c) {
         const size_t ch = static_cast<size_t>(c) * 32 + h;
+        const size_t ok = ch * 128 * kC + 8 * (wave * 2 * 64 + lane);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const size_t ok = (ch * 128 + 32 * wave + 16 * ct + n) * kC + 8 * kb;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                kr[ct][ks][0] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 32 * ks);
-                kr[ct][ks][1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 32 * ks);
-            }
+        for (int ks = 0; ks < 2; ++ks) {
+            S.kr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 512 * ks);
+            S.kr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 512 * ks);
         }
     };
-    fetch_u(0);
-    fetch_wqp(0);
-    fetch_k(0);
-    for (int c = 0; c < nch; ++c) {
+    // One chunk from stage S, refilling S with chunk cn. The refill loads are
+    // unconditional (cn is clamped to the last chunk) and so are the output
+    // stores (the output buffer holds whole chunks): with no branch around a
+    // memory instruction the compiler's vmcnt bookkeeping stays exact and
+    // each wait covers only the loads it needs.
+    auto step = [&](Stage& S, int c, int cn) {
         // [S | U~^T] -> LDS
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    uint16_t hh, ll;
-                    split_bf16(sacc[r][cc][ii], hh, ll);
-                    const int o = (16 * r + 4 * kb + ii) * LA + 32 * wave + 16 * cc + n;
-                    Ah[o] = hh;
-                    Al[o] = ll;
-                }
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int q = t + 256 * j, arr = q / (RB * 8), rem = q % (RB * 8);
-            *reinterpret_cast<u32x4_t*>((arr ? Al : Ah) + (rem >> 3) * LA + 128 + 8 * (rem & 7)) = ur[j];
+        for (int ii = 0; ii < 4; ++ii) {
+            uint16_t hh, ll;
+            split_bf16(sacc[ii], hh, ll);
+            const int o = (4 * kb + ii) * kLA + 16 * wave + n;
+            Ah[o] = hh;
+            Al[o] = ll;
         }
-        const float g = gam;
-        // The next chunk's loads are issued unconditionally (the last
-        // iteration re-reads its own chunk) and so are the output stores
-        // (the output buffer holds whole chunks): with no branch around a
-        // memory instruction the compiler's vmcnt bookkeeping stays exact and
-        // each wait covers only the loads it needs.
-        const int cn = min(c + 1, nch - 1);
+        if (t < 256) {
+            const int arr = t >> 7, rem = t & 127;
+            *reinterpret_cast<u32x4_t*>((arr ? Al : Ah) + (rem >> 3) * kLA + 128 + 8 * (rem & 7)) = S.ur;
+        }
+        const float g = S.gam;
         __syncthreads();
-        fetch_u(cn);
-        // U^T acc = S W^T (k = d, 4 steps), O^T = S Qe^T + U~^T P^T (6 steps)
-        f32x4_t au[RT], ao[RT];
-#pragma unroll
-        for (int r = 0; r < RT; ++r) au[r] = ao[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        fetch_u(S, cn);
+        // U waves: acc = S W^T (k = d, 4 steps); O waves: acc = S Qe^T +
+        // U~^T P^T (6 steps). Three accumulators (lo*hi, hi*lo, hi*hi) keep
+        // the dependent MFMA chains short.
+        f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
 #pragma unroll
         for (int ks = 0; ks < 6; ++ks) {
-            u32x4_t a_h[RT], a_l[RT];
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                a_h[r] = *reinterpret_cast<const u32x4_t*>(Ah + (16 * r + n) * LA + 32 * ks + 8 * kb);
-                a_l[r] = *reinterpret_cast<const u32x4_t*>(Al + (16 * r + n) * LA + 32 * ks + 8 * kb);
-            }
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                if (ks < 4) {
-                    au[r] = mfma_16x16x32_bf16(a_l[r], wr[ks][0], au[r]);
-                    au[r] = mfma_16x16x32_bf16(a_h[r], wr[ks][1], au[r]);
-                    au[r] = mfma_16x16x32_bf16(a_h[r], wr[ks][0], au[r]);
-                    ao[r] = mfma_16x16x32_bf16(a_l[r], qr[ks][0], ao[r]);
-                    ao[r] = mfma_16x16x32_bf16(a_h[r], qr[ks][1], ao[r]);
-                    ao[r] = mfma_16x16x32_bf16(a_h[r], qr[ks][0], ao[r]);
-                } else {
-                    ao[r] = mfma_16x16x32_bf16(a_l[r], pr[ks - 4][0], ao[r]);
-                    ao[r] = mfma_16x16x32_bf16(a_h[r], pr[ks - 4][1], ao[r]);
-                    ao[r] = mfma_16x16x32_bf16(a_h[r], pr[ks - 4][0], ao[r]);
-                }
-            }
+            if (ks >= 4 && !owave) break;
+            const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(Ah + n * kLA + 32 * ks + 8 * kb);
+            const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(Al + n * kLA + 32 * ks + 8 * kb);
+            a0 = mfma_16x16x32_bf16(a_l, S.op[2 * ks], a0);
+            a1 = mfma_16x16x32_bf16(a_h, S.op[2 * ks + 1], a1);
+            a2 = mfma_16x16x32_bf16(a_h, S.op[2 * ks], a2);
         }
-        fetch_wqp(cn);
-        // U^T = U~^T - S W^T -> LDS; O^T -> pre-norm output (token-major)
-        const int i = 16 * wave + n;
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
+        fetch_op(S, cn);
+        const f32x4_t acc = a0 + a1 + a2;
+        const int i = 16 * tt + n;
+        if (owave) {
+            // O^T -> pre-norm output (token-major)
+            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + i) * 4096 + h * 128 + 16 * rb + 4 * kb) = acc;
+        } else {
+            // U^T = U~^T - S W^T -> LDS
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int row = 16 * r + 4 * kb + ii;
-                const float ut = bf16_to_f32(Ah[row * LA + 128 + i]) + bf16_to_f32(Al[row * LA + 128 + i]) - au[r][ii];
+                const int row = 4 * kb + ii;
+                const float ut = bf16_to_f32(Ah[row * kLA + 128 + i]) + bf16_to_f32(Al[row * kLA + 128 + i]) - acc[ii];
                 uint16_t hh, ll;
                 split_bf16(ut, hh, ll);
                 Uh[row * kLT + i] = hh;
                 Ul[row * kLT + i] = ll;
             }
-            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + i) * 4096 + h * 128 + RB * rb + 16 * r +
-                                        4 * kb) = ao[r];
         }
         __syncthreads();
         // S = e^{G_C} S + U^T K~ (k = token, 2 steps)
-#pragma unroll
-        for (int r = 0; r < RT; ++r)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) sacc[r][cc][ii] *= g;
+        f32x4_t s1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        sacc *= g;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            u32x4_t a_h[RT], a_l[RT];
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                a_h[r] = *reinterpret_cast<const u32x4_t*>(Uh + (16 * r + n) * kLT + 32 * ks + 8 * kb);
-                a_l[r] = *reinterpret_cast<const u32x4_t*>(Ul + (16 * r + n) * kLT + 32 * ks + 8 * kb);
-            }
-#pragma unroll
-            for (int r = 0; r < RT; ++r)
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    sacc[r][ct] = mfma_16x16x32_bf16(a_l[r], kr[ct][ks][0], sacc[r][ct]);
-                    sacc[r][ct] = mfma_16x16x32_bf16(a_h[r], kr[ct][ks][1], sacc[r][ct]);
-                    sacc[r][ct] = mfma_16x16x32_bf16(a_h[r], kr[ct][ks][0], sacc[r][ct]);
-                }
+            const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(Uh + n * kLT + 32 * ks + 8 * kb);
+            const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(Ul + n * kLT + 32 * ks + 8 * kb);
+            s1 = mfma_16x16x32_bf16(a_l, S.kr[ks][0], s1);
+            s1 = mfma_16x16x32_bf16(a_h, S.kr[ks][1], s1);
+            sacc = mfma_16x16x32_bf16(a_h, S.kr[ks][0], sacc);
         }
-        fetch_k(cn);
+        sacc += s1;
+        fetch_k(S, cn);
+    };
+    Stage s0, s1;
+    fetch_u(s0, 0);
+    fetch_op(s0, 0);
+    fetch_k(s0, 0);
+    const int c1 = min(1, nch - 1);
+    fetch_u(s1, c1);
+    fetch_op(s1, c1);
+    fetch_k(s1, c1);
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        step(s0, c, min(c + 2, nch - 1));
+        step(s1, c + 1, min(c + 3, nch - 1));
     }
+    if (c < nch) step(s0, c, c);
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                Sg[(16 * r + 4 * kb + ii) * 128 + 32 * wave + 16 * cc + n] = sacc[r][cc][ii];
+    for (int ii = 0; ii < 4; ++ii) Sg[(4 * kb + ii) * 128 + 16 * wave + n] = sacc[ii];
 }
 
 hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
@@ -624,8 +605,7 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
                                                                conv_state, ctx->dn);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
-    constexpr int kRB = QFF_DN_STATE_RB;
-    dn_chunk_state_kernel<kRB><<<32 * (128 / kRB), 256, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);
+    dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);
     return hipGetLastError();
 }
 
