@@ -113,6 +113,30 @@ __device__ __forceinline__ void conv8_any(bool edge, const void* __restrict__ qk
         conv8<IN_DT, NT, false>(qkv, conv_state, conv_w, ch, tok0, T, y);
 }
 
+// Interior chunks of bf16 input: the 7 projection rows tok0-3 .. tok0+3 of
+// 8 channels are loaded up front (one 16-B load each), so every conv pass's
+// loads are in flight together, and the conv runs from registers.
+__device__ __forceinline__ void conv_rows_bf16(const void* __restrict__ qkv, int ch, int tok0, u32x4_t (&r)[7]) {
+#pragma unroll
+    for (int i = 0; i < 7; ++i)
+        r[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(qkv) +
+                                                 static_cast<size_t>(tok0 - 3 + i) * 8192 + ch);
+}
+
+__device__ __forceinline__ void conv_from_rows(const u32x4_t (&r)[7], const float* __restrict__ conv_w, int ch,
+                                               float (&y)[4][8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float4 w = reinterpret_cast<const float4*>(conv_w)[ch + k];
+        float e[7];
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+            e[i] = (k & 1) ? __uint_as_float(r[i][k >> 1] & 0xffff0000u) : __uint_as_float(r[i][k >> 1] << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i][k] = silu_fast(e[i] * w.x + e[i + 1] * w.y + e[i + 2] * w.z + e[i + 3] * w.w);
+    }
+}
+
 // Splits 8 floats into bf16 hi / lo and stores 16 B of each.
 __device__ __forceinline__ void store_split8(uint16_t* hi, uint16_t* lo, const float (&x)[8]) {
     uint32_t hw[4], lw[4];
@@ -170,6 +194,38 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
     float* G = reinterpret_cast<float*>(smem + kOffG);
     float* Bt = G + kC;
 
+    // Conv passes: thread -> channels 8oc .. 8oc+7 of a 128-channel block x
+    // tokens 4g .. 4g+3 (q and k of key head kh, v of value head h).
+    const int oc = t & 15, g = t >> 4;
+    const bool fast = IN_DT == 1 && !edge;
+    u32x4_t rq[7], rk[7], rv[7];
+    if (fast) {
+        conv_rows_bf16(qkv, kh * 128 + 8 * oc, t0 + 4 * g, rq);
+        conv_rows_bf16(qkv, 2048 + kh * 128 + 8 * oc, t0 + 4 * g, rk);
+        conv_rows_bf16(qkv, 4096 + h * 128 + 8 * oc, t0 + 4 * g, rv);
+    }
+    auto conv = [&](const u32x4_t (&r)[7], int chn, float (&y)[4][8]) {
+        if (fast)
+            conv_from_rows(r, conv_w, chn, y);
+        else
+            conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, chn, t0 + 4 * g, T, y);
+    };
+    // L2 norm per token over the 16 lanes of its head (deltanet.metal
+    // :282-305), q then / sqrt(128); into LDS as bf16 hi/lo.
+    auto l2norm_store = [&](float (&y)[4][8], bool isq, uint16_t* dh, uint16_t* dl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
+            ss = group_sum<16>(ss);
+            const float inv = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) y[i][k] = isq ? (y[i][k] * inv) * (1.0f / sqrtf(128.0f)) : y[i][k] * inv;
+            store_split8(dh + (4 * g + i) * kLD + 8 * oc, dl + (4 * g + i) * kLD + 8 * oc, y[i]);
+        }
+    };
+
     // gates (deltanet.metal:250-280): log g = -e^{A_log} softplus(a + dt_bias),
     // beta = sigmoid(b); G = inclusive prefix sum over the chunk. Padded
     // tokens have log g = 0 and beta = 0, so they change nothing.
@@ -186,50 +242,32 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         Bt[lane] = ok ? sigmoid(b[gi]) : 0.0f;
         if (lane == 63) out.gam[ch] = expf(x);
     }
+    float qn[4][8], kn[4][8];
+    conv(rq, kh * 128 + 8 * oc, qn);
+    l2norm_store(qn, true, Qh, Ql);
+    conv(rk, 2048 + kh * 128 + 8 * oc, kn);
+    l2norm_store(kn, false, Kh, Kl);
     __syncthreads();
-
-    // q and k of key head kh: thread -> 8 channels (lanes 0-15 of each 32
-    // q, 16-31 k) x tokens 8g .. 8g+7; L2 norm per token over the 16 lanes of
-    // its head (deltanet.metal:282-305), q then / sqrt(128).
+    // K~^T rows 8oc .. 8oc+7, tokens 4g .. 4g+3 (half of an operand piece)
     {
-        const bool isq = (t & 31) < 16;
-        const int oc = t & 15, g = t >> 5;
-        const int chn = (isq ? 0 : 2048) + kh * 128 + 8 * oc;
-        float y[8][8];
-        conv8_any<IN_DT, 8>(edge, qkv, conv_state, conv_w, chn, t0 + 8 * g, T, y);
+        const float gc = G[kC - 1];
+        float sk[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float ss = 0.0f;
+        for (int i = 0; i < 4; ++i) sk[i] = expf(gc - G[4 * g + i]);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
-            ss = group_sum<16>(ss);
-            const float inv = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) y[i][k] = isq ? (y[i][k] * inv) * (1.0f / sqrtf(128.0f)) : y[i][k] * inv;
-            const int row = 8 * g + i;
-            store_split8((isq ? Qh : Kh) + row * kLD + 8 * oc, (isq ? Ql : Kl) + row * kLD + 8 * oc, y[i]);
-        }
-        if (!isq) {
-            // K~^T rows 8oc .. 8oc+7, tokens 8g .. 8g+7
-            const float gc = G[kC - 1];
-            float sk[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sk[i] = expf(gc - G[8 * g + i]);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float x[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) x[i] = sk[i] * y[i][k];
-                const size_t o = ch * 128 * kC + 8 * swz<kC>(8 * oc + k, g);
-                store_split8(out.kth + o, out.ktl + o, x);
-            }
+        for (int k = 0; k < 8; ++k) {
+            uint32_t h0, l0, h1, l1;
+            split_bf16x2(sk[0] * kn[0][k], sk[1] * kn[1][k], h0, l0);
+            split_bf16x2(sk[2] * kn[2][k], sk[3] * kn[3][k], h1, l1);
+            const size_t o = ch * 128 * kC + 8 * swz<kC>(8 * oc + k, g >> 1) + 4 * (g & 1);
+            *reinterpret_cast<u32x2_t*>(out.kth + o) = u32x2_t{h0, h1};
+            *reinterpret_cast<u32x2_t*>(out.ktl + o) = u32x2_t{l0, l1};
         }
     }
-    // beta v of value head h: thread -> 8 channels x tokens 4g .. 4g+3
+    // beta v of value head h
     {
-        const int oc = t & 15, g = t >> 4;
         float y[4][8];
-        conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, 4096 + h * 128 + 8 * oc, t0 + 4 * g, T, y);
+        conv(rv, 4096 + h * 128 + 8 * oc, y);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * g + i;
@@ -238,6 +276,13 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
             for (int k = 0; k < 8; ++k) y[i][k] *= bb;
             store_split8(Vh + row * kLD + 8 * oc, Vl + row * kLD + 8 * oc, y[i]);
         }
+    }
+    // Q~ = e^G q, kept for Qe
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float eg = expf(G[4 * g + i]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qn[i][k] *= eg;
     }
     __syncthreads();
 
@@ -264,12 +309,14 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
-    // P out, 16 B per thread and piece
+    // P out, 16 B per thread and piece; the pieces stay in registers until
+    // the T region is free again
+    u32x4_t pkeep[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Tl : Th) + row * kLT + c8);
-        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7)) = v;
+        pkeep[k] = *reinterpret_cast<const u32x4_t*>((arr ? Tl : Th) + row * kLT + c8);
+        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7)) = pkeep[k];
     }
     // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
     //   diagonal blocks by forward substitution, one wave each;
@@ -283,10 +330,10 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
             float tc[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float acc = 0.0f;
+                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < i; ++j) acc = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], acc);
-                tc[i] = (i == lane ? 1.0f : 0.0f) - acc;
+                for (int j = 0; j < i; ++j) acc[j & 3] = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], acc[j & 3]);
+                tc[i] = (i == lane ? 1.0f : 0.0f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
                 Tm[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
             }
         }
@@ -369,8 +416,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
-    // W out; P back from global into the T region (T is consumed). The same
-    // workgroup wrote P above, and the barriers since make it visible.
+    // W out; P back into the T region (T is consumed)
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int q = t + 256 * k, arr = q >> 10, row = (q & 1023) >> 4, c8 = 8 * (q & 15);
@@ -380,8 +426,7 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
-        *reinterpret_cast<u32x4_t*>((arr ? Tl : Th) + row * kLT + c8) =
-            *reinterpret_cast<const u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7));
+        *reinterpret_cast<u32x4_t*>((arr ? Tl : Th) + row * kLT + c8) = pkeep[k];
     }
     __syncthreads();
     // P W -> fp32 [64][132] in the K region (X is consumed)
@@ -399,29 +444,18 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
                 PW[(16 * wave + 4 * kb + ii) * 132 + 64 * half + 16 * cd + n] = pw[0][cd][ii];
     }
     __syncthreads();
-    // Qe = e^G q - P W with q recomputed (conv + norm): thread -> 8 channels
-    // x tokens 4g .. 4g+3
-    {
-        const int oc = t & 15, g = t >> 4;
-        float y[4][8];
-        conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, kh * 128 + 8 * oc, t0 + 4 * g, T, y);
+    // Qe = Q~ - P W
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 4 * g + i;
-            float ss = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * g + i;
+        const float4 p0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc);
+        const float4 p1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc + 4);
+        const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        float y[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
-            ss = group_sum<16>(ss);
-            const float inv = 1.0f / sqrtf(ss + 1e-6f);
-            const float eg = expf(G[row]);
-            const float4 p0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc);
-            const float4 p1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc + 4);
-            const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) y[i][k] = eg * ((y[i][k] * inv) * (1.0f / sqrtf(128.0f))) - pw[k];
-            const size_t o = ch * kC * 128 + 8 * swz<128>(row, oc);
-            store_split8(out.qeh + o, out.qel + o, y[i]);
-        }
+        for (int k = 0; k < 8; ++k) y[k] = qn[i][k] - pw[k];
+        const size_t o = ch * kC * 128 + 8 * swz<128>(row, oc);
+        store_split8(out.qeh + o, out.qel + o, y);
     }
 }
 
