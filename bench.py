@@ -29,6 +29,14 @@ C0_BYTES = 4_424_448           # DeltaNet decode, one layer-step at B=1
 C0_FLOPS = 3_670_016
 C1_FLOPS = 23_622_320_128      # DeltaNet chunked prefill T=4096
 C1_BYTES = 137_428_992
+# Config 1 per kernel, per launch (64 chunks x 32 heads, C = 64, d = 128):
+# the chunk-local pass owns K K^T, Q K^T, T X and T V (4 * 2C^2 d per chunk
+# and head), the state pass P U~, S W^T, S Qe^T and U^T K~ (2C^2 d + 3 * 2Cd^2).
+C1_KERNEL_FLOPS = {
+    "dn_chunk_local": 2048 * 4 * 2 * 64 * 64 * 128,
+    "dn_chunk_state": 2048 * (2 * 64 * 64 * 128 + 3 * 2 * 64 * 128 * 128),
+}
+COPY_PROBE_BYTES = 256 << 20   # --copy-probe: one D2D copy of this size (counter calibration)
 
 
 def log(*a):
@@ -208,29 +216,50 @@ def bench_c2(ctx, B, steps, warmup, max_ctx=8192):
             "TFLOPs": flops / (part * 1e-3) / 1e12}
 
 
-def cpu_baseline_c1(budget_s=20.0):
+def cpu_baseline_c1(min_s=10.0, max_reps=12):
     """The fp32 reference-order oracle (sequential, one thread) on the
-    config-1 workload: as many tokens as fit in ~budget_s of CPU."""
-    import numpy as np
+    config-1 workload: whole 4096-token sequences from zero state, repeated
+    until at least min_s seconds of CPU work have run."""
     from oracle import oracle as O
     from qff import synth
     T = 4096
     p = synth.deltanet_params()
     inp = synth.deltanet_prefill_inputs(T)
     qkv, z = O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"])
-    # calibrate on 64 tokens, then run a bounded prefix
-    t0 = time.perf_counter()
-    O.deltanet_sequence(qkv[:64], z[:64], inp["a"][:64], inp["b"][:64], p["a_log"], p["dt_bias"],
-                        p["conv_w"], p["norm_w"], inp["conv_state"], inp["ssm_state"])
-    per_tok = (time.perf_counter() - t0) / 64
-    n = int(min(T, max(64, budget_s / per_tok)))
-    t0 = time.perf_counter()
-    O.deltanet_sequence(qkv[:n], z[:n], inp["a"][:n], inp["b"][:n], p["a_log"], p["dt_bias"],
-                        p["conv_w"], p["norm_w"], inp["conv_state"], inp["ssm_state"])
-    dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"first {n} of the 4096 config-1 tokens through the fp32 sequential oracle "
-                      f"(oracle/qff_oracle.c, gcc -O2), 1 thread, {dt:.1f} s"}
+    reps, dt = 0, 0.0
+    while dt < min_s and reps < max_reps:
+        t0 = time.perf_counter()
+        O.deltanet_sequence(qkv, z, inp["a"], inp["b"], p["a_log"], p["dt_bias"], p["conv_w"], p["norm_w"],
+                            inp["conv_state"], inp["ssm_state"])
+        dt += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x the 4096-token config-1 sequence from zero state through the fp32 "
+                      f"sequential oracle (oracle/qff_oracle.c, gcc -O2), 1 thread, {dt:.1f} s"}
+
+
+def copy_probe():
+    """One device-to-device copy of COPY_PROBE_BYTES, for scaling the
+    FETCH_SIZE / WRITE_SIZE counters of a profiling run to bytes."""
+    import torch
+    src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/traffic_c1.json, FETCH_SIZE + WRITE_SIZE scaled by the copy
+    probe), or None when it holds no figure for that kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic_c1.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        return rec["kernels"][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main():
@@ -240,6 +269,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of c0,c1,c2,dnb")
+    ap.add_argument("--copy-probe", action="store_true", help="also run one copy of known size "
+                    "(calibrates FETCH_SIZE / WRITE_SIZE in a counter run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
@@ -272,15 +303,21 @@ def main():
         log("cpu baseline (oracle, 1 thread)")
         cpu = cpu_baseline_c1()
 
+    if args.copy_probe:
+        log("copy probe")
+        copy_probe()
+
     roof = None
     if c1 is not None:
         kt = c1["kernels_ms"]
         dom = max(kt, key=kt.get)
-        achieved = C1_FLOPS / (kt[dom] * 1e-3) / 1e12
+        achieved = C1_KERNEL_FLOPS[dom] / (kt[dom] * 1e-3) / 1e12
+        traffic = traffic_for(dom)
         roof = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None, "kernel": dom,
-                "kernel_ms": kt[dom],
-                "hbm_GBps": C1_BYTES / (kt[dom] * 1e-3) / 1e9}
+                "frac": achieved / BF16_PEAK_TFLOPS, "traffic": traffic, "kernel": dom,
+                "kernel_ms": kt[dom], "flops_per_launch": C1_KERNEL_FLOPS[dom],
+                "path_TFLOPs": C1_FLOPS / (c1["ms_per_step"] * 1e-3) / 1e12,
+                "path_hbm_GBps": C1_BYTES / (c1["ms_per_step"] * 1e-3) / 1e9}
     value = c1["tokens_per_s"] if c1 else None
     line = {
         "metric": "attn tokens/s: DeltaNet+GQA decode (B=1..32) & 8K prefill; % HBM/MFMA roofline",
