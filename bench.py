@@ -36,6 +36,8 @@ C1_KERNEL_FLOPS = {
     "dn_chunk_local": 2048 * 4 * 2 * 64 * 64 * 128,
     "dn_chunk_state": 2048 * (2 * 64 * 64 * 128 + 3 * 2 * 64 * 128 * 128),
 }
+C3_ATTN_FLOPS = 549_822_922_752   # GQA causal prefill T=8192: 32 D T (T + 1)
+C3_PROJ_FLOPS = 309_237_645_312   # 2 T 2048 (8192 + 512 + 512)
 COPY_PROBE_BYTES = 256 << 20   # --copy-probe: one D2D copy of this size (counter calibration)
 
 
@@ -216,6 +218,46 @@ def bench_c2(ctx, B, steps, warmup, max_ctx=8192):
             "TFLOPs": flops / (part * 1e-3) / 1e12}
 
 
+def bench_c3(ctx, steps, warmup):
+    """Config 3: GQA causal prefill, T = 8192, with the q|gate, k and v
+    affine-Q4 projections from hidden 2048 (three Q4 GEMMs, then attention)."""
+    import numpy as np
+    import torch
+    import qff
+    from qff import synth
+    T, H = 8192, 2048
+    g = torch.Generator(device="cuda").manual_seed(3)
+    p = {k: torch.from_numpy(v).cuda() for k, v in synth.gqa_params().items()}
+    X = bf16_randn((T, H), g)
+    wts = []
+    for i, rows in enumerate((8192, 512, 512)):
+        w, sc, bi = synth.q4_weight(rows, H, seed=300 + i)
+        wts.append((torch.from_numpy(w.view(np.int32)).cuda(),
+                    torch.from_numpy(sc.view(np.int16)).view(torch.float16).cuda(),
+                    torch.from_numpy(bi.view(np.int16)).view(torch.float16).cuda()))
+    qg = torch.empty(T, 8192, dtype=torch.bfloat16, device="cuda")
+    k = torch.empty(T, 512, dtype=torch.bfloat16, device="cuda")
+    v = torch.empty(T, 512, dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros(T, 2, 256, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros(T, 2, 256, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(T, 16, 256, dtype=torch.bfloat16, device="cuda")
+
+    def step(i):
+        for (w, sc, bi), y in zip(wts, (qg, k, v)):
+            qff.q4_matmul(ctx, w, sc, bi, X, out=y)
+        qff.gqa_prefill(ctx, p, qg.view(T, 16, 512), k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out=out)
+
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    kt, cnt = kernel_times(ctx, step, max(2, min(steps, 5)))
+    # three projections per step; kernel_times gives each kernel's mean launch
+    proj_ms = 3 * sum(v for k_, v in kt.items() if k_.startswith("q4_"))
+    attn_ms = sum(v for k_, v in kt.items() if k_.startswith("gqa_prefill"))
+    return {"ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "kernels_ms": kt,
+            "attention_TFLOPs": C3_ATTN_FLOPS / (attn_ms * 1e-3) / 1e12 if attn_ms else None,
+            "projection_TFLOPs": C3_PROJ_FLOPS / (proj_ms * 1e-3) / 1e12 if proj_ms else None,
+            "path_TFLOPs": (C3_ATTN_FLOPS + C3_PROJ_FLOPS) / (ms * 1e-3) / 1e12}
+
+
 def cpu_baseline_c1(min_s=10.0, max_reps=12):
     """The fp32 reference-order oracle (sequential, one thread) on the
     config-1 workload: whole 4096-token sequences from zero state, repeated
@@ -268,7 +310,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,dnb")
+    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,dnb")
     ap.add_argument("--copy-probe", action="store_true", help="also run one copy of known size "
                     "(calibrates FETCH_SIZE / WRITE_SIZE in a counter run)")
     args = ap.parse_args()
@@ -279,8 +321,8 @@ def main():
     import torch
     import qff
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "dnb"}
-    ctx = qff.Context(max_batch=32, max_ctx=8192, max_prefill_tokens=4096)
+    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "c3", "dnb"}
+    ctx = qff.Context(max_batch=32, max_ctx=8192, max_prefill_tokens=8192)
     configs = {}
     if "c0" in only:
         log("config 0: DeltaNet decode B=1")
@@ -293,6 +335,9 @@ def main():
         for B in (1, 8, 32):
             log(f"config 2: GQA decode B={B}")
             configs[f"c2_gqa_decode_b{B}"] = bench_c2(ctx, B, max(args.steps * 10, 200), args.warmup)
+    if "c3" in only:
+        log("config 3: GQA prefill T=8192 + Q4 projections")
+        configs["c3_gqa_prefill_t8192"] = bench_c3(ctx, max(2, args.steps // 4), 1)
     c1 = None
     if "c1" in only:
         log("config 1: DeltaNet prefill T=4096")

@@ -4,6 +4,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 
 #include "common.hpp"
@@ -22,6 +23,9 @@ static qff_ctx_cfg resolve(const qff_ctx_cfg* cfg) {
     return c;
 }
 
+// Tokens per slice of a many-token Q4 product (group sums in workspace).
+int q4_xs_tokens(const qff_ctx_cfg& cfg) { return std::max(std::max(cfg.max_batch, cfg.max_prefill_tokens), 1024); }
+
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     WorkspaceLayout L{};
     size_t off = 0;
@@ -32,6 +36,7 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_d = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
     L.gqa_o = take(B * 2 * kGqaMaxChunks * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
+    L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(float));
     const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
@@ -148,6 +153,8 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_o = reinterpret_cast<float*>(base + L.gqa_o);
     auto u16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
     c->gqa_qb = u16(L.gqa_qb);
+    c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
+    c->q4_xs_tokens = q4_xs_tokens(c->cfg);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
     c->dn = qff_dn_bufs{u16(L.wh),  u16(L.wl),  u16(L.qeh), u16(L.qel), u16(L.kth), u16(L.ktl),
                         u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam)};

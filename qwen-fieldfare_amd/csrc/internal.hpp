@@ -38,6 +38,9 @@ struct qff_ctx {
     float* gqa_o = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8 * 256]
     // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
     uint16_t* gqa_qb = nullptr;
+    // Many-token Q4 products: per-token group sums [q4_xs_tokens][64] fp32.
+    float* q4_xs = nullptr;
+    int q4_xs_tokens = 0;
     // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
     // chunk intermediates.
     float* pf_o = nullptr;
@@ -54,10 +57,11 @@ constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, pf_o, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, pf_o, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
+int q4_xs_tokens(const qff_ctx_cfg& cfg);
 
 // Brackets the kernels launched in its scope with the context's profiling
 // events when profiling is on; costs one branch otherwise.

@@ -138,6 +138,244 @@ __global__ __launch_bounds__(256) void q4_matmul_mfma_kernel(
     }
 }
 
+// ---- many-token GEMM (prefill projections) -----------------------------------
+//
+// y[m, r] for batch >= kQ4GemmMinBatch, as
+//   y = sum_g s_g P_g + sum_g b_g X_g,
+//   P_g[r, m] = sum_{c in g} (128 + q[r, c]) x[m, c] - 128 X_g[m],
+//   X_g[m] = sum_{c in g} x[m, c]
+// with x rounded to bf16 (exactly the operands the matrix cores see).
+// q4_xsum_kernel forms X_g first (group-major). q4_gemm_kernel: one workgroup
+// per 128 rows x 128 tokens, four waves of 64 x 64 (4 x 4 MFMA tiles, C rows =
+// weight rows so each lane's four outputs are adjacent in y). Per 64-column
+// group the workgroup stages the group's weight words, converted once, the
+// bf16 activations and -128 X_g in LDS while the next group's loads are in
+// flight; the MFMAs start from -128 X_g, so P_g is the small sum q x and the
+// large 128 X_g cancels inside the fp32 accumulator, and s_g P_g is added on
+// the vector units. The bias sums are one small product at the end, on
+// bf16x3 MFMAs over the groups.
+//
+// Within each 8-column word the matrix-core k order is (c0, c4, c1, c5, c2,
+// c6, c3, c7): dword j of the converted word is then
+// ((w >> 4j) & 0x000F000F) | 0x43004300 (two instructions), and the
+// activations are staged in the same order.
+constexpr int kQ4GemmMinBatch = 64;
+constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
+
+__device__ __forceinline__ u32x4_t q4_to_bf16_interleaved(uint32_t w) {
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = ((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
+    return r;
+}
+
+// 8 bf16 (x0 .. x7 in 4 dwords) -> (x0 x4, x1 x5, x2 x6, x3 x7)
+__device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
+    return u32x4_t{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                   __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+}
+
+// X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
+// lane l sums half-groups l, l + 64 (32 columns each), pairs of lanes combine.
+template <int X_DT>
+__global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x, float* __restrict__ xs, int cols,
+                                                      int batch, int xs_stride) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int G = cols / 64;
+    if (m >= batch) return;
+    for (int hg0 = 0; hg0 < 2 * G; hg0 += 64) {
+        const int hg = hg0 + lane;
+        float acc = 0.0f;
+        if (hg < 2 * G) {
+            const size_t o = static_cast<size_t>(m) * cols + 32 * hg;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (X_DT == 1) {
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + o + 8 * i);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc += __uint_as_float(v[j] << 16) + __uint_as_float(v[j] & 0xffff0000u);
+                } else {
+                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + o + 8 * i);
+                    const float4 a = p[0], b = p[1];
+                    acc += bf16_to_f32(f32_to_bf16(a.x)) + bf16_to_f32(f32_to_bf16(a.y)) +
+                           bf16_to_f32(f32_to_bf16(a.z)) + bf16_to_f32(f32_to_bf16(a.w)) +
+                           bf16_to_f32(f32_to_bf16(b.x)) + bf16_to_f32(f32_to_bf16(b.y)) +
+                           bf16_to_f32(f32_to_bf16(b.z)) + bf16_to_f32(f32_to_bf16(b.w));
+                }
+            }
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        if ((lane & 1) == 0 && hg < 2 * G) xs[static_cast<size_t>(hg >> 1) * xs_stride + m] = acc;
+    }
+}
+
+template <int SB_DT, int X_DT, int Y_DT>
+__global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint16_t* __restrict__ biases,
+                                                      const void* __restrict__ x, const float* __restrict__ xs,
+                                                      int xs_stride, void* __restrict__ y, int rows, int cols,
+                                                      int batch) {
+    const int G = cols / 64;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = lane & 15, kb = lane >> 4;
+    const int wr = wave & 1, wm = wave >> 1;
+    const int R0 = blockIdx.x * 128, M0 = blockIdx.y * 128;
+
+    __shared__ __attribute__((aligned(16))) uint16_t Wl[128 * kQ4LD];
+    __shared__ __attribute__((aligned(16))) uint16_t Xl[128 * kQ4LD];
+    __shared__ __attribute__((aligned(16))) float sl[kQ4MaxGroups][128];
+    __shared__ float xsl[128];
+
+    // scales of rows R0 .. R0+127, all groups
+    for (int idx = t; idx < 128 * G; idx += 256) {
+        const int r = idx / G, g = idx % G;
+        sl[g][r] = elem<SB_DT>::load(scales, static_cast<size_t>(min(R0 + r, rows - 1)) * G + g);
+    }
+
+    // staging: thread -> weight row t/2, words 4(t%2) .. +3 of the group;
+    // token t/2, columns 32(t%2) .. +31 of the group
+    const int srow = t >> 1, shalf = t & 1;
+    const uint32_t* wsrc = w + static_cast<size_t>(min(R0 + srow, rows - 1)) * (cols / 8) + 4 * shalf;
+    const int xm = min(M0 + srow, batch - 1);
+    const int xsm = min(M0 + (t & 127), batch - 1);
+    u32x4_t wreg, xreg[4];
+    float xsreg;
+    auto fetch = [&](int g) {
+        wreg = *reinterpret_cast<const u32x4_t*>(wsrc + 8 * g);
+        xsreg = xs[static_cast<size_t>(g) * xs_stride + xsm];
+        const size_t xo = static_cast<size_t>(xm) * cols + 64 * g + 32 * shalf;
+        if (X_DT == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                xreg[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo + 8 * i);
+                const float4 a = p[0], b = p[1];
+                xreg[i] = u32x4_t{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y),
+                                  pack_bf16x2(b.z, b.w)};
+            }
+        }
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    fetch(0);
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<u32x4_t*>(&Wl[srow * kQ4LD + 32 * shalf + 8 * i]) = q4_to_bf16_interleaved(wreg[i]);
+            *reinterpret_cast<u32x4_t*>(&Xl[srow * kQ4LD + 32 * shalf + 8 * i]) = interleave8(xreg[i]);
+        }
+        if (t < 128) xsl[t] = -128.0f * xsreg;
+        __syncthreads();
+        if (g + 1 < G) fetch(g + 1);
+        f32x4_t P[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float x0 = xsl[64 * wm + 16 * b + n];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) P[a][b] = f32x4_t{x0, x0, x0, x0};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            u32x4_t A[4], B[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+                A[rt] = *reinterpret_cast<const u32x4_t*>(&Wl[(64 * wr + 16 * rt + n) * kQ4LD + 32 * ks + 8 * kb]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                B[mt] = *reinterpret_cast<const u32x4_t*>(&Xl[(64 * wm + 16 * mt + n) * kQ4LD + 32 * ks + 8 * kb]);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) P[rt][mt] = mfma_16x16x32_bf16(A[rt], B[mt], P[rt][mt]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(&sl[g][64 * wr + 16 * rt + 4 * kb]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[rt][mt][i] = fmaf(sv[i], P[rt][mt][i], acc[rt][mt][i]);
+        }
+        __syncthreads();
+    }
+    // bias sums: acc += B X^T over the groups (k = g), bf16x3. A lane holds
+    // B[row][8kb .. 8kb+7] and X[token][8kb .. 8kb+7] of a 32-group step;
+    // groups past G are zero.
+    for (int g0 = 0; g0 < G; g0 += 32) {
+        u32x4_t bh[4], bl[4], xh[4], xl[4];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const size_t gi = static_cast<size_t>(min(R0 + 64 * wr + 16 * rt + n, rows - 1)) * G + g0 + 8 * kb;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                v[e] = g0 + 8 * kb + e < G ? elem<SB_DT>::load(biases, gi + e) : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t hh, ll;
+                split_bf16x2(v[2 * e], v[2 * e + 1], hh, ll);
+                bh[rt][e] = hh;
+                bl[rt][e] = ll;
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const float* xp = xs + static_cast<size_t>(g0 + 8 * kb) * xs_stride +
+                              min(M0 + 64 * wm + 16 * mt + n, batch - 1);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = g0 + 8 * kb + e < G ? xp[static_cast<size_t>(e) * xs_stride] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t hh, ll;
+                split_bf16x2(v[2 * e], v[2 * e + 1], hh, ll);
+                xh[mt][e] = hh;
+                xl[mt][e] = ll;
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                acc[rt][mt] = mfma_16x16x32_bf16(bl[rt], xh[mt], acc[rt][mt]);
+                acc[rt][mt] = mfma_16x16x32_bf16(bh[rt], xl[mt], acc[rt][mt]);
+                acc[rt][mt] = mfma_16x16x32_bf16(bh[rt], xh[mt], acc[rt][mt]);
+            }
+    }
+    // lane: token 64wm + 16mt + n, rows 64wr + 16rt + 4kb .. +3 (adjacent in y)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int m = M0 + 64 * wm + 16 * mt + n;
+        if (m >= batch) continue;
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const int r = R0 + 64 * wr + 16 * rt + 4 * kb;
+            const size_t o = static_cast<size_t>(m) * rows + r;
+            if (r + 3 < rows && (rows & 3) == 0) {
+                if (Y_DT == 1)
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
+                        u32x2_t{pack_bf16x2(acc[rt][mt][0], acc[rt][mt][1]), pack_bf16x2(acc[rt][mt][2], acc[rt][mt][3])};
+                else
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = acc[rt][mt];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r + i < rows) elem<Y_DT>::store(y, o + i, acc[rt][mt][i]);
+            }
+        }
+    }
+}
+
 hipError_t launch_q4_dequant(hipStream_t stream, const uint32_t* w, const void* scales,
                              const void* biases, qff_dtype sb_dtype, float* out, int rows, int cols) {
     const size_t words = static_cast<size_t>(rows) * (cols / 8);
@@ -153,10 +391,38 @@ hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w,
                             const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
                             void* y, qff_dtype y_dtype, int rows, int cols, int batch) {
     if (cols / 64 > kQ4MaxGroups) return hipErrorInvalidValue;
-    const dim3 grid((rows + 63) / 64, (batch + 15) / 16);
-    ProfScope prof(ctx, stream, "q4_matmul");
     const uint16_t* s = static_cast<const uint16_t*>(scales);
     const uint16_t* b = static_cast<const uint16_t*>(biases);
+    if (batch >= kQ4GemmMinBatch) {
+        // token slices of at most the workspace's capacity for group sums
+        for (int m0 = 0; m0 < batch; m0 += ctx->q4_xs_tokens) {
+            const int mb = min(ctx->q4_xs_tokens, batch - m0);
+            const void* xm = static_cast<const char*>(x) + static_cast<size_t>(m0) * cols * (x_dtype == QFF_BF16 ? 2 : 4);
+            void* ym = static_cast<char*>(y) + static_cast<size_t>(m0) * rows * (y_dtype == QFF_BF16 ? 2 : 4);
+            {
+                ProfScope prof(ctx, stream, "q4_xsum");
+                if (x_dtype == QFF_BF16)
+                    q4_xsum_kernel<1><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb, ctx->q4_xs_tokens);
+                else
+                    q4_xsum_kernel<0><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb, ctx->q4_xs_tokens);
+            }
+            const dim3 grid((rows + 127) / 128, (mb + 127) / 128);
+            ProfScope prof(ctx, stream, "q4_gemm");
+#define QFF_Q4G(S, X, Y) \
+    q4_gemm_kernel<S, X, Y><<<grid, 256, 0, stream>>>(w, s, b, xm, ctx->q4_xs, ctx->q4_xs_tokens, ym, rows, cols, mb)
+#define QFF_Q4G_Y(S, X) \
+    if (y_dtype == QFF_BF16) QFF_Q4G(S, X, 1); else QFF_Q4G(S, X, 0)
+#define QFF_Q4G_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4G_Y(S, 1); } else { QFF_Q4G_Y(S, 0); }
+            if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
+#undef QFF_Q4G_X
+#undef QFF_Q4G_Y
+#undef QFF_Q4G
+        }
+        return hipGetLastError();
+    }
+    const dim3 grid((rows + 63) / 64, (batch + 15) / 16);
+    ProfScope prof(ctx, stream, "q4_matmul");
 #define QFF_Q4(S, X, Y) q4_matmul_mfma_kernel<S, X, Y><<<grid, 256, 0, stream>>>(w, s, b, x, y, rows, cols, batch)
 #define QFF_Q4_Y(S, X) \
     if (y_dtype == QFF_BF16) QFF_Q4(S, X, 1); else QFF_Q4(S, X, 0)
