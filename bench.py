@@ -258,6 +258,92 @@ def bench_c3(ctx, steps, warmup):
             "path_TFLOPs": (C3_ATTN_FLOPS + C3_PROJ_FLOPS) / (ms * 1e-3) / 1e12}
 
 
+C4_BYTES = {(16, 32768): 13_535_395_840, (1, 65536): 2_193_735_680}
+
+
+def _q4_rand(rows, cols, g):
+    """Random affine-Q4 weight on the GPU: uniform nibbles, fp16 scales
+    U(0.005, 0.02) and biases N(0, 0.05) (the config-3/4 distributions)."""
+    import torch
+    w = torch.randint(-2 ** 31, 2 ** 31 - 1, (rows, cols // 8), dtype=torch.int32, device="cuda", generator=g)
+    sc = (torch.rand(rows, cols // 64, device="cuda", generator=g) * 0.015 + 0.005).half()
+    bi = (torch.randn(rows, cols // 64, device="cuda", generator=g) * 0.05).half()
+    return w, sc, bi
+
+
+def bench_c4(B, L, steps, warmup):
+    """Config 4: attention-only stack of the 40-layer pattern (3 Gated DeltaNet
+    + 1 GQA) x 10, hidden 2048, every projection affine-Q4 group 64, MoE
+    replaced by identity: one decode step of B sequences at context L. Each
+    layer reads the synthetic hidden state (the MoE is identity and no
+    residual stream is modelled), so per-layer work is the workload's. The
+    step is captured once in a HIP graph and replayed (the serving loop's
+    shape), so the timing is GPU time, not Python launch time."""
+    import numpy as np
+    import torch
+    import qff
+    from qff import synth
+    g = torch.Generator(device="cuda").manual_seed(40 + B)
+    ctx = qff.Context(max_batch=B, max_ctx=L, max_prefill_tokens=64)
+    dnp = {k: torch.from_numpy(v).cuda() for k, v in synth.deltanet_params().items()}
+    gqp = {k: torch.from_numpy(v).cuda() for k, v in synth.gqa_params().items()}
+    x = bf16_randn((B, 2048), g)
+    qkv = torch.empty(B, 8192, dtype=torch.bfloat16, device="cuda")
+    z = torch.empty(B, 4096, dtype=torch.bfloat16, device="cuda")
+    a = torch.empty(B, 32, device="cuda")
+    b = torch.empty(B, 32, device="cuda")
+    core = torch.empty(B, 4096, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(B, 2048, dtype=torch.bfloat16, device="cuda")
+    qg = torch.empty(B, 8192, dtype=torch.bfloat16, device="cuda")
+    kn = torch.empty(B, 512, dtype=torch.bfloat16, device="cuda")
+    vn = torch.empty(B, 512, dtype=torch.bfloat16, device="cuda")
+    att = torch.empty(B, 16, 256, dtype=torch.bfloat16, device="cuda")
+    pos = torch.full((B,), L - 1, dtype=torch.int32, device="cuda")
+    layers = []
+    for i in range(40):
+        if i % 4 == 3:
+            layers.append(("gqa", [_q4_rand(r, 2048, g) for r in (8192, 512, 512)] + [_q4_rand(2048, 4096, g)],
+                           bf16_randn((B, L, 2, 256), g), bf16_randn((B, L, 2, 256), g)))
+        else:
+            conv = torch.randn(B, 8192, 4, device="cuda", generator=g)
+            ssm = torch.randn(B, 32, 128, 128, device="cuda", generator=g) * 0.02
+            layers.append(("dn", [_q4_rand(r, 2048, g) for r in (8192, 4096, 32, 32)] + [_q4_rand(2048, 4096, g)],
+                           conv, ssm))
+
+    def step(i):
+        for kind, W, s1, s2 in layers:
+            if kind == "dn":
+                for (w, sc, bi), o in zip(W[:4], (qkv, z, b, a)):
+                    qff.q4_matmul(ctx, w, sc, bi, x, out=o)
+                qff.deltanet_decode(ctx, dnp, qkv, z, a, b, s1, s2, out=core)
+                qff.q4_matmul(ctx, *W[4], core, out=y)
+            else:
+                for (w, sc, bi), o in zip(W[:3], (qg, kn, vn)):
+                    qff.q4_matmul(ctx, w, sc, bi, x, out=o)
+                qff.gqa_decode(ctx, gqp, qg.view(B, 16, 512), kn.view(B, 2, 256), vn.view(B, 2, 256), s1, s2,
+                               pos, out=att)
+                qff.q4_matmul(ctx, *W[3], att.view(B, 4096), out=y)
+
+    kt, cnt = kernel_times(ctx, step, 2)
+    per_step_kernel_ms = {k: v * cnt[k] / 2 for k, v in kt.items()}
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step(0)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(0)
+    ms = timed(lambda i: graph.replay(), steps, warmup, torch.cuda.current_stream())
+    nbytes = C4_BYTES.get((B, L))
+    ctx.close()
+    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "batch": B, "context": L,
+            "kernel_ms_per_step": per_step_kernel_ms,
+            "GBps": nbytes / (ms * 1e-3) / 1e9 if nbytes else None,
+            "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS if nbytes else None}
+
+
 def cpu_baseline_c1(min_s=10.0, max_reps=12):
     """The fp32 reference-order oracle (sequential, one thread) on the
     config-1 workload: whole 4096-token sequences from zero state, repeated
@@ -310,7 +396,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,dnb")
+    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4,dnb")
     ap.add_argument("--copy-probe", action="store_true", help="also run one copy of known size "
                     "(calibrates FETCH_SIZE / WRITE_SIZE in a counter run)")
     args = ap.parse_args()
@@ -321,7 +407,7 @@ def main():
     import torch
     import qff
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "c3", "dnb"}
+    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "c3", "c4", "dnb"}
     ctx = qff.Context(max_batch=32, max_ctx=8192, max_prefill_tokens=8192)
     configs = {}
     if "c0" in only:
@@ -338,6 +424,12 @@ def main():
     if "c3" in only:
         log("config 3: GQA prefill T=8192 + Q4 projections")
         configs["c3_gqa_prefill_t8192"] = bench_c3(ctx, max(2, args.steps // 4), 1)
+    if "c4" in only:
+        for B, L in ((16, 32768), (1, 65536)):
+            log(f"config 4: 40-layer stack decode B={B} L={L}")
+            configs[f"c4_stack_b{B}_l{L}"] = bench_c4(B, L, max(5, args.steps // 2), 2)
+            import torch
+            torch.cuda.empty_cache()
     c1 = None
     if "c1" in only:
         log("config 1: DeltaNet prefill T=4096")

@@ -9,12 +9,13 @@
 // factored form scale * sum(q x) + bias * sum(x) per group on the vector
 // units, one SIMD group per row (deltanet.metal:1838-1895). Here the group
 // products run on the matrix cores: a nibble q becomes the exact bf16 value
-// 128 + q by OR-ing it into the mantissa of 0x4300 (128.0), so one
-// v_mfma_f32_16x16x32_bf16 yields P = sum (128 + q) x over 32 columns, and
+// 128 + q by OR-ing it into the mantissa of 0x4300 (128.0), so an MFMA over
+// those operands yields P = sum (128 + q) x, and
 //   sum_c W x = s * P + (b - 128 s) * sum(x)       (per group, per row)
-// with sum(x) over the same bf16-rounded x the MFMA saw. A wave owns a
-// 16-row x 16-column output tile and walks the groups; each group's scale
-// and folded bias come from LDS, staged once per workgroup.
+// with sum(x) over the same bf16-rounded x the MFMA saw. Two kernels:
+// q4_gemv_kernel for decode batches (<= 32 tokens), streaming each weight row
+// once with the K dimension split over a workgroup's waves, and
+// q4_gemm_kernel for many tokens (prefill projections), tiled 128 x 128.
 #include "common.hpp"
 #include "internal.hpp"
 #include "mfma.hpp"
@@ -44,96 +45,138 @@ __global__ __launch_bounds__(256) void q4_dequant_kernel(const uint32_t* __restr
     o[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// 8 nibbles -> 4 dwords of bf16 pairs holding 128 + q (exact).
-__device__ __forceinline__ u32x4_t q4_to_bf16_offset(uint32_t w) {
+constexpr int kQ4MaxGroups = 64;  // cols <= 4096
+
+// 8 nibbles -> bf16 128 + q in the k order (c0, c4, c1, c5, c2, c6, c3, c7):
+// dword j = ((w >> 4j) & 0x000F000F) | 0x43004300, two instructions each.
+__device__ __forceinline__ u32x4_t q4_to_bf16_interleaved(uint32_t w) {
     u32x4_t r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = 0x43004300u | ((w >> (8 * i)) & 0xFu) | (((w >> (8 * i + 4)) & 0xFu) << 16);
+    for (int j = 0; j < 4; ++j) r[j] = ((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
     return r;
 }
 
-// x[m][c0 .. c0+7] as 8 bf16 (rounded when x is fp32); zeros past `batch`.
-template <int X_DT>
-__device__ __forceinline__ u32x4_t load_x8(const void* x, int m, int batch, int cols, int c0) {
-    if (m >= batch) return u32x4_t{0u, 0u, 0u, 0u};
-    const size_t off = static_cast<size_t>(m) * cols + c0;
-    if (X_DT == 1) return *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + off);
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + off);
-    const float4 a = p[0], b = p[1];
-    return u32x4_t{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+// 8 bf16 (x0 .. x7 in 4 dwords) -> (x0 x4, x1 x5, x2 x6, x3 x7)
+__device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
+    return u32x4_t{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                   __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
 }
 
-template <int X_DT>
-__device__ __forceinline__ float load_x_rounded(const void* x, size_t i) {
-    if (X_DT == 1) return bf16_to_f32(static_cast<const uint16_t*>(x)[i]);
-    return bf16_to_f32(f32_to_bf16(static_cast<const float*>(x)[i]));
-}
+// ---- decode-shaped product (batch <= 32) ---------------------------------------
+//
+// One workgroup per 16 weight rows, the K dimension split over its eight
+// waves (wave w: groups w*ceil(G/8) .. ), all batch tiles of 16 tokens in the
+// same pass. A lane issues every load it needs up front: 8 bytes of its row
+// per group (the words 2kb, 2kb+1: MFMA k step 0 takes the even words, step 1
+// the odd ones) and the 16 x values of the same columns per batch tile; the
+// scales and folded biases of the 16 rows go to LDS first. Per group: P =
+// sum (128 + q) x on the matrix cores, the group sum of x from the same
+// registers (plus two shuffles), acc += s P + (b - 128 s) sum(x) in fp32.
+// The eight partial sums meet in LDS.
+constexpr int kQ4GemvWaves = 8;
+constexpr int kQ4GemvMaxGroupsPerWave = kQ4MaxGroups / kQ4GemvWaves;
 
-constexpr int kQ4MaxGroups = 64;  // cols <= 4096
-
-// grid (ceil(rows/64), ceil(batch/16)), 256 threads: wave w owns rows
-// blockIdx.x*64 + 16w .. +15 and batch columns blockIdx.y*16 .. +15.
-template <int SB_DT, int X_DT, int Y_DT>
-__global__ __launch_bounds__(256) void q4_matmul_mfma_kernel(
-    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const void* __restrict__ x, void* __restrict__ y, int rows, int cols, int batch) {
-    const int G = cols / 64;
+template <int SB_DT, int X_DT, int Y_DT, int NBT>
+__global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(const uint32_t* __restrict__ w,
+                                                                    const uint16_t* __restrict__ scales,
+                                                                    const uint16_t* __restrict__ biases,
+                                                                    const void* __restrict__ x, void* __restrict__ y,
+                                                                    int rows, int cols, int batch) {
+    constexpr int NT = 64 * kQ4GemvWaves;
+    const int G = cols / 64, Gw = (G + kQ4GemvWaves - 1) / kQ4GemvWaves;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const int r0 = blockIdx.x * 64 + wave * 16;
-    const int m0 = blockIdx.y * 16;
+    const int R0 = blockIdx.x * 16;
 
-    __shared__ float xsum[16][kQ4MaxGroups];
-    __shared__ float2 sb[4][kQ4MaxGroups][16];
+    __shared__ float2 sb[16][kQ4MaxGroups];          // (s, b - 128 s) per row and group
+    __shared__ __attribute__((aligned(16))) f32x4_t part[kQ4GemvWaves][NBT][64];
 
-    for (int idx = t; idx < 16 * G; idx += 256) {
-        const int m = idx / G, g = idx % G;
-        float acc = 0.0f;
-        if (m0 + m < batch) {
-            const size_t base = static_cast<size_t>(m0 + m) * cols + g * 64;
-            for (int c = 0; c < 64; ++c) acc += load_x_rounded<X_DT>(x, base + c);
-        }
-        xsum[m][g] = acc;
+    // loads: scales/biases for LDS first, then this lane's weights and x
+    float sreg[2], breg[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int idx = min(t + NT * k, 16 * G - 1);
+        const size_t gi = static_cast<size_t>(min(R0 + idx / G, rows - 1)) * G + idx % G;
+        sreg[k] = elem<SB_DT>::load(scales, gi);
+        breg[k] = elem<SB_DT>::load(biases, gi);
     }
-    for (int idx = lane; idx < 16 * G; idx += 64) {
-        const int i = idx / G, g = idx % G;
-        float2 v = make_float2(0.0f, 0.0f);
-        if (r0 + i < rows) {
-            const size_t gi = static_cast<size_t>(r0 + i) * G + g;
-            const float s = elem<SB_DT>::load(scales, gi);
-            const float b = elem<SB_DT>::load(biases, gi);
-            v = make_float2(s, b - 128.0f * s);
+    const int g0 = wave * Gw, gn = min(Gw, G - g0);   // this wave's groups (gn may be <= 0)
+    const uint32_t* wrow = w + static_cast<size_t>(min(R0 + n, rows - 1)) * (cols / 8) + 2 * kb;
+    u32x2_t wv[kQ4GemvMaxGroupsPerWave];
+    u32x4_t xv[kQ4GemvMaxGroupsPerWave][NBT][2];
+#pragma unroll
+    for (int i = 0; i < kQ4GemvMaxGroupsPerWave; ++i) {
+        if (i < gn) {
+            const int g = g0 + i;
+            wv[i] = *reinterpret_cast<const u32x2_t*>(wrow + 8 * g);
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                const size_t xo = static_cast<size_t>(min(16 * bt + n, batch - 1)) * cols + 64 * g + 16 * kb;
+                if (X_DT == 1) {
+                    xv[i][bt][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
+                    xv[i][bt][1] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8);
+                } else {
+                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo);
+                    const float4 e0 = p[0], e1 = p[1], e2 = p[2], e3 = p[3];
+                    xv[i][bt][0] = u32x4_t{pack_bf16x2(e0.x, e0.y), pack_bf16x2(e0.z, e0.w),
+                                           pack_bf16x2(e1.x, e1.y), pack_bf16x2(e1.z, e1.w)};
+                    xv[i][bt][1] = u32x4_t{pack_bf16x2(e2.x, e2.y), pack_bf16x2(e2.z, e2.w),
+                                           pack_bf16x2(e3.x, e3.y), pack_bf16x2(e3.z, e3.w)};
+                }
+            }
         }
-        sb[wave][g][i] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int idx = t + NT * k;
+        if (idx < 16 * G) sb[idx / G][idx % G] = make_float2(sreg[k], breg[k] - 128.0f * sreg[k]);
     }
     __syncthreads();
 
-    const int row = min(r0 + n, rows - 1);
-    const uint32_t* wrow = w + static_cast<size_t>(row) * (cols / 8);
-    const int m = m0 + n;
-    float yacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int g = 0; g < G; ++g) {
-        f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[NBT];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int c0 = 64 * g + 32 * hf + 8 * kb;
-            const u32x4_t a = q4_to_bf16_offset(wrow[c0 / 8]);
-            const u32x4_t b = load_x8<X_DT>(x, m, batch, cols, c0);
-            P = mfma_16x16x32_bf16(a, b, P);
-        }
-        const float X = xsum[n][g];
+    for (int bt = 0; bt < NBT; ++bt) acc[bt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float2 v = sb[wave][g][4 * kb + i];
-            yacc[i] = fmaf(v.x, P[i], fmaf(v.y, X, yacc[i]));
+    for (int i = 0; i < kQ4GemvMaxGroupsPerWave; ++i) {
+        if (i >= gn) break;
+        const int g = g0 + i;
+        const u32x4_t a0 = q4_to_bf16_interleaved(wv[i][0]);
+        const u32x4_t a1 = q4_to_bf16_interleaved(wv[i][1]);
+        float2 svb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) svb[j] = sb[4 * kb + j][g];
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+            const u32x4_t x0 = xv[i][bt][0], x1 = xv[i][bt][1];
+            float xsum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xsum += (__uint_as_float(x0[j] << 16) + __uint_as_float(x0[j] & 0xffff0000u)) +
+                        (__uint_as_float(x1[j] << 16) + __uint_as_float(x1[j] & 0xffff0000u));
+            xsum += __shfl_xor(xsum, 16, 64);
+            xsum += __shfl_xor(xsum, 32, 64);
+            f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            P = mfma_16x16x32_bf16(a0, interleave8(x0), P);
+            P = mfma_16x16x32_bf16(a1, interleave8(x1), P);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[bt][j] = fmaf(svb[j].x, P[j], fmaf(svb[j].y, xsum, acc[bt][j]));
         }
     }
-    if (m < batch) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r0 + 4 * kb + i;
-            if (r < rows) elem<Y_DT>::store(y, static_cast<size_t>(m) * rows + r, yacc[i]);
+    for (int bt = 0; bt < NBT; ++bt) part[wave][bt][lane] = acc[bt];
+    __syncthreads();
+    if (wave < NBT) {
+        const int bt = wave;
+        f32x4_t v = part[0][bt][lane];
+#pragma unroll
+        for (int ww = 1; ww < kQ4GemvWaves; ++ww) v += part[ww][bt][lane];
+        const int m = 16 * bt + n;
+        if (m < batch) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = R0 + 4 * kb + j;
+                if (r < rows) elem<Y_DT>::store(y, static_cast<size_t>(m) * rows + r, v[j]);
+            }
         }
     }
 }
@@ -159,21 +202,8 @@ __global__ __launch_bounds__(256) void q4_matmul_mfma_kernel(
 // c6, c3, c7): dword j of the converted word is then
 // ((w >> 4j) & 0x000F000F) | 0x43004300 (two instructions), and the
 // activations are staged in the same order.
-constexpr int kQ4GemmMinBatch = 64;
+constexpr int kQ4GemmMinBatch = 33;
 constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
-
-__device__ __forceinline__ u32x4_t q4_to_bf16_interleaved(uint32_t w) {
-    u32x4_t r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = ((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
-    return r;
-}
-
-// 8 bf16 (x0 .. x7 in 4 dwords) -> (x0 x4, x1 x5, x2 x6, x3 x7)
-__device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
-    return u32x4_t{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
-                   __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
-}
 
 // X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
 // lane l sums half-groups l, l + 64 (32 columns each), pairs of lanes combine.
@@ -421,17 +451,21 @@ hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w,
         }
         return hipGetLastError();
     }
-    const dim3 grid((rows + 63) / 64, (batch + 15) / 16);
+    const int nbt = (batch + 15) / 16;
     ProfScope prof(ctx, stream, "q4_matmul");
-#define QFF_Q4(S, X, Y) q4_matmul_mfma_kernel<S, X, Y><<<grid, 256, 0, stream>>>(w, s, b, x, y, rows, cols, batch)
-#define QFF_Q4_Y(S, X) \
-    if (y_dtype == QFF_BF16) QFF_Q4(S, X, 1); else QFF_Q4(S, X, 0)
-#define QFF_Q4_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4_Y(S, 1); } else { QFF_Q4_Y(S, 0); }
-    if (sb_dtype == QFF_BF16) { QFF_Q4_X(1); } else { QFF_Q4_X(2); }
-#undef QFF_Q4_X
-#undef QFF_Q4_Y
-#undef QFF_Q4
+#define QFF_Q4V(S, X, Y, NB) \
+    q4_gemv_kernel<S, X, Y, NB><<<(rows + 15) / 16, 64 * kQ4GemvWaves, 0, stream>>>(w, s, b, x, y, rows, cols, batch)
+#define QFF_Q4V_B(S, X, Y) \
+    if (nbt == 1) QFF_Q4V(S, X, Y, 1); else QFF_Q4V(S, X, Y, 2)
+#define QFF_Q4V_Y(S, X) \
+    if (y_dtype == QFF_BF16) { QFF_Q4V_B(S, X, 1); } else { QFF_Q4V_B(S, X, 0); }
+#define QFF_Q4V_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4V_Y(S, 1); } else { QFF_Q4V_Y(S, 0); }
+    if (sb_dtype == QFF_BF16) { QFF_Q4V_X(1); } else { QFF_Q4V_X(2); }
+#undef QFF_Q4V_X
+#undef QFF_Q4V_Y
+#undef QFF_Q4V_B
+#undef QFF_Q4V
     return hipGetLastError();
 }
 
