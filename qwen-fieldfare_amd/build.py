@@ -24,6 +24,10 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Work-queue atomics are issued by one lane and their result is used much
+    # later; the wave-aggregating rewrite would read it back at once and so
+    # wait for every memory operation issued before it.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -39,6 +39,8 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(float));
+    L.dn_o = take(B * 4096 * sizeof(float));
+    L.sched = take(2 * kSchedSlots * sizeof(unsigned));
     const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
     L.wh = take(big); L.wl = take(big);
     L.qeh = take(big); L.qel = take(big);
@@ -156,6 +158,15 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
+    c->dn_o = reinterpret_cast<float*>(base + L.dn_o);
+    c->sched = reinterpret_cast<unsigned*>(base + L.sched);
+    c->num_cu = prop.multiProcessorCount;
+    if (hipMemset(c->sched, 0, 2 * kSchedSlots * sizeof(unsigned)) != hipSuccess) {
+        (void)hipFree(c->ws);
+        delete c;
+        (void)hipSetDevice(prev);
+        return QFF_ERR_HIP;
+    }
     c->dn = qff_dn_bufs{u16(L.wh),  u16(L.wl),  u16(L.qeh), u16(L.qel), u16(L.kth), u16(L.ktl),
                         u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam)};
     (void)hipSetDevice(prev);

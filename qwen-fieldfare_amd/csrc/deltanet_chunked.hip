@@ -34,6 +34,8 @@
 // + a_hi b_lo + a_lo b_hi, ~2^-16 relative per product), which keeps the
 // fp32 state within 1e-4 of the sequential fp32 recurrence; plain bf16
 // operands would not.
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 #include "mfma.hpp"
@@ -46,95 +48,131 @@ constexpr int kLT = 72;     // bf16 row stride of [64][64] LDS tiles (64 + 8)
 
 // ---- chunk-local pass --------------------------------------------------------
 
-// Conv input of 8 consecutive channels at stream position pos: the token's
-// projection for pos >= 0, conv-state slot pos + 4 for pos in [-3, -1].
+constexpr float kLog2e = 1.44269504088896341f;
+
+// Raw projection pair (channels ch, ch+1) as stored: two bf16 in one word,
+// or two floats.
+template <int IN_DT> struct RawPair;
+template <> struct RawPair<1> {
+    uint32_t v;
+    __device__ __forceinline__ void load(const void* p, size_t i) {
+        v = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p) + i);
+    }
+    __device__ __forceinline__ float lo() const { return __uint_as_float(v << 16); }
+    __device__ __forceinline__ float hi() const { return __uint_as_float(v & 0xffff0000u); }
+};
+template <> struct RawPair<0> {
+    float2 v;
+    __device__ __forceinline__ void load(const void* p, size_t i) {
+        v = *reinterpret_cast<const float2*>(static_cast<const float*>(p) + i);
+    }
+    __device__ __forceinline__ float lo() const { return v.x; }
+    __device__ __forceinline__ float hi() const { return v.y; }
+};
+
+// Everything one (chunk, value head) unit reads from global memory, for one
+// thread (wave w: tokens 8w .. 8w+7 of the chunk; lane l: channels 2l, 2l+1
+// of the q, k and v blocks): the conv input rows at positions tok-3 ..
+// tok+7 clamped into [0, T), the conv weights and the gate inputs of
+// token lane. Every load is unconditional and in bounds, so the loads of the
+// next unit can be issued while the current one is processed and the
+// compiler's vmcnt accounting stays exact. (The conv-state slots that
+// chunk 0 needs are read when that unit is processed.)
 template <int IN_DT>
-__device__ __forceinline__ void load_e8(const void* __restrict__ qkv, const float* __restrict__ conv_state, int ch,
-                                        int pos, float (&e)[8], bool may_precede) {
-    if (!may_precede || pos >= 0) {
-        if (IN_DT == 1) {
-            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(qkv) +
-                                                                static_cast<size_t>(pos) * 8192 + ch);
+struct UnitIn {
+    RawPair<IN_DT> r[3][11];
+    float4 w[3][2];
+    float av, bv;
+};
+
+__device__ __forceinline__ void unit_coords(int u, int& c, int& h) {
+    c = u >> 5;
+    h = u & 31;
+}
+
+template <int IN_DT>
+__device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, const void* __restrict__ qkv,
+                                           const float* __restrict__ a, const float* __restrict__ b,
+                                           const float* __restrict__ conv_w, const float* __restrict__ conv_state,
+                                           int wave, int lane) {
+    int c, h;
+    unit_coords(u, c, h);
+    const int kh = h >> 1, t0 = c * kC, tw = t0 + 8 * wave;
+    const int chs[3] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + h * 128 + 2 * lane};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                e[2 * k] = __uint_as_float(v[k] << 16);
-                e[2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
-            }
-        } else {
-            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(qkv) +
-                                                              static_cast<size_t>(pos) * 8192 + ch);
-            const float4 v0 = p[0], v1 = p[1];
-            e[0] = v0.x; e[1] = v0.y; e[2] = v0.z; e[3] = v0.w;
-            e[4] = v1.x; e[5] = v1.y; e[6] = v1.z; e[7] = v1.w;
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) in.w[p][j] = reinterpret_cast<const float4*>(conv_w)[chs[p] + j];
+#pragma unroll
+        for (int i = 0; i < 11; ++i) {
+            const int pos = min(max(tw - 3 + i, 0), T - 1);
+            in.r[p][i].load(qkv, static_cast<size_t>(pos) * 8192 + chs[p]);
         }
-    } else {
+    }
+    const size_t gi = static_cast<size_t>(min(t0 + lane, T - 1)) * 32 + h;
+    in.av = a[gi];
+    in.bv = b[gi];
+}
+
+// Conv inputs e[i][c] of pass p, channels ch + c, at positions tw-3+i: the
+// projection inside [0, T), 0 past the end; before token 0 (wave 0 of
+// chunk 0 only) the conv-state slots pos + 4.
+template <int IN_DT>
+__device__ __forceinline__ void unit_rows(const UnitIn<IN_DT>& in, int p, int tw, int T, int ch,
+                                          const float* __restrict__ conv_state, float (&e)[11][2]) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = conv_state[(ch + k) * 4 + pos + 4];
+    for (int i = 0; i < 11; ++i) {
+        const int pos = tw - 3 + i;
+        e[i][0] = pos < T ? in.r[p][i].lo() : 0.0f;
+        e[i][1] = pos < T ? in.r[p][i].hi() : 0.0f;
+    }
+    if (tw == 0) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            e[i][0] = conv_state[ch * 4 + 1 + i];
+            e[i][1] = conv_state[(ch + 1) * 4 + 1 + i];
+        }
     }
 }
 
-// y[i][k] = SiLU(conv1d) of channel ch + k at token tok0 + i (deltanet.metal
+// y[i][c] = SiLU(conv1d) of channel ch + c at token tok0 + i (deltanet.metal
 // :120-137: taps w.x .. w.w over inputs tok-3 .. tok); 0 for tokens >= T.
-// EDGE: the window may reach before token 0 (conv state) or past T - 1;
-// chunks away from both ends take the branch-free path.
-template <int IN_DT, int NT, bool EDGE>
-__device__ __forceinline__ void conv8(const void* __restrict__ qkv, const float* __restrict__ conv_state,
-                                      const float* __restrict__ conv_w, int ch, int tok0, int T,
-                                      float (&y)[NT][8]) {
-    float e[NT + 3][8];
+__device__ __forceinline__ void conv2x8(const float (&e)[11][2], const float4 (&w)[2], int tok0, int T,
+                                        float (&y)[8][2]) {
 #pragma unroll
-    for (int i = 0; i < NT + 3; ++i) {
-        const int pos = tok0 - 3 + i;
-        if (!EDGE || pos < T) {
-            load_e8<IN_DT>(qkv, conv_state, ch, pos, e[i], EDGE);
-        } else {
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) e[i][k] = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            const float v = silu_fast(e[i][c] * w[c].x + e[i + 1][c] * w[c].y + e[i + 2][c] * w[c].z +
+                                      e[i + 3][c] * w[c].w);
+            y[i][c] = tok0 + i < T ? v : 0.0f;
         }
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float4 w = reinterpret_cast<const float4*>(conv_w)[ch + k];
-#pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const float v = silu_fast(e[i][k] * w.x + e[i + 1][k] * w.y + e[i + 2][k] * w.z + e[i + 3][k] * w.w);
-            y[i][k] = !EDGE || tok0 + i < T ? v : 0.0f;
-        }
-    }
 }
 
-template <int IN_DT, int NT>
-__device__ __forceinline__ void conv8_any(bool edge, const void* __restrict__ qkv, const float* __restrict__ conv_state,
-                                          const float* __restrict__ conv_w, int ch, int tok0, int T,
-                                          float (&y)[NT][8]) {
-    if (edge)
-        conv8<IN_DT, NT, true>(qkv, conv_state, conv_w, ch, tok0, T, y);
-    else
-        conv8<IN_DT, NT, false>(qkv, conv_state, conv_w, ch, tok0, T, y);
-}
-
-// Interior chunks of bf16 input: the 7 projection rows tok0-3 .. tok0+3 of
-// 8 channels are loaded up front (one 16-B load each), so every conv pass's
-// loads are in flight together, and the conv runs from registers.
-__device__ __forceinline__ void conv_rows_bf16(const void* __restrict__ qkv, int ch, int tok0, u32x4_t (&r)[7]) {
+// Totals over the 64 lanes of a wave of eight per-lane partials, in every
+// lane: a reduce-scatter (exchanges with lane ^ 32, ^ 16, ^ 8 halve the set
+// each time), the last three butterfly steps, then one readlane per value.
+__device__ __forceinline__ void wave_sum8(const float (&p)[8], float (&tot)[8], int lane) {
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float q4[4], q2[2];
 #pragma unroll
-    for (int i = 0; i < 7; ++i)
-        r[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(qkv) +
-                                                 static_cast<size_t>(tok0 - 3 + i) * 8192 + ch);
-}
-
-__device__ __forceinline__ void conv_from_rows(const u32x4_t (&r)[7], const float* __restrict__ conv_w, int ch,
-                                               float (&y)[4][8]) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float4 w = reinterpret_cast<const float4*>(conv_w)[ch + k];
-        float e[7];
-#pragma unroll
-        for (int i = 0; i < 7; ++i)
-            e[i] = (k & 1) ? __uint_as_float(r[i][k >> 1] & 0xffff0000u) : __uint_as_float(r[i][k >> 1] << 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) y[i][k] = silu_fast(e[i] * w.x + e[i + 1] * w.y + e[i + 2] * w.z + e[i + 3] * w.w);
+    for (int j = 0; j < 4; ++j) {
+        const float keep = b5 ? p[4 + j] : p[j], give = b5 ? p[j] : p[4 + j];
+        q4[j] = keep + __shfl_xor(give, 32, 64);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float keep = b4 ? q4[2 + j] : q4[j], give = b4 ? q4[j] : q4[2 + j];
+        q2[j] = keep + __shfl_xor(give, 16, 64);
+    }
+    float q1 = (b3 ? q2[1] : q2[0]) + __shfl_xor(b3 ? q2[0] : q2[1], 8, 64);
+    q1 += __shfl_xor(q1, 4, 64);
+    q1 += __shfl_xor(q1, 2, 64);
+    q1 += __shfl_xor(q1, 1, 64);
+    // lane L now holds the total of value (L >> 3) & 7
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        tot[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q1), 8 * j));
 }
 
 // Splits 8 floats into bf16 hi / lo and stores 16 B of each.
@@ -156,10 +194,18 @@ template <int K>
 __device__ __forceinline__ int swz(int r, int k8) {
     return ((r >> 4) * (K / 32) + (k8 >> 2)) * 64 + (k8 & 3) * 16 + (r & 15);
 }
+// Its inverse: piece p -> (r, k8). Writers walk p with the thread index, so
+// each store instruction covers one contiguous 1 KB block.
+template <int K>
+__device__ __forceinline__ void unswz(int p, int& r, int& k8) {
+    const int q = p >> 6;
+    r = (q / (K / 32)) * 16 + (p & 15);
+    k8 = (q % (K / 32)) * 4 + ((p >> 4) & 3);
+}
 
 // LDS carve-up of the chunk-local kernel (bytes)
 constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
-constexpr int kOffK = 0;                          // K hi, lo; then X = beta e^G K; then P W (fp32)
+constexpr int kOffK = 0;                          // K hi, lo; then X = beta e^G K; then P W, Qe (fp32)
 constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T (fp32) + scratch; then W hi, lo
 constexpr int kOffV = 4 * kTile128;               // beta V hi, lo
 constexpr int kOffA = 6 * kTile128;               // A fp32 [64][65]
@@ -167,21 +213,31 @@ constexpr int kOffT = kOffA + kC * 65 * 4;        // P hi, lo, then T hi, lo, th
 constexpr int kOffG = kOffT + 2 * kC * kLT * 2;   // G[64], beta[64]
 constexpr int kLocalSmem = kOffG + 2 * kC * 4;
 
-// grid (ceil(T/64), 32 value heads), 256 threads.
+// Persistent: grid = min(units, CUs) workgroups of 512 threads (eight
+// waves, two per SIMD) walk the (chunk, value head) units. Units 0 .. 2g-1
+// go out statically (g = grid size), the rest through an atomic counter, so
+// a workgroup on a CU that runs slow (or shares its XCD with other work)
+// simply takes fewer units; the launch's last workgroup resets the counter.
+// While a unit is processed the inputs of the workgroup's next unit are
+// already loading into registers (UnitIn).
+// Conv passes map wave w to tokens 8w .. 8w+7 and lane l to channels 2l,
+// 2l+1 of a 128-channel block, so a lane's 8 tokens of a channel are one
+// K~^T operand piece and each conv input row is one 256-B load per wave.
+// Every global load of a unit is issued before its first global store: on
+// gfx950 vmcnt counts stores too, so a load consumed after stores would
+// wait for them.
+constexpr int kLocalThreads = 512;
+
 template <int IN_DT>
-__global__ __launch_bounds__(256) void dn_chunk_local_kernel(
+__global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     int T, const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ a_log, const float* __restrict__ dt_bias, const float* __restrict__ conv_w,
-    const float* __restrict__ conv_state, qff_dn_bufs out) {
-    const int c = blockIdx.x, h = blockIdx.y, kh = h >> 1;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = lane & 15, kb = lane >> 4;
-    const int t0 = c * kC;
-    const int nv = min(kC, T - t0);
-    const size_t ch = static_cast<size_t>(c) * 32 + h;
-    const bool edge = c == 0 || t0 + kC > T;   // conv window leaves [0, T)
+    const float* __restrict__ conv_state, qff_dn_bufs out, unsigned* __restrict__ sched) {
+    const int units = ((T + kC - 1) / kC) * 32;
+    const int grid = gridDim.x;
 
     __shared__ __attribute__((aligned(16))) unsigned char smem[kLocalSmem];
+    __shared__ int s_next;
     uint16_t* Kh = reinterpret_cast<uint16_t*>(smem + kOffK);
     uint16_t* Kl = Kh + kC * kLD;
     uint16_t* Qh = reinterpret_cast<uint16_t*>(smem + kOffQ);
@@ -194,137 +250,174 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
     float* G = reinterpret_cast<float*>(smem + kOffG);
     float* Bt = G + kC;
 
-    // Conv passes: thread -> channels 8oc .. 8oc+7 of a 128-channel block x
-    // tokens 4g .. 4g+3 (q and k of key head kh, v of value head h).
-    const int oc = t & 15, g = t >> 4;
-    const bool fast = IN_DT == 1 && !edge;
-    u32x4_t rq[7], rk[7], rv[7];
-    if (fast) {
-        conv_rows_bf16(qkv, kh * 128 + 8 * oc, t0 + 4 * g, rq);
-        conv_rows_bf16(qkv, 2048 + kh * 128 + 8 * oc, t0 + 4 * g, rk);
-        conv_rows_bf16(qkv, 4096 + h * 128 + 8 * oc, t0 + 4 * g, rv);
-    }
-    auto conv = [&](const u32x4_t (&r)[7], int chn, float (&y)[4][8]) {
-        if (fast)
-            conv_from_rows(r, conv_w, chn, y);
-        else
-            conv8_any<IN_DT, 4>(edge, qkv, conv_state, conv_w, chn, t0 + 4 * g, T, y);
-    };
-    // L2 norm per token over the 16 lanes of its head (deltanet.metal
-    // :282-305), q then / sqrt(128); into LDS as bf16 hi/lo.
-    auto l2norm_store = [&](float (&y)[4][8], bool isq, uint16_t* dh, uint16_t* dl) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) ss += y[i][k] * y[i][k];
-            ss = group_sum<16>(ss);
-            const float inv = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) y[i][k] = isq ? (y[i][k] * inv) * (1.0f / sqrtf(128.0f)) : y[i][k] * inv;
-            store_split8(dh + (4 * g + i) * kLD + 8 * oc, dl + (4 * g + i) * kLD + 8 * oc, y[i]);
-        }
-    };
+    int u = blockIdx.x, un = blockIdx.x + grid;
+    UnitIn<IN_DT> in;
+    fetch_unit<IN_DT>(in, u, T, qkv, a, b, conv_w, conv_state, threadIdx.x >> 6, threadIdx.x & 63);
+    if (threadIdx.x == 0) s_next = 2 * grid + static_cast<int>(atomicAdd(sched, 1u));
+    // Wait here for the first unit's loads: the loop's own waits then only
+    // count the operations of the previous iteration, which issues stores
+    // after its prefetch, so consuming the prefetch does not wait for them.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    while (u < units) {
+    // thread coordinates re-derived in every iteration through an opaque
+    // copy, so the compiler recomputes the index arithmetic built on them
+    // where it is used instead of keeping it live across the whole loop
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    const int lane = t & 63, wave = t >> 6;
+    const int n = lane & 15, kb = lane >> 4;
+    const int rt = wave & 3, role = wave >> 2;   // MFMA row tile; which of a wave pair's two products
+    int c, h;
+    unit_coords(u, c, h);
+    const int kh = h >> 1;
+    const int t0 = c * kC;
+    const int nv = min(kC, T - t0);
+    const size_t ch = static_cast<size_t>(u);    // == c * 32 + h
+    const int tw = t0 + 8 * wave;                  // this wave's first token
 
     // gates (deltanet.metal:250-280): log g = -e^{A_log} softplus(a + dt_bias),
     // beta = sigmoid(b); G = inclusive prefix sum over the chunk. Padded
     // tokens have log g = 0 and beta = 0, so they change nothing.
     if (wave == 0) {
         const bool ok = lane < nv;
-        const size_t gi = static_cast<size_t>(t0 + lane) * 32 + h;
-        float x = ok ? -expf(a_log[h]) * softplus(a[gi] + dt_bias[h]) : 0.0f;
+        float x = ok ? -expf(a_log[h]) * softplus(in.av + dt_bias[h]) : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o, 64);
             if (lane >= o) x += y;
         }
         G[lane] = x;
-        Bt[lane] = ok ? sigmoid(b[gi]) : 0.0f;
+        Bt[lane] = ok ? sigmoid(in.bv) : 0.0f;
         if (lane == 63) out.gam[ch] = expf(x);
     }
-    float qn[4][8], kn[4][8];
-    conv(rq, kh * 128 + 8 * oc, qn);
-    l2norm_store(qn, true, Qh, Ql);
-    conv(rk, 2048 + kh * 128 + 8 * oc, kn);
-    l2norm_store(kn, false, Kh, Kl);
+    const int chs[3] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + h * 128 + 2 * lane};
+    auto conv = [&](int p, float (&y)[8][2]) {
+        float e[11][2];
+        unit_rows<IN_DT>(in, p, tw, T, chs[p], conv_state, e);
+        conv2x8(e, in.w[p], tw, T, y);
+    };
+
+    // ---- conv + SiLU, L2 norms over each token's 128 channels (deltanet.metal
+    // :282-305, q then / sqrt(128)); q, k to LDS as bf16 hi/lo ---------------
+    auto norm_store = [&](float (&y)[8][2], float post, uint16_t* dh, uint16_t* dl) {
+        float ss[8], tot[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss[i] = y[i][0] * y[i][0] + y[i][1] * y[i][1];
+        wave_sum8(ss, tot, lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float inv = 1.0f / sqrtf(tot[i] + 1e-6f);
+            y[i][0] = (y[i][0] * inv) * post;
+            y[i][1] = (y[i][1] * inv) * post;
+            uint32_t hh, ll;
+            split_bf16x2(y[i][0], y[i][1], hh, ll);
+            const int o = (8 * wave + i) * kLD + 2 * lane;
+            *reinterpret_cast<uint32_t*>(dh + o) = hh;
+            *reinterpret_cast<uint32_t*>(dl + o) = ll;
+        }
+    };
+    float qn[8][2], kn[8][2], vn[8][2];
+    conv(0, qn);
+    norm_store(qn, 1.0f / sqrtf(128.0f), Qh, Ql);
+    conv(1, kn);
+    norm_store(kn, 1.0f, Kh, Kl);
+    conv(2, vn);
+    // the unit after next, and the next unit's inputs (the unit index is
+    // clamped, so the loads stay in bounds when the queue has run out)
+    const int unn = s_next;
+    fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, conv_w, conv_state, wave, lane);
     __syncthreads();
-    // K~^T rows 8oc .. 8oc+7, tokens 4g .. 4g+3 (half of an operand piece)
+    // grabbed now, published at the end of the unit, when it has long arrived
+    unsigned grabbed = 0;
+    if (t == 0) grabbed = atomicAdd(sched, 1u);
+
+    // ---- K~^T out (channels 2l, 2l+1 x this wave's 8 tokens: one operand
+    // piece each), beta v to LDS, Q~ = e^G q kept for Qe ------------------------
     {
         const float gc = G[kC - 1];
-        float sk[4];
+        float gw[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sk[i] = expf(gc - G[4 * g + i]);
+        for (int i = 0; i < 8; ++i) gw[i] = G[8 * wave + i];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            uint32_t h0, l0, h1, l1;
-            split_bf16x2(sk[0] * kn[0][k], sk[1] * kn[1][k], h0, l0);
-            split_bf16x2(sk[2] * kn[2][k], sk[3] * kn[3][k], h1, l1);
-            const size_t o = ch * 128 * kC + 8 * swz<kC>(8 * oc + k, g >> 1) + 4 * (g & 1);
-            *reinterpret_cast<u32x2_t*>(out.kth + o) = u32x2_t{h0, h1};
-            *reinterpret_cast<u32x2_t*>(out.ktl + o) = u32x2_t{l0, l1};
+        for (int cc = 0; cc < 2; ++cc) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                split_bf16x2(__builtin_amdgcn_exp2f((gc - gw[2 * j]) * kLog2e) * kn[2 * j][cc],
+                             __builtin_amdgcn_exp2f((gc - gw[2 * j + 1]) * kLog2e) * kn[2 * j + 1][cc], hw[j], lw[j]);
+            const size_t o = ch * 128 * kC + 8 * swz<kC>(2 * lane + cc, wave);
+            *reinterpret_cast<u32x4_t*>(out.kth + o) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+            *reinterpret_cast<u32x4_t*>(out.ktl + o) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
         }
-    }
-    // beta v of value head h
-    {
-        float y[4][8];
-        conv(rv, 4096 + h * 128 + 8 * oc, y);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 4 * g + i;
-            const float bb = Bt[row];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) y[i][k] *= bb;
-            store_split8(Vh + row * kLD + 8 * oc, Vl + row * kLD + 8 * oc, y[i]);
+        for (int i = 0; i < 8; ++i) {
+            const float bb = Bt[8 * wave + i];
+            uint32_t hh, ll;
+            split_bf16x2(bb * vn[i][0], bb * vn[i][1], hh, ll);
+            const int o = (8 * wave + i) * kLD + 2 * lane;
+            *reinterpret_cast<uint32_t*>(Vh + o) = hh;
+            *reinterpret_cast<uint32_t*>(Vl + o) = ll;
+            const float eg = __builtin_amdgcn_exp2f(gw[i] * kLog2e);
+            qn[i][0] *= eg;
+            qn[i][1] *= eg;
         }
-    }
-    // Q~ = e^G q, kept for Qe
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float eg = expf(G[4 * g + i]);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) qn[i][k] *= eg;
     }
     __syncthreads();
 
-    // K K^T -> A (strictly lower, scaled), Q K^T -> P (lower incl. diagonal)
+    // ---- waves 0-3: K K^T -> A (strictly lower, scaled); waves 4-7: Q K^T ->
+    // P (lower incl. diagonal); row tile rt each ---------------------------------
     {
-        f32x4_t kk[1][4], qk[1][4];
+        f32x4_t acc[1][4];
 #pragma unroll
-        for (int cj = 0; cj < 4; ++cj) kk[0][cj] = qk[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<128, 1, 4, false>(kk, Kh, Kl, kLD, 16 * wave, Kh, Kl, kLD, 0, lane);
-        mma_block_x3<128, 1, 4, false>(qk, Qh, Ql, kLD, 16 * wave, Kh, Kl, kLD, 0, lane);
+        for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
+        float gi[4], bi[4], gj[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            gi[ii] = G[16 * rt + 4 * kb + ii] * kLog2e;
+            bi[ii] = Bt[16 * rt + 4 * kb + ii];
+            gj[ii] = G[16 * ii + n] * kLog2e;
+        }
 #pragma unroll
         for (int cj = 0; cj < 4; ++cj) {
             const int j = 16 * cj + n;
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int i = 16 * wave + 4 * kb + ii;
-                const float decay = j <= i ? expf(G[i] - G[j]) : 0.0f;
-                Am[i * 65 + j] = j < i ? Bt[i] * decay * kk[0][cj][ii] : 0.0f;
-                uint16_t hh, ll;
-                split_bf16(decay * qk[0][cj][ii], hh, ll);
-                Th[i * kLT + j] = hh;
-                Tl[i * kLT + j] = ll;
+                const int i = 16 * rt + 4 * kb + ii;
+                // e^{G_i - G_j}; for j > i the product is discarded by the select
+                const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * acc[0][cj][ii];
+                if (role == 0) {
+                    Am[i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
+                } else {
+                    uint16_t hh, ll;
+                    split_bf16(j <= i ? v : 0.0f, hh, ll);
+                    Th[i * kLT + j] = hh;
+                    Tl[i * kLT + j] = ll;
+                }
             }
         }
     }
     __syncthreads();
-    // P out, 16 B per thread and piece; the pieces stay in registers until
-    // the T region is free again
-    u32x4_t pkeep[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
-        pkeep[k] = *reinterpret_cast<const u32x4_t*>((arr ? Tl : Th) + row * kLT + c8);
-        *reinterpret_cast<u32x4_t*>((arr ? out.pl : out.ph) + ch * kC * kC + 8 * swz<kC>(row, q & 7)) = pkeep[k];
+    // ---- P out, one coalesced 1 KB block per wave and array; the pieces stay in
+    // registers until the T region is free again --------------------------------
+    u32x4_t pkeep[2];
+    {
+        int row, k8;
+        unswz<kC>(t, row, k8);
+        pkeep[0] = *reinterpret_cast<const u32x4_t*>(Th + row * kLT + 8 * k8);
+        pkeep[1] = *reinterpret_cast<const u32x4_t*>(Tl + row * kLT + 8 * k8);
+        *reinterpret_cast<u32x4_t*>(out.ph + ch * kC * kC + 8 * t) = pkeep[0];
+        *reinterpret_cast<u32x4_t*>(out.pl + ch * kC * kC + 8 * t) = pkeep[1];
     }
     // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
-    //   diagonal blocks by forward substitution, one wave each;
+    //   diagonal blocks by forward substitution, waves 0-3 one each;
     //   T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i > j, wave j walking
     //   column block j downwards (fp32 MFMA 16x16x4).
     float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [64][65] (Q is consumed)
-    float* scr = reinterpret_cast<float*>(smem + kOffQ + kTile128) + wave * (16 * 17);
-    {
+    float* scr = reinterpret_cast<float*>(smem + kOffQ + kTile128) + rt * (16 * 17);
+    if (role == 0) {
         const int bi = wave;
         if (lane < 16) {
             float tc[16];
@@ -337,7 +430,9 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
                 Tm[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
             }
         }
+    } else {
         // blocks right of the diagonal are zero
+        const int bi = rt;
         for (int idx = lane; idx < 16 * (48 - 16 * bi); idx += 64) {
             const int i = idx / (48 - 16 * bi), j = 16 * (bi + 1) + idx % (48 - 16 * bi);
             Tm[(16 * bi + i) * 65 + j] = 0.0f;
@@ -361,8 +456,8 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
-    // T -> bf16 hi/lo; X = beta e^G K in place of K
-    for (int idx = t; idx < kC * kC; idx += 256) {
+    // ---- T -> bf16 hi/lo; X = beta e^G K in place of K --------------------------
+    for (int idx = t; idx < kC * kC; idx += kLocalThreads) {
         const int i = idx >> 6, j = idx & 63;
         uint16_t hh, ll;
         split_bf16(Tm[i * 65 + j], hh, ll);
@@ -370,9 +465,9 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         Tl[i * kLT + j] = ll;
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int q = t + 256 * k, row = q >> 4, c8 = 8 * (q & 15);
-        const float s = Bt[row] * expf(G[row]);
+    for (int k = 0; k < 2; ++k) {
+        const int q = t + kLocalThreads * k, row = q >> 4, c8 = 8 * (q & 15);
+        const float s = Bt[row] * __builtin_amdgcn_exp2f(G[row] * kLog2e);
         const u32x4_t hv = *reinterpret_cast<const u32x4_t*>(Kh + row * kLD + c8);
         const u32x4_t lv = *reinterpret_cast<const u32x4_t*>(Kl + row * kLD + c8);
         float x[8];
@@ -384,78 +479,103 @@ __global__ __launch_bounds__(256) void dn_chunk_local_kernel(
         store_split8(Kh + row * kLD + c8, Kl + row * kLD + c8, x);
     }
     __syncthreads();
-    // W = T X -> LDS (Q region); U~ = T (beta V) -> U~^T out.
-    // Wave -> row tile (16 tokens), 8 column tiles of 16 dims in two halves.
+    // ---- waves 0-3: W = T X -> LDS (Q region); waves 4-7: U~ = T (beta V) ->
+    // U~^T out. Row tile rt (16 tokens), 8 column tiles of 16 dims in two
+    // halves. -----------------------------------------------------------------
     uint16_t* Wh = Qh;
     uint16_t* Wl = Ql;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-        f32x4_t w[1][4], u[1][4];
+        f32x4_t w[1][4];
 #pragma unroll
-        for (int cd = 0; cd < 4; ++cd) w[0][cd] = u[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * wave, Kh, Kl, kLD, 64 * half, lane);
-        mma_block_x3<kC, 1, 4, true>(u, Th, Tl, kLT, 16 * wave, Vh, Vl, kLD, 64 * half, lane);
+        for (int cd = 0; cd < 4; ++cd) w[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * rt, role ? Vh : Kh, role ? Vl : Kl, kLD, 64 * half, lane);
 #pragma unroll
         for (int cd = 0; cd < 4; ++cd) {
             const int d = 64 * half + 16 * cd + n;
-            uint16_t uh4[4], ul4[4];
+            uint16_t h4[4], l4[4];
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int i = 16 * wave + 4 * kb + ii;
-                uint16_t hh, ll;
-                split_bf16(w[0][cd][ii], hh, ll);
-                Wh[i * kLD + d] = hh;
-                Wl[i * kLD + d] = ll;
-                split_bf16(u[0][cd][ii], uh4[ii], ul4[ii]);
+            for (int ii = 0; ii < 4; ++ii) split_bf16(w[0][cd][ii], h4[ii], l4[ii]);
+            if (role == 0) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const int i = 16 * rt + 4 * kb + ii;
+                    Wh[i * kLD + d] = h4[ii];
+                    Wl[i * kLD + d] = l4[ii];
+                }
+            } else {
+                const size_t o = (ch * 128 + d) * kC + 16 * rt + 4 * kb;
+                *reinterpret_cast<u32x2_t*>(out.uth + o) =
+                    u32x2_t{h4[0] | (static_cast<uint32_t>(h4[1]) << 16), h4[2] | (static_cast<uint32_t>(h4[3]) << 16)};
+                *reinterpret_cast<u32x2_t*>(out.utl + o) =
+                    u32x2_t{l4[0] | (static_cast<uint32_t>(l4[1]) << 16), l4[2] | (static_cast<uint32_t>(l4[3]) << 16)};
             }
-            const size_t o = (ch * 128 + d) * kC + 16 * wave + 4 * kb;
-            *reinterpret_cast<u32x2_t*>(out.uth + o) =
-                u32x2_t{uh4[0] | (static_cast<uint32_t>(uh4[1]) << 16), uh4[2] | (static_cast<uint32_t>(uh4[3]) << 16)};
-            *reinterpret_cast<u32x2_t*>(out.utl + o) =
-                u32x2_t{ul4[0] | (static_cast<uint32_t>(ul4[1]) << 16), ul4[2] | (static_cast<uint32_t>(ul4[3]) << 16)};
         }
     }
     __syncthreads();
-    // W out; P back into the T region (T is consumed)
+    // ---- W out (coalesced); P back into the T region (T is consumed) ------------
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int q = t + 256 * k, arr = q >> 10, row = (q & 1023) >> 4, c8 = 8 * (q & 15);
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((arr ? Wl : Wh) + row * kLD + c8);
-        *reinterpret_cast<u32x4_t*>((arr ? out.wl : out.wh) + ch * kC * 128 + 8 * swz<128>(row, q & 15)) = v;
+    for (int k = 0; k < 2; ++k) {
+        const int p = t + kLocalThreads * k;
+        int row, k8;
+        unswz<128>(p, row, k8);
+        const u32x4_t vh = *reinterpret_cast<const u32x4_t*>(Wh + row * kLD + 8 * k8);
+        const u32x4_t vl = *reinterpret_cast<const u32x4_t*>(Wl + row * kLD + 8 * k8);
+        *reinterpret_cast<u32x4_t*>(out.wh + ch * kC * 128 + 8 * p) = vh;
+        *reinterpret_cast<u32x4_t*>(out.wl + ch * kC * 128 + 8 * p) = vl;
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int q = t + 256 * k, arr = q >> 9, row = (q & 511) >> 3, c8 = 8 * (q & 7);
-        *reinterpret_cast<u32x4_t*>((arr ? Tl : Th) + row * kLT + c8) = pkeep[k];
+    {
+        int row, k8;
+        unswz<kC>(t, row, k8);
+        *reinterpret_cast<u32x4_t*>(Th + row * kLT + 8 * k8) = pkeep[0];
+        *reinterpret_cast<u32x4_t*>(Tl + row * kLT + 8 * k8) = pkeep[1];
     }
     __syncthreads();
-    // P W -> fp32 [64][132] in the K region (X is consumed)
+    // ---- P W -> fp32 [64][132] in the K region (X is consumed); wave -> row
+    // tile rt, column half `role` -----------------------------------------------
     float* PW = reinterpret_cast<float*>(smem + kOffK);
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    {
         f32x4_t pw[1][4];
 #pragma unroll
         for (int cd = 0; cd < 4; ++cd) pw[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<kC, 1, 4, true>(pw, Th, Tl, kLT, 16 * wave, Wh, Wl, kLD, 64 * half, lane);
+        mma_block_x3<kC, 1, 4, true>(pw, Th, Tl, kLT, 16 * rt, Wh, Wl, kLD, 64 * role, lane);
 #pragma unroll
         for (int cd = 0; cd < 4; ++cd)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii)
-                PW[(16 * wave + 4 * kb + ii) * 132 + 64 * half + 16 * cd + n] = pw[0][cd][ii];
+                PW[(16 * rt + 4 * kb + ii) * 132 + 64 * role + 16 * cd + n] = pw[0][cd][ii];
     }
     __syncthreads();
-    // Qe = Q~ - P W
+    // ---- Qe = Q~ - P W, in place (each thread its own channel pairs) -----------
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = 4 * g + i;
-        const float4 p0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc);
-        const float4 p1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * oc + 4);
-        const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        float y[8];
+    for (int i = 0; i < 8; ++i) {
+        float2* pp = reinterpret_cast<float2*>(PW + (8 * wave + i) * 132 + 2 * lane);
+        const float2 pw = *pp;
+        *pp = make_float2(qn[i][0] - pw.x, qn[i][1] - pw.y);
+    }
+    __syncthreads();
+    // ---- Qe out (coalesced) -----------------------------------------------------
 #pragma unroll
-        for (int k = 0; k < 8; ++k) y[k] = qn[i][k] - pw[k];
-        const size_t o = ch * kC * 128 + 8 * swz<128>(row, oc);
+    for (int k = 0; k < 2; ++k) {
+        const int p = t + kLocalThreads * k;
+        int row, k8;
+        unswz<128>(p, row, k8);
+        const float4 v0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * k8);
+        const float4 v1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * k8 + 4);
+        const float y[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const size_t o = ch * kC * 128 + 8 * p;
         store_split8(out.qeh + o, out.qel + o, y);
+    }
+    if (t == 0) s_next = 2 * grid + static_cast<int>(grabbed);
+    __syncthreads();
+    u = un;
+    un = unn;
+    }
+    // the last workgroup out resets the queue for the next launch (every
+    // workgroup has finished taking units by then)
+    if (threadIdx.x == 0 && atomicAdd(sched + 1, 1u) == static_cast<unsigned>(grid - 1)) {
+        atomicExch(sched, 0u);
+        atomicExch(sched + 1, 0u);
     }
 }
 
@@ -630,13 +750,15 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
     const int nch = (T + kC - 1) / kC;
     {
         ProfScope prof(ctx, stream, "dn_chunk_local");
-        const dim3 grid(nch, 32);
+        const int units = nch * 32;
+        const int grid = std::min(units, std::max(ctx->num_cu, 1));
+        unsigned* sched = ctx->sched + 2 * kSchedChunkLocal;
         if (in_dtype == QFF_BF16)
-            dn_chunk_local_kernel<1><<<grid, 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
-                                                               conv_state, ctx->dn);
+            dn_chunk_local_kernel<1><<<grid, kLocalThreads, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias,
+                                                                         p->conv_w, conv_state, ctx->dn, sched);
         else
-            dn_chunk_local_kernel<0><<<grid, 256, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
-                                                               conv_state, ctx->dn);
+            dn_chunk_local_kernel<0><<<grid, kLocalThreads, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias,
+                                                                         p->conv_w, conv_state, ctx->dn, sched);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
     dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);

@@ -45,6 +45,12 @@ struct qff_ctx {
     // chunk intermediates.
     float* pf_o = nullptr;
     qff_dn_bufs dn{};
+    // DeltaNet decode: pre-norm outputs [max_batch][32][128] fp32.
+    float* dn_o = nullptr;
+    // Work-queue counters of the persistent kernels, zero between launches
+    // (each launch's last workgroup resets its pair); kSchedSlots pairs.
+    unsigned* sched = nullptr;
+    int num_cu = 0;
     // Kernel timing (qff_profile_enable): a pool of event pairs.
     bool prof = false;
     std::vector<qff_prof_record> prof_pool;
@@ -54,10 +60,12 @@ struct qff_ctx {
 namespace qff {
 
 constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head)
+constexpr int kSchedSlots = 8;         // work-queue counter pairs in the context
+constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, pf_o, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

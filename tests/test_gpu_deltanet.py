@@ -35,7 +35,7 @@ def _oracle_decode(p, inp, in_f32=False):
     return np.stack(outs), np.stack(convs), np.stack(ssms)
 
 
-@pytest.mark.parametrize("B", [1, 3, 16])
+@pytest.mark.parametrize("B", [1, 3, 16, 20])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
     import qff
@@ -58,12 +58,13 @@ def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
     assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
 
 
-def test_deltanet_decode_f32_inputs_and_repeat(hip):
+@pytest.mark.parametrize("B", [4, 6])
+def test_deltanet_decode_f32_inputs_and_repeat(hip, B):
     """fp32 activations, and three steps in a row on the same context and
-    state buffers."""
+    state buffers (batch 4 takes the two-launch split, 6 the one-launch
+    kernel)."""
     import qff
     p = synth.deltanet_params()
-    B = 4
     inp = synth.deltanet_decode_inputs(B, seed=7)
     ctx = qff.Context(max_batch=8, max_prefill_tokens=1)
     conv = f32_tensor(inp["conv_state"])
