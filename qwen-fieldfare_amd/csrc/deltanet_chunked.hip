@@ -115,16 +115,17 @@ __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, cons
 }
 
 // Conv inputs e[i][c] of pass p, channels ch + c, at positions tw-3+i: the
-// projection inside [0, T), 0 past the end; before token 0 (wave 0 of
-// chunk 0 only) the conv-state slots pos + 4.
-template <int IN_DT>
+// projection inside [0, T), 0 past the end (TAIL: the chunk reaches past
+// T - 1); before token 0 (wave 0 of chunk 0 only) the conv-state slots
+// pos + 4.
+template <int IN_DT, bool TAIL>
 __device__ __forceinline__ void unit_rows(const UnitIn<IN_DT>& in, int p, int tw, int T, int ch,
                                           const float* __restrict__ conv_state, float (&e)[11][2]) {
 #pragma unroll
     for (int i = 0; i < 11; ++i) {
         const int pos = tw - 3 + i;
-        e[i][0] = pos < T ? in.r[p][i].lo() : 0.0f;
-        e[i][1] = pos < T ? in.r[p][i].hi() : 0.0f;
+        e[i][0] = !TAIL || pos < T ? in.r[p][i].lo() : 0.0f;
+        e[i][1] = !TAIL || pos < T ? in.r[p][i].hi() : 0.0f;
     }
     if (tw == 0) {
 #pragma unroll
@@ -137,6 +138,7 @@ __device__ __forceinline__ void unit_rows(const UnitIn<IN_DT>& in, int p, int tw
 
 // y[i][c] = SiLU(conv1d) of channel ch + c at token tok0 + i (deltanet.metal
 // :120-137: taps w.x .. w.w over inputs tok-3 .. tok); 0 for tokens >= T.
+template <bool TAIL>
 __device__ __forceinline__ void conv2x8(const float (&e)[11][2], const float4 (&w)[2], int tok0, int T,
                                         float (&y)[8][2]) {
 #pragma unroll
@@ -145,7 +147,7 @@ __device__ __forceinline__ void conv2x8(const float (&e)[11][2], const float4 (&
         for (int i = 0; i < 8; ++i) {
             const float v = silu_fast(e[i][c] * w[c].x + e[i + 1][c] * w[c].y + e[i + 2][c] * w[c].z +
                                       e[i + 3][c] * w[c].w);
-            y[i][c] = tok0 + i < T ? v : 0.0f;
+            y[i][c] = !TAIL || tok0 + i < T ? v : 0.0f;
         }
 }
 
@@ -293,10 +295,16 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         if (lane == 63) out.gam[ch] = expf(x);
     }
     const int chs[3] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + h * 128 + 2 * lane};
+    const bool tail = t0 + kC > T;
     auto conv = [&](int p, float (&y)[8][2]) {
         float e[11][2];
-        unit_rows<IN_DT>(in, p, tw, T, chs[p], conv_state, e);
-        conv2x8(e, in.w[p], tw, T, y);
+        if (tail) {
+            unit_rows<IN_DT, true>(in, p, tw, T, chs[p], conv_state, e);
+            conv2x8<true>(e, in.w[p], tw, T, y);
+        } else {
+            unit_rows<IN_DT, false>(in, p, tw, T, chs[p], conv_state, e);
+            conv2x8<false>(e, in.w[p], tw, T, y);
+        }
     };
 
     // ---- conv + SiLU, L2 norms over each token's 128 channels (deltanet.metal
@@ -308,9 +316,9 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         wave_sum8(ss, tot, lane);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float inv = 1.0f / sqrtf(tot[i] + 1e-6f);
-            y[i][0] = (y[i][0] * inv) * post;
-            y[i][1] = (y[i][1] * inv) * post;
+            const float sc = __builtin_amdgcn_rsqf(tot[i] + 1e-6f) * post;
+            y[i][0] *= sc;
+            y[i][1] *= sc;
             uint32_t hh, ll;
             split_bf16x2(y[i][0], y[i][1], hh, ll);
             const int o = (8 * wave + i) * kLD + 2 * lane;
@@ -320,7 +328,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     };
     float qn[8][2], kn[8][2], vn[8][2];
     conv(0, qn);
-    norm_store(qn, 1.0f / sqrtf(128.0f), Qh, Ql);
+    norm_store(qn, 0.08838834764831845f, Qh, Ql);   // 1 / sqrt(128)
     conv(1, kn);
     norm_store(kn, 1.0f, Kh, Kl);
     conv(2, vn);
