@@ -367,13 +367,15 @@ def cpu_baseline_c1(min_s=10.0, max_reps=12):
 
 
 def copy_probe():
-    """One device-to-device copy of COPY_PROBE_BYTES, for scaling the
-    FETCH_SIZE / WRITE_SIZE counters of a profiling run to bytes."""
+    """One elementwise pass (dst = -src, fp32) that reads and writes
+    COPY_PROBE_BYTES each, for scaling the FETCH_SIZE / WRITE_SIZE counters
+    of a profiling run to bytes. An elementwise kernel spreads over every CU
+    like the kernels it calibrates; a runtime blit copy does not always."""
     import torch
-    src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    dst.copy_(src)
+    torch.neg(src, out=dst)
     torch.cuda.synchronize()
 
 
