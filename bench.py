@@ -311,15 +311,16 @@ def bench_c4(B, L, steps, warmup):
                            conv, ssm))
 
     def step(i):
+        # in-projections as one launch each: the DeltaNet layer's four parts
+        # (qkv, z, b, a) as the reference's fused in-projection, the
+        # full-attention layer's q/gate, k and v likewise
         for kind, W, s1, s2 in layers:
             if kind == "dn":
-                for (w, sc, bi), o in zip(W[:4], (qkv, z, b, a)):
-                    qff.q4_matmul(ctx, w, sc, bi, x, out=o)
+                qff.q4_matmul_parts(ctx, W[:4], x, outs=(qkv, z, b, a))
                 qff.deltanet_decode(ctx, dnp, qkv, z, a, b, s1, s2, out=core)
                 qff.q4_matmul(ctx, *W[4], core, out=y)
             else:
-                for (w, sc, bi), o in zip(W[:3], (qg, kn, vn)):
-                    qff.q4_matmul(ctx, w, sc, bi, x, out=o)
+                qff.q4_matmul_parts(ctx, W[:3], x, outs=(qg, kn, vn))
                 qff.gqa_decode(ctx, gqp, qg.view(B, 16, 512), kn.view(B, 2, 256), vn.view(B, 2, 256), s1, s2,
                                pos, out=att)
                 qff.q4_matmul(ctx, *W[3], att.view(B, 4096), out=y)

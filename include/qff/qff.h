@@ -114,6 +114,32 @@ int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
                   const void* x, qff_dtype x_dtype, void* y, qff_dtype y_dtype,
                   int rows, int cols, int batch);
 
+/* One part of a grouped product: W [rows, cols] affine-Q4 as above (its own
+ * scales/biases, sb_dtype of the call) and its output y [batch, rows] of
+ * y_dtype. */
+typedef struct qff_q4_part {
+    const uint32_t* w;
+    const void* scales;
+    const void* biases;
+    int rows;
+    void* y;
+    qff_dtype y_dtype;
+} qff_q4_part;
+
+#define QFF_Q4_MAX_PARTS 8
+
+/* y_p = x W_p^T for every part p (1 <= nparts <= QFF_Q4_MAX_PARTS), all
+ * sharing x [batch, cols]: one launch over the parts' rows laid end to end
+ * for decode batches. Replaces the fused four-part DeltaNet in-projection
+ * qwen_fused_linear_attn_in_proj_q4_simd_f32 (deltanet.metal:1921-1983:
+ * qkv 8192, z 4096, b 32, a 32 rows, separate weights and outputs, one
+ * global row index), dispatched at QwenQ4ActiveExpertStreamingRunner
+ * .swift:982-997, and serves the q/k/v projections of a full-attention
+ * layer (.swift:1056-1074, three dispatches there) the same way. */
+int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts,
+                        int nparts, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
+                        int cols, int batch);
+
 /* ---------------------------------------------------------------- DeltaNet */
 
 /* Per-layer constants of a Gated DeltaNet layer (fp32, device pointers),

@@ -32,9 +32,10 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     auto take = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
     const size_t B = static_cast<size_t>(cfg.max_batch);
     const size_t T = static_cast<size_t>(cfg.max_prefill_tokens);
-    L.gqa_m = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
-    L.gqa_d = take(B * 2 * kGqaMaxChunks * 8 * sizeof(float));
-    L.gqa_o = take(B * 2 * kGqaMaxChunks * 8 * 256 * sizeof(float));
+    const size_t S = static_cast<size_t>(gqa_slots(cfg));
+    L.gqa_m = take(S * 8 * sizeof(float));
+    L.gqa_d = take(S * 8 * sizeof(float));
+    L.gqa_o = take(S * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
     L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
@@ -257,6 +258,27 @@ int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w, const vo
     if (cols % 64 != 0 || cols > 4096) return QFF_ERR_UNSUPPORTED;
     QFF_CHECK_HIP(launch_q4_matmul(ctx, stream, w, scales, biases, sb_dtype, x, x_dtype, y, y_dtype,
                                    rows, cols, batch));
+    return QFF_OK;
+}
+
+int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts, int nparts,
+                        qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
+    if (!ctx || !parts || !x || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return QFF_ERR_INVALID_ARG;
+    if (sb_dtype != QFF_F16 && sb_dtype != QFF_BF16) return QFF_ERR_INVALID_ARG;
+    if (!dtype_ok(x_dtype) || cols <= 0 || batch <= 0) return QFF_ERR_INVALID_ARG;
+    for (int i = 0; i < nparts; ++i) {
+        const qff_q4_part& q = parts[i];
+        if (!q.w || !q.scales || !q.biases || !q.y || q.rows <= 0 || !dtype_ok(q.y_dtype))
+            return QFF_ERR_INVALID_ARG;
+    }
+    if (cols % 64 != 0 || cols > 4096) return QFF_ERR_UNSUPPORTED;
+    if (batch >= kQ4GemmMinBatch) {
+        for (int i = 0; i < nparts; ++i)
+            QFF_CHECK_HIP(launch_q4_matmul(ctx, stream, parts[i].w, parts[i].scales, parts[i].biases, sb_dtype,
+                                           x, x_dtype, parts[i].y, parts[i].y_dtype, parts[i].rows, cols, batch));
+        return QFF_OK;
+    }
+    QFF_CHECK_HIP(launch_q4_gemv_parts(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, cols, batch));
     return QFF_OK;
 }
 

@@ -53,7 +53,7 @@ void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, float* __restrict__ pm,
+    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
     float* __restrict__ pd, float* __restrict__ po) {
     const int kvh = blockIdx.y, seq = blockIdx.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -259,7 +259,7 @@ void gqa_decode_partial_kernel(
     // ---- partial (m, d, o) of this chunk; oacc[jd][i] = O[head 4kb+i][dim 16jd+n]
     d_run += __shfl_xor(d_run, 16, 64);
     d_run += __shfl_xor(d_run, 32, 64);
-    const size_t pbase = (static_cast<size_t>(seq) * 2 + kvh) * kGqaMaxChunks + c;
+    const size_t pbase = (static_cast<size_t>(seq) * 2 + kvh) * cstride + c;
     if (lane < 8) {
         pm[pbase * 8 + lane] = m_run;
         pd[pbase * 8 + lane] = d_run;
@@ -281,7 +281,7 @@ void gqa_decode_partial_kernel(
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int max_ctx, int chunk_len,
-    const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
+    int cstride, const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
     __shared__ float es[kGqaMaxChunks], red[16];
     __shared__ __attribute__((aligned(16))) float osum[8][256];
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     }
     const int L = pos + 1;
     const int nc = (L + chunk_len - 1) / chunk_len;
-    const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * kGqaMaxChunks;
+    const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * cstride;
     const float m = t < nc ? pm[(base + t) * 8 + hl] : -INFINITY;
     const float d = t < nc ? pd[(base + t) * 8 + hl] : 0.0f;
     const float wmax = group_max<64>(m);
@@ -342,13 +342,20 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     }
 }
 
+// Chunks per (sequence, kv head) available to a call of this batch: the
+// workspace's partial slots spread over the batch, at most kGqaMaxChunks.
+int gqa_chunk_cap(const qff_ctx_cfg& cfg, int batch) {
+    const int cap = gqa_slots(cfg) / (2 * batch);
+    return cap < kGqaMaxChunks ? cap : kGqaMaxChunks;
+}
+
 // Chunk length: aim for ~4096 one-wave partial workgroups over the batch
-// (16 per CU), at most kGqaMaxChunks chunks per sequence, multiples of 64
-// positions (4 MFMA tiles).
-int gqa_chunk_len(int max_ctx, int batch) {
+// (16 per CU), at most `cap` chunks per sequence, multiples of 64 positions
+// (4 MFMA tiles).
+int gqa_chunk_len(int max_ctx, int batch, int cap) {
     int target = 4096 / (2 * batch);
     if (target < 1) target = 1;
-    if (target > kGqaMaxChunks) target = kGqaMaxChunks;
+    if (target > cap) target = cap;
     const int per = (max_ctx + target - 1) / target;
     const int ch = ((per + 63) / 64) * 64;
     return ch < 64 ? 64 : ch;
@@ -359,7 +366,8 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              qff_dtype in_dtype, void* k_cache, void* v_cache,
                              const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                              int max_ctx) {
-    const int ch = gqa_chunk_len(max_ctx, batch);
+    const int cap = gqa_chunk_cap(ctx->cfg, batch);
+    const int ch = gqa_chunk_len(max_ctx, batch, cap);
     const int nc = (max_ctx + ch - 1) / ch;
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
@@ -369,7 +377,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
         const bool grouped = ch >= 256;
 #define QFF_PART(I, W)                                                                                     \
     gqa_decode_partial_kernel<I, W><<<dim3((nc + W - 1) / W, 2, batch), 64 * W, 0, stream>>>(              \
-        q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, \
+        q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
         ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
         if (in_dtype == QFF_BF16) {
             if (grouped) QFF_PART(1, 4); else QFF_PART(1, 1);
@@ -381,7 +389,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
     const dim3 cgrid(16, batch);
     ProfScope prof(ctx, stream, "gqa_decode_combine");
 #define QFF_COMB(I, O) \
-    gqa_decode_combine_kernel<I, O><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
+    gqa_decode_combine_kernel<I, O><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
     if (in_dtype == QFF_BF16) {
         if (out_dtype == QFF_BF16) QFF_COMB(1, 1); else QFF_COMB(1, 0);
     } else {

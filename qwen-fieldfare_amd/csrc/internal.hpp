@@ -33,9 +33,9 @@ struct qff_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     // Full-attention decode: split-KV partials per (sequence, kv head, chunk).
-    float* gqa_m = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8]
+    float* gqa_m = nullptr;       // [gqa_slots(cfg) * 8]
     float* gqa_d = nullptr;       // same
-    float* gqa_o = nullptr;       // [max_batch * 2 * kGqaMaxChunks * 8 * 256]
+    float* gqa_o = nullptr;       // [gqa_slots(cfg) * 8 * 256]
     // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
     uint16_t* gqa_qb = nullptr;
     // Many-token Q4 products: per-token group sums [q4_xs_tokens][64] fp32.
@@ -59,7 +59,11 @@ struct qff_ctx {
 
 namespace qff {
 
-constexpr int kGqaMaxChunks = 128;     // split-KV chunks per (sequence, kv head)
+constexpr int kGqaMaxChunks = 512;     // split-KV chunks per (sequence, kv head), any call
+constexpr int kGqaSeqChunks = 128;     // partial slots per (sequence, kv head) at max_batch
+// (sequence, kv head, chunk) partial slots of the workspace: a call with a
+// smaller batch spreads them over more chunks per sequence.
+inline int gqa_slots(const qff_ctx_cfg& cfg) { return 2 * (cfg.max_batch > 4 ? cfg.max_batch : 4) * kGqaSeqChunks; }
 constexpr int kSchedSlots = 8;         // work-queue counter pairs in the context
 constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
@@ -129,6 +133,11 @@ hipError_t launch_q4_dequant(hipStream_t stream, const uint32_t* w, const void* 
 hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
                             const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
                             void* y, qff_dtype y_dtype, int rows, int cols, int batch);
+// Decode-batch product over up to QFF_Q4_MAX_PARTS parts in one launch
+// (batch < the GEMM threshold).
+hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch);
+constexpr int kQ4GemmMinBatch = 33;   // batches at least this large take the tiled GEMM
 hipError_t launch_kv_append(hipStream_t stream, const float* k, const float* v, void* k_cache,
                             void* v_cache, qff_dtype cache_dtype, int pos, int max_seq);
 hipError_t launch_attention_gate(hipStream_t stream, const uint16_t* attn, const float* gate,

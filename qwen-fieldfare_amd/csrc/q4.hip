@@ -76,17 +76,34 @@ __device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
 constexpr int kQ4GemvWaves = 8;
 constexpr int kQ4GemvMaxGroupsPerWave = kQ4MaxGroups / kQ4GemvWaves;
 
-template <int SB_DT, int X_DT, int Y_DT, int NBT>
-__global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(const uint32_t* __restrict__ w,
-                                                                    const uint16_t* __restrict__ scales,
-                                                                    const uint16_t* __restrict__ biases,
-                                                                    const void* __restrict__ x, void* __restrict__ y,
-                                                                    int rows, int cols, int batch) {
+// The parts of one launch (a single product is one part): workgroups
+// blk0[p] .. blk0[p+1]-1 take part p's 16-row blocks.
+struct Q4Parts {
+    const uint32_t* w[QFF_Q4_MAX_PARTS];
+    const uint16_t* s[QFF_Q4_MAX_PARTS];
+    const uint16_t* b[QFF_Q4_MAX_PARTS];
+    void* y[QFF_Q4_MAX_PARTS];
+    int rows[QFF_Q4_MAX_PARTS];
+    int ybf16[QFF_Q4_MAX_PARTS];
+    int blk0[QFF_Q4_MAX_PARTS + 1];
+    int n;
+};
+
+template <int SB_DT, int X_DT, int NBT>
+__global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
+                                                                    int cols, int batch) {
     constexpr int NT = 64 * kQ4GemvWaves;
     const int G = cols / 64, Gw = (G + kQ4GemvWaves - 1) / kQ4GemvWaves;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const int R0 = blockIdx.x * 16;
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < QFF_Q4_MAX_PARTS; ++i) p += (i < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[i]);
+    const uint32_t* __restrict__ w = parts.w[p];
+    const uint16_t* __restrict__ scales = parts.s[p];
+    const uint16_t* __restrict__ biases = parts.b[p];
+    const int rows = parts.rows[p];
+    const int R0 = (blockIdx.x - parts.blk0[p]) * 16;
 
     __shared__ float2 sb[16][kQ4MaxGroups];          // (s, b - 128 s) per row and group
     __shared__ __attribute__((aligned(16))) f32x4_t part[kQ4GemvWaves][NBT][64];
@@ -175,7 +192,10 @@ __global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(const uint32
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = R0 + 4 * kb + j;
-                if (r < rows) elem<Y_DT>::store(y, static_cast<size_t>(m) * rows + r, v[j]);
+                if (r < rows) {
+                    if (parts.ybf16[p]) elem<1>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
+                    else elem<0>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
+                }
             }
         }
     }
@@ -202,7 +222,6 @@ __global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(const uint32
 // c6, c3, c7): dword j of the converted word is then
 // ((w >> 4j) & 0x000F000F) | 0x43004300 (two instructions), and the
 // activations are staged in the same order.
-constexpr int kQ4GemmMinBatch = 33;
 constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
 
 // X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
@@ -451,19 +470,36 @@ hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w,
         }
         return hipGetLastError();
     }
+    const qff_q4_part part{w, scales, biases, rows, y, y_dtype};
+    return launch_q4_gemv_parts(ctx, stream, &part, 1, sb_dtype, x, x_dtype, cols, batch);
+}
+
+hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
+    if (cols / 64 > kQ4MaxGroups || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return hipErrorInvalidValue;
+    Q4Parts P{};
+    int blocks = 0;
+    for (int i = 0; i < nparts; ++i) {
+        P.w[i] = parts[i].w;
+        P.s[i] = static_cast<const uint16_t*>(parts[i].scales);
+        P.b[i] = static_cast<const uint16_t*>(parts[i].biases);
+        P.y[i] = parts[i].y;
+        P.rows[i] = parts[i].rows;
+        P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
+        P.blk0[i] = blocks;
+        blocks += (parts[i].rows + 15) / 16;
+    }
+    P.blk0[nparts] = blocks;
+    P.n = nparts;
     const int nbt = (batch + 15) / 16;
     ProfScope prof(ctx, stream, "q4_matmul");
-#define QFF_Q4V(S, X, Y, NB) \
-    q4_gemv_kernel<S, X, Y, NB><<<(rows + 15) / 16, 64 * kQ4GemvWaves, 0, stream>>>(w, s, b, x, y, rows, cols, batch)
-#define QFF_Q4V_B(S, X, Y) \
-    if (nbt == 1) QFF_Q4V(S, X, Y, 1); else QFF_Q4V(S, X, Y, 2)
-#define QFF_Q4V_Y(S, X) \
-    if (y_dtype == QFF_BF16) { QFF_Q4V_B(S, X, 1); } else { QFF_Q4V_B(S, X, 0); }
+#define QFF_Q4V(S, X, NB) q4_gemv_kernel<S, X, NB><<<blocks, 64 * kQ4GemvWaves, 0, stream>>>(P, x, cols, batch)
+#define QFF_Q4V_B(S, X) \
+    if (nbt == 1) QFF_Q4V(S, X, 1); else QFF_Q4V(S, X, 2)
 #define QFF_Q4V_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4V_Y(S, 1); } else { QFF_Q4V_Y(S, 0); }
+    if (x_dtype == QFF_BF16) { QFF_Q4V_B(S, 1); } else { QFF_Q4V_B(S, 0); }
     if (sb_dtype == QFF_BF16) { QFF_Q4V_X(1); } else { QFF_Q4V_X(2); }
 #undef QFF_Q4V_X
-#undef QFF_Q4V_Y
 #undef QFF_Q4V_B
 #undef QFF_Q4V
     return hipGetLastError();

@@ -34,6 +34,13 @@ class GqaParams(ctypes.Structure):
                 ("scale", _f), ("eps", _f)]
 
 
+class Q4Part(ctypes.Structure):
+    _fields_ = [("w", _vp), ("scales", _vp), ("biases", _vp), ("rows", _i), ("y", _vp), ("y_dtype", _i)]
+
+
+Q4_MAX_PARTS = 8
+
+
 class CtxCfg(ctypes.Structure):
     _fields_ = [("max_batch", _i), ("max_ctx", _i), ("max_prefill_tokens", _i)]
 
@@ -47,6 +54,7 @@ SIGNATURES = {
     "qff_version": [],
     "qff_q4_dequant": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i],
     "qff_q4_matmul": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i],
+    "qff_q4_matmul_parts": [_vp, _vp, ctypes.POINTER(Q4Part), _i, _i, _vp, _i, _i, _i],
     "qff_deltanet_decode": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp, _vp,
                             _vp, _vp, _i, _i],
     "qff_deltanet_prefill": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp,

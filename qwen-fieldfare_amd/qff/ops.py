@@ -12,7 +12,7 @@ import ctypes
 
 import torch
 
-from ._lib import BF16, F16, F32, CtxCfg, DeltaNetParams, GqaParams, QffError, check, lib
+from ._lib import BF16, F16, F32, Q4_MAX_PARTS, CtxCfg, DeltaNetParams, GqaParams, Q4Part, QffError, check, lib
 
 _DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 _TORCH = {F32: torch.float32, BF16: torch.bfloat16, F16: torch.float16}
@@ -85,6 +85,33 @@ def q4_matmul(ctx: Context, w, scales, biases, x: torch.Tensor, out=None,
                                                _ptr(biases), _code(scales), _ptr(x2), _code(x2),
                                                _ptr(out), _code(out), rows, cols, batch))
     return out
+
+
+def q4_matmul_parts(ctx: Context, parts, x: torch.Tensor, outs=None, out_dtypes=None):
+    """One launch of y_p = x W_p^T for every part (w, scales, biases) in
+    `parts` (all with the same cols and scale dtype), sharing x [batch, cols].
+    Returns the list of outputs [batch, rows_p]."""
+    if not 1 <= len(parts) <= Q4_MAX_PARTS:
+        raise ValueError(f"1 .. {Q4_MAX_PARTS} parts")
+    cols = parts[0][0].shape[1] * 8
+    x2 = x.reshape(-1, cols)
+    batch = x2.shape[0]
+    arr = (Q4Part * len(parts))()
+    res = []
+    for i, (w, s, b) in enumerate(parts):
+        rows = w.shape[0]
+        if w.shape[1] * 8 != cols or s.dtype != parts[0][1].dtype:
+            raise ValueError("parts must share cols and scale dtype")
+        if outs is not None:
+            out = outs[i]
+        else:
+            dt = out_dtypes[i] if out_dtypes is not None else torch.float32
+            out = torch.empty(batch, rows, dtype=dt, device=x.device)
+        arr[i] = Q4Part(_ptr(w), _ptr(s), _ptr(b), rows, _ptr(out), _code(out))
+        res.append(out)
+    check("qff_q4_matmul_parts", lib().qff_q4_matmul_parts(ctx.handle, _stream(), arr, len(parts),
+                                                           _code(parts[0][1]), _ptr(x2), _code(x2), cols, batch))
+    return res
 
 
 def _dn_params(p: dict, eps: float):

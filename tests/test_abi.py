@@ -63,6 +63,10 @@ def test_workspace_size_and_argument_checks_without_gpu():
     assert L.qff_deltanet_decode(N, N, N, N, N, 1, N, N, N, N, N, 1, 1) == -1
     assert L.qff_gqa_decode(N, N, N, N, N, N, 1, N, N, N, N, 1, 1, 16) == -1
     assert L.qff_q4_matmul(N, N, N, N, N, 2, N, 1, N, 0, 64, 64, 1) == -1
+    assert L.qff_q4_matmul_parts(N, N, N, 1, 2, N, 1, 64, 1) == -1
+    from qff._lib import Q4Part
+    parts = (Q4Part * 9)()
+    assert L.qff_q4_matmul_parts(N, N, parts, 9, 2, N, 1, 64, 1) == -1   # null ctx and too many parts
 
 
 def test_product_has_no_cpu_fallback():

@@ -73,8 +73,15 @@ def test_gqa_decode_batch_random_lengths(hip, B):
 
 
 def test_gqa_decode_long_context(hip):
-    # 64K context (config 4's single-sequence decode) at two positions
+    # 64K context at two positions (batch 2: 256 chunks per sequence)
     _run_case(hip, [65536, 40000], 65536)
+
+
+@pytest.mark.parametrize("L", [65536, 50001])
+def test_gqa_decode_batch1_long_context(hip, L):
+    # config 4's single-sequence decode: batch 1 spreads the split over 512
+    # chunks per kv head
+    _run_case(hip, [L], 65536, out_dtype=torch.bfloat16, seed=L)
 
 
 def test_kv_append_and_gate_kats(hip):

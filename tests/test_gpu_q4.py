@@ -98,3 +98,45 @@ def test_q4_rejects_bad_shapes(hip):
     with pytest.raises(qff.QffError) as e:
         qff.q4_dequant(ctx, w, s, s)
     assert e.value.status == -2
+
+
+@pytest.mark.parametrize("batch", [1, 3, 16, 32, 40])
+def test_q4_matmul_parts_match_single_products(hip, batch):
+    """The four-part DeltaNet in-projection shape (qkv 8192, z 4096, b 32,
+    a 32 rows; bf16, bf16, f32, f32 outputs) in one call: each part equals
+    the single-matrix product bit for bit (same kernel per row block), and
+    the first part matches the fp64 dequantized product."""
+    import qff
+    print(f"q4_matmul_parts batch={batch}", flush=True)
+    cols = 2048
+    shapes = [(8192, torch.bfloat16), (4096, torch.bfloat16), (32, torch.float32), (32, torch.float32)]
+    ws = [synth.q4_weight(r, cols, seed=11 * r + batch) for r, _ in shapes]
+    rng = np.random.default_rng(100 + batch)
+    xb = O.f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32))
+    ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=64)
+    parts = [_w_gpu(w, s, b, "f16") for w, s, b in ws]
+    x = bf16_tensor(xb)
+    outs = qff.q4_matmul_parts(ctx, parts, x, out_dtypes=[dt for _, dt in shapes])
+    singles = [qff.q4_matmul(ctx, *pp, x, out_dtype=dt) for pp, (_, dt) in zip(parts, shapes)]
+    torch.cuda.synchronize()
+    for o, s1 in zip(outs, singles):
+        assert o.dtype == s1.dtype and torch.equal(o.view(torch.int16) if o.dtype == torch.bfloat16 else o,
+                                                    s1.view(torch.int16) if s1.dtype == torch.bfloat16 else s1)
+    w, s, b = ws[2]
+    ref = O.bf16_to_f32(xb).astype(np.float64) @ O.q4_dequant(w, s, b, O.F16).astype(np.float64).T
+    assert _rel(to_np(outs[2]), ref) <= 1e-5
+
+
+def test_q4_matmul_parts_rejects_bad_calls(hip):
+    import qff
+    from qff._lib import Q4Part, lib
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    w, s, b = _w_gpu(*synth.q4_weight(64, 128, seed=3), "f16")
+    x = torch.zeros(1, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        qff.q4_matmul_parts(ctx, [], x)
+    with pytest.raises(ValueError):
+        qff.q4_matmul_parts(ctx, [(w, s, b)] * 9, x)
+    arr = (Q4Part * 1)()
+    arr[0] = Q4Part(w.data_ptr(), s.data_ptr(), b.data_ptr(), 0, x.data_ptr(), 0)   # rows = 0
+    assert lib().qff_q4_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, 128, 1) == -1
