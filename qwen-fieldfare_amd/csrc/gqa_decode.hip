@@ -41,8 +41,10 @@ struct DecTile {
     u32x4_t k[8], v[8];
 };
 
-// grid (ceil(chunks / NW), 2 kv heads, batch), 64 NW threads: wave w takes
-// chunk NW * blockIdx.x + w. NW = 4 (long chunks) shares one q preparation
+// grid (2 kv heads x ceil(chunks / NW), 1, batch), 64 NW threads: the kv
+// head is the fastest-varying block index, so the two heads' workgroups of a
+// chunk group are dispatched together and stream the interleaved halves of
+// the same cache records at the same time; wave w takes chunk NW * group + w. NW = 4 (long chunks) shares one q preparation
 // between four chunks and keeps the next tile's loads in flight (two register
 // stages, two waves per SIMD); NW = 1 (short chunks, small batches) loads
 // each tile as it goes and keeps three or more single-wave workgroups per
@@ -55,15 +57,15 @@ void gqa_decode_partial_kernel(
     float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
     const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
     float* __restrict__ pd, float* __restrict__ po) {
-    const int kvh = blockIdx.y, seq = blockIdx.z;
+    const int kvh = blockIdx.x & 1, grp = blockIdx.x >> 1, seq = blockIdx.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int c = NW * blockIdx.x + wave;
+    const int c = NW * grp + wave;
     const int pos = positions[seq];
     // a position outside the cache is the caller's error: skip the sequence
     // (the combine writes NaN for it) rather than touch memory past the cache
     if (pos < 0 || pos >= max_ctx) return;
     const int L = pos + 1;
-    if (NW * blockIdx.x * chunk_len >= L) return;   // the whole group is past the end
+    if (NW * grp * chunk_len >= L) return;   // the whole group is past the end
     const int p_start = c * chunk_len;
     const int p_end = min(L, p_start + chunk_len);
 
@@ -376,7 +378,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
         ProfScope prof(ctx, stream, "gqa_decode_partial");
         const bool grouped = ch >= 256;
 #define QFF_PART(I, W)                                                                                     \
-    gqa_decode_partial_kernel<I, W><<<dim3((nc + W - 1) / W, 2, batch), 64 * W, 0, stream>>>(              \
+    gqa_decode_partial_kernel<I, W><<<dim3(2 * ((nc + W - 1) / W), 1, batch), 64 * W, 0, stream>>>(              \
         q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
         ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
         if (in_dtype == QFF_BF16) {

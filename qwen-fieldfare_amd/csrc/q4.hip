@@ -64,20 +64,23 @@ __device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
 
 // ---- decode-shaped product (batch <= 32) ---------------------------------------
 //
-// One workgroup per 16 weight rows, the K dimension split over its eight
-// waves (wave w: groups w*ceil(G/8) .. ), all batch tiles of 16 tokens in the
-// same pass. A lane issues every load it needs up front: 8 bytes of its row
-// per group (the words 2kb, 2kb+1: MFMA k step 0 takes the even words, step 1
-// the odd ones) and the 16 x values of the same columns per batch tile; the
-// scales and folded biases of the 16 rows go to LDS first. Per group: P =
-// sum (128 + q) x on the matrix cores, the group sum of x from the same
+// One workgroup per 16 RT weight rows, cols/512 waves (at least one), each
+// wave taking 8 of the row's 64-column groups. The workgroup first streams
+// its rows' weight words into LDS with 16-B loads that cover whole rows
+// (consecutive threads, consecutive bytes: full cache lines per
+// instruction), together with the scales and folded biases; each lane has
+// meanwhile issued the loads of its x values (16 per group and token tile).
+// Per group: the lane reads its 8 B of each row tile from LDS, P = sum
+// (128 + q) x on the matrix cores, the group sum of x from the same
 // registers (plus two shuffles), acc += s P + (b - 128 s) sum(x) in fp32.
-// The eight partial sums meet in LDS.
-constexpr int kQ4GemvWaves = 8;
-constexpr int kQ4GemvMaxGroupsPerWave = kQ4MaxGroups / kQ4GemvWaves;
+// The waves' partial sums meet in LDS. RT = 4 reads x a quarter as often
+// per weight byte (several tokens over long matrices); RT = 1 gives the most
+// workgroups (batch 1, short matrices).
+constexpr int kQ4GemvMaxWaves = 8;
+constexpr int kQ4GemvGroupsPerWave = 8;
 
-// The parts of one launch (a single product is one part): workgroups
-// blk0[p] .. blk0[p+1]-1 take part p's 16-row blocks.
+// Q4Parts: the parts of one launch (a single product is one part):
+// workgroups blk0[p] .. blk0[p+1]-1 take part p's row blocks.
 struct Q4Parts {
     const uint32_t* w[QFF_Q4_MAX_PARTS];
     const uint16_t* s[QFF_Q4_MAX_PARTS];
@@ -89,11 +92,23 @@ struct Q4Parts {
     int n;
 };
 
-template <int SB_DT, int X_DT, int NBT>
-__global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
-                                                                    int cols, int batch) {
-    constexpr int NT = 64 * kQ4GemvWaves;
-    const int G = cols / 64, Gw = (G + kQ4GemvWaves - 1) / kQ4GemvWaves;
+__host__ __device__ constexpr int q4_gemv_waves(int cols) { return cols >= 4096 ? 8 : cols >= 512 ? cols / 512 : 1; }
+__host__ __device__ constexpr int q4_lds_stride(int cols) { return cols / 8 + 8; }   // dwords per staged row
+
+template <int RT, int NBT>
+__host__ __device__ constexpr int q4_gemv_lds_bytes(int cols) {
+    return (16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8) >
+                   q4_gemv_waves(cols) * RT * NBT * 64 * 16
+               ? 16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8
+               : q4_gemv_waves(cols) * RT * NBT * 64 * 16;
+}
+
+template <int SB_DT, int X_DT, int NBT, int RT>
+__global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
+                                                                       int cols, int batch) {
+    constexpr int RW = 16 * RT;                     // rows per workgroup
+    const int G = cols / 64, W8 = cols / 8, S = q4_lds_stride(cols);
+    const int nw = q4_gemv_waves(cols), NT = 64 * nw;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
     int p = 0;
@@ -103,95 +118,145 @@ __global__ __launch_bounds__(64 * kQ4GemvWaves) void q4_gemv_kernel(Q4Parts part
     const uint16_t* __restrict__ scales = parts.s[p];
     const uint16_t* __restrict__ biases = parts.b[p];
     const int rows = parts.rows[p];
-    const int R0 = (blockIdx.x - parts.blk0[p]) * 16;
+    const int R0 = (blockIdx.x - parts.blk0[p]) * RW;
 
-    __shared__ float2 sb[16][kQ4MaxGroups];          // (s, b - 128 s) per row and group
-    __shared__ __attribute__((aligned(16))) f32x4_t part[kQ4GemvWaves][NBT][64];
+    // LDS: the rows' weight words [RW][S], then (s, b - 128 s) [RW][G]; after
+    // the products the same bytes hold the waves' partial sums
+    extern __shared__ __attribute__((aligned(16))) unsigned char q4lds[];
+    uint32_t* wl = reinterpret_cast<uint32_t*>(q4lds);
+    float2* sb = reinterpret_cast<float2*>(q4lds + RW * S * 4);
+    f32x4_t* part = reinterpret_cast<f32x4_t*>(q4lds);
 
-    // loads: scales/biases for LDS first, then this lane's weights and x
-    float sreg[2], breg[2];
+    // weight pieces (16 B): piece q -> row q / (W8/4), words 4 (q % (W8/4));
+    // at most RW/4 per thread (NT >= W8), clamped so every load is issued
+    const int ppr = W8 / 4, npieces = RW * ppr;
+    u32x4_t wp[RW / 4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int idx = min(t + NT * k, 16 * G - 1);
+    for (int i = 0; i < RW / 4; ++i) {
+        const int q = min(t + NT * i, npieces - 1);
+        const int r = q / ppr, c4 = q - r * ppr;
+        wp[i] = *reinterpret_cast<const u32x4_t*>(w + static_cast<size_t>(min(R0 + r, rows - 1)) * W8 + 4 * c4);
+    }
+    // scales/biases: at most RW/8 entries per thread (NT >= 8 G)
+    float sreg[RW / 8], breg[RW / 8];
+#pragma unroll
+    for (int k = 0; k < RW / 8; ++k) {
+        const int idx = min(t + NT * k, RW * G - 1);
         const size_t gi = static_cast<size_t>(min(R0 + idx / G, rows - 1)) * G + idx % G;
         sreg[k] = elem<SB_DT>::load(scales, gi);
         breg[k] = elem<SB_DT>::load(biases, gi);
     }
-    const int g0 = wave * Gw, gn = min(Gw, G - g0);   // this wave's groups (gn may be <= 0)
-    const uint32_t* wrow = w + static_cast<size_t>(min(R0 + n, rows - 1)) * (cols / 8) + 2 * kb;
-    u32x2_t wv[kQ4GemvMaxGroupsPerWave];
-    u32x4_t xv[kQ4GemvMaxGroupsPerWave][NBT][2];
+    // this lane's x (16 values per group and token tile): bf16 activations
+    // for all 8 groups of its wave up front; fp32 ones (converted to bf16
+    // as they arrive) group by group in the product loop
+    const int g0 = wave * kQ4GemvGroupsPerWave, gn = min(kQ4GemvGroupsPerWave, G - g0);
+    auto load_x = [&](int i, u32x4_t (&xo2)[NBT][2]) {
+        const int g = min(g0 + i, G - 1);
 #pragma unroll
-    for (int i = 0; i < kQ4GemvMaxGroupsPerWave; ++i) {
-        if (i < gn) {
-            const int g = g0 + i;
-            wv[i] = *reinterpret_cast<const u32x2_t*>(wrow + 8 * g);
-#pragma unroll
-            for (int bt = 0; bt < NBT; ++bt) {
-                const size_t xo = static_cast<size_t>(min(16 * bt + n, batch - 1)) * cols + 64 * g + 16 * kb;
-                if (X_DT == 1) {
-                    xv[i][bt][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
-                    xv[i][bt][1] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8);
-                } else {
-                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo);
-                    const float4 e0 = p[0], e1 = p[1], e2 = p[2], e3 = p[3];
-                    xv[i][bt][0] = u32x4_t{pack_bf16x2(e0.x, e0.y), pack_bf16x2(e0.z, e0.w),
-                                           pack_bf16x2(e1.x, e1.y), pack_bf16x2(e1.z, e1.w)};
-                    xv[i][bt][1] = u32x4_t{pack_bf16x2(e2.x, e2.y), pack_bf16x2(e2.z, e2.w),
-                                           pack_bf16x2(e3.x, e3.y), pack_bf16x2(e3.z, e3.w)};
-                }
+        for (int bt = 0; bt < NBT; ++bt) {
+            const size_t xo = static_cast<size_t>(min(16 * bt + n, batch - 1)) * cols + 64 * g + 16 * kb;
+            if (X_DT == 1) {
+                xo2[bt][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
+                xo2[bt][1] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8);
+            } else {
+                const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo);
+                const float4 e0 = q[0], e1 = q[1], e2 = q[2], e3 = q[3];
+                xo2[bt][0] = u32x4_t{pack_bf16x2(e0.x, e0.y), pack_bf16x2(e0.z, e0.w),
+                                     pack_bf16x2(e1.x, e1.y), pack_bf16x2(e1.z, e1.w)};
+                xo2[bt][1] = u32x4_t{pack_bf16x2(e2.x, e2.y), pack_bf16x2(e2.z, e2.w),
+                                     pack_bf16x2(e3.x, e3.y), pack_bf16x2(e3.z, e3.w)};
             }
+        }
+    };
+    constexpr int kXPre = X_DT == 1 ? kQ4GemvGroupsPerWave : 1;
+    u32x4_t xv[kXPre][NBT][2];
+    if (X_DT == 1) {
+#pragma unroll
+        for (int i = 0; i < kXPre; ++i) load_x(i, xv[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < RW / 4; ++i) {
+        const int q = t + NT * i;
+        if (q < npieces) {
+            const int r = q / ppr, c4 = q - r * ppr;
+            *reinterpret_cast<u32x4_t*>(wl + r * S + 4 * c4) = wp[i];
         }
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < RW / 8; ++k) {
         const int idx = t + NT * k;
-        if (idx < 16 * G) sb[idx / G][idx % G] = make_float2(sreg[k], breg[k] - 128.0f * sreg[k]);
+        if (idx < RW * G) sb[idx] = make_float2(sreg[k], breg[k] - 128.0f * sreg[k]);
     }
     __syncthreads();
 
-    f32x4_t acc[NBT];
+    f32x4_t acc[RT][NBT];
 #pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) acc[bt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int i = 0; i < kQ4GemvMaxGroupsPerWave; ++i) {
-        if (i >= gn) break;
-        const int g = g0 + i;
-        const u32x4_t a0 = q4_to_bf16_interleaved(wv[i][0]);
-        const u32x4_t a1 = q4_to_bf16_interleaved(wv[i][1]);
-        float2 svb[4];
+        for (int bt = 0; bt < NBT; ++bt) acc[rt][bt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // all 8 groups unrolled (groups past the row end, only for cols < 512,
+    // read group G-1 and are masked), so the LDS reads, shuffles and MFMAs of
+    // different groups overlap
 #pragma unroll
-        for (int j = 0; j < 4; ++j) svb[j] = sb[4 * kb + j][g];
+    for (int i = 0; i < kQ4GemvGroupsPerWave; ++i) {
+        const int g = min(g0 + i, G - 1);
+        const float keep = i < gn ? 1.0f : 0.0f;
+        float xsum[NBT];
+        u32x4_t xi[NBT][2];
+        u32x4_t (&xg)[NBT][2] = xv[X_DT == 1 ? i : 0];
+        if (X_DT != 1) load_x(i, xg);
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
-            const u32x4_t x0 = xv[i][bt][0], x1 = xv[i][bt][1];
-            float xsum = 0.0f;
+            const u32x4_t x0 = xg[bt][0], x1 = xg[bt][1];
+            float sx = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xsum += (__uint_as_float(x0[j] << 16) + __uint_as_float(x0[j] & 0xffff0000u)) +
-                        (__uint_as_float(x1[j] << 16) + __uint_as_float(x1[j] & 0xffff0000u));
-            xsum += __shfl_xor(xsum, 16, 64);
-            xsum += __shfl_xor(xsum, 32, 64);
-            f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            P = mfma_16x16x32_bf16(a0, interleave8(x0), P);
-            P = mfma_16x16x32_bf16(a1, interleave8(x1), P);
+                sx += (__uint_as_float(x0[j] << 16) + __uint_as_float(x0[j] & 0xffff0000u)) +
+                      (__uint_as_float(x1[j] << 16) + __uint_as_float(x1[j] & 0xffff0000u));
+            sx += __shfl_xor(sx, 16, 64);
+            sx += __shfl_xor(sx, 32, 64);
+            xsum[bt] = sx;
+            xi[bt][0] = interleave8(x0);
+            xi[bt][1] = interleave8(x1);
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[bt][j] = fmaf(svb[j].x, P[j], fmaf(svb[j].y, xsum, acc[bt][j]));
+        for (int rt = 0; rt < RT; ++rt) {
+            const u32x2_t wv = *reinterpret_cast<const u32x2_t*>(wl + (16 * rt + n) * S + 8 * g + 2 * kb);
+            const u32x4_t a0 = q4_to_bf16_interleaved(wv[0]);
+            const u32x4_t a1 = q4_to_bf16_interleaved(wv[1]);
+            float2 svb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                svb[j] = sb[(16 * rt + 4 * kb + j) * G + g];
+                svb[j].x *= keep;
+                svb[j].y *= keep;
+            }
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                P = mfma_16x16x32_bf16(a0, xi[bt][0], P);
+                P = mfma_16x16x32_bf16(a1, xi[bt][1], P);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[rt][bt][j] = fmaf(svb[j].x, P[j], fmaf(svb[j].y, xsum[bt], acc[rt][bt][j]));
+            }
         }
     }
+    __syncthreads();   // the staged weights are consumed; their bytes take the partial sums
 #pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) part[wave][bt][lane] = acc[bt];
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) part[(wave * RT * NBT + rt * NBT + bt) * 64 + lane] = acc[rt][bt];
     __syncthreads();
-    if (wave < NBT) {
-        const int bt = wave;
-        f32x4_t v = part[0][bt][lane];
-#pragma unroll
-        for (int ww = 1; ww < kQ4GemvWaves; ++ww) v += part[ww][bt][lane];
+    for (int tile = wave; tile < RT * NBT; tile += nw) {
+        const int rt = tile / NBT, bt = tile % NBT;
+        f32x4_t v = part[tile * 64 + lane];
+        for (int ww = 1; ww < nw; ++ww) v += part[(ww * RT * NBT + tile) * 64 + lane];
         const int m = 16 * bt + n;
         if (m < batch) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = R0 + 4 * kb + j;
+                const int r = R0 + 16 * rt + 4 * kb + j;
                 if (r < rows) {
                     if (parts.ybf16[p]) elem<1>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
                     else elem<0>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
@@ -474,9 +539,34 @@ hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w,
     return launch_q4_gemv_parts(ctx, stream, &part, 1, sb_dtype, x, x_dtype, cols, batch);
 }
 
+// Dynamic LDS past 64 KB needs the kernel's attribute raised (once per
+// kernel instantiation and size).
+template <auto Kernel>
+static hipError_t q4_allow_lds(int bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    static int raised = 0;   // largest size set so far for this kernel
+    if (bytes <= raised) return hipSuccess;
+    const hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) raised = bytes;
+    return e;
+}
+
+#define QFF_CHECK_HIP_RET(x)            \
+    do {                                \
+        const hipError_t e_ = (x);      \
+        if (e_ != hipSuccess) return e_; \
+    } while (0)
+
 hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                                 qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
     if (cols / 64 > kQ4MaxGroups || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return hipErrorInvalidValue;
+    // four row tiles per workgroup when x is read for several tokens over
+    // enough rows to keep one workgroup per CU busy; one otherwise
+    int total_rows = 0;
+    for (int i = 0; i < nparts; ++i) total_rows += parts[i].rows;
+    const bool rt4 = batch >= 2 && cols <= 2048 && total_rows >= 8192;
+    const int rw = rt4 ? 64 : 16;
     Q4Parts P{};
     int blocks = 0;
     for (int i = 0; i < nparts; ++i) {
@@ -487,15 +577,25 @@ hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
         P.rows[i] = parts[i].rows;
         P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
         P.blk0[i] = blocks;
-        blocks += (parts[i].rows + 15) / 16;
+        blocks += (parts[i].rows + rw - 1) / rw;
     }
     P.blk0[nparts] = blocks;
     P.n = nparts;
     const int nbt = (batch + 15) / 16;
+    const int threads = 64 * q4_gemv_waves(cols);
     ProfScope prof(ctx, stream, "q4_matmul");
-#define QFF_Q4V(S, X, NB) q4_gemv_kernel<S, X, NB><<<blocks, 64 * kQ4GemvWaves, 0, stream>>>(P, x, cols, batch)
+#define QFF_Q4V(S, X, NB)                                                                          \
+    if (rt4) {                                                                                     \
+        QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, 4>>(q4_gemv_lds_bytes<4, NB>(cols)))); \
+        q4_gemv_kernel<S, X, NB, 4><<<blocks, threads, q4_gemv_lds_bytes<4, NB>(cols), stream>>>(     \
+            P, x, cols, batch);                                                                    \
+    } else {                                                                                       \
+        QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, 1>>(q4_gemv_lds_bytes<1, NB>(cols)))); \
+        q4_gemv_kernel<S, X, NB, 1><<<blocks, threads, q4_gemv_lds_bytes<1, NB>(cols), stream>>>(     \
+            P, x, cols, batch);                                                                    \
+    }
 #define QFF_Q4V_B(S, X) \
-    if (nbt == 1) QFF_Q4V(S, X, 1); else QFF_Q4V(S, X, 2)
+    if (nbt == 1) { QFF_Q4V(S, X, 1); } else { QFF_Q4V(S, X, 2); }
 #define QFF_Q4V_X(S) \
     if (x_dtype == QFF_BF16) { QFF_Q4V_B(S, 1); } else { QFF_Q4V_B(S, 0); }
     if (sb_dtype == QFF_BF16) { QFF_Q4V_X(1); } else { QFF_Q4V_X(2); }

@@ -43,6 +43,8 @@ def _rel(a, b):
 
 @pytest.mark.parametrize("rows,cols,batch", [(8192, 2048, 1), (512, 2048, 5), (4096, 2048, 16),
                                              (2048, 4096, 32), (100, 2048, 33), (32, 2048, 1),
+                                             # 64-row workgroups (batch >= 2, >= 8192 rows), ragged end
+                                             (8192, 2048, 2), (8200, 2048, 17), (9216, 2048, 32),
                                              # many-token GEMM path (batch >= 64), ragged tiles included
                                              (512, 2048, 64), (100, 2048, 300), (8192, 2048, 256),
                                              (2048, 4096, 130), (512, 2048, 8192)])
@@ -73,6 +75,21 @@ def test_q4_matmul_f32_activations_vs_reference_order(hip):
         ref = O.q4_matvec(w, s, b, x[m])
         assert _rel(to_np(y)[m], ref) <= 1e-2
         assert _rel(to_np(yb)[m], ref) <= 1e-2
+
+
+def test_q4_gemv_f32_activations_64_row_workgroups(hip):
+    """Decode batch over >= 8192 rows (four row tiles per workgroup) with fp32
+    activations: the product matches the fp64 product with bf16-rounded x."""
+    import qff
+    rows, cols, batch = 8256, 2048, 9
+    w, s, b = synth.q4_weight(rows, cols, seed=8)
+    x = np.random.default_rng(9).standard_normal((batch, cols)).astype(np.float32)
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    y = qff.q4_matmul(ctx, *_w_gpu(w, s, b, "bf16"), f32_tensor(x))
+    torch.cuda.synchronize()
+    dense = O.q4_dequant(w, s, b, O.BF16).astype(np.float64)
+    ref = O.round_bf16(x).astype(np.float64) @ dense.T
+    assert _rel(to_np(y), ref) <= 1e-5
 
 
 def test_q4_gemm_f32_activations_round_like_bf16(hip):
