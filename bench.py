@@ -24,7 +24,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 
-# Canonical work per unit ("Measurement")
+# Canonical work per unit of each workload (algorithmic bytes and flops)
 C0_BYTES = 4_424_448           # DeltaNet decode, one layer-step at B=1
 C0_FLOPS = 3_670_016
 C1_FLOPS = 23_622_320_128      # DeltaNet chunked prefill T=4096
