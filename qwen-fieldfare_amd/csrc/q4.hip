@@ -266,6 +266,146 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     }
 }
 
+// ---- single-token product on the vector units ---------------------------------
+//
+// Batch 1 is latency bound, so this path has no LDS staging, no barrier and
+// no cross-wave reduction: a wave streams whole weight rows, one 16-B load
+// per lane per 2048 columns (lane l takes columns 32l .. 32l+31 of each
+// 2048), all RPW rows' loads in flight at once, and multiplies on the vector
+// units: the nibbles of a word become floats with two masks and byte
+// conversions, y_lane = s (sum q x) + b (sum x) over the lane's half group.
+// The RPW row sums meet in a reduce-scatter over the wave (7 shuffles).
+// x is rounded to bf16, as on the matrix-core path.
+// byte I of v as a float (one v_cvt_f32_ubyteI)
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) { return static_cast<float>((v >> (8 * I)) & 0xffu); }
+
+constexpr int kQ4VecRows = 4;      // rows per wave
+constexpr int kQ4VecWaves = 4;     // waves per workgroup
+
+template <int SB_DT, int X_DT, int KW>
+__global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts parts, const void* __restrict__ x,
+                                                                    int cols) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < QFF_Q4_MAX_PARTS; ++i) p += (i < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[i]);
+    const uint32_t* __restrict__ w = parts.w[p];
+    const uint16_t* __restrict__ scales = parts.s[p];
+    const uint16_t* __restrict__ biases = parts.b[p];
+    const int rows = parts.rows[p];
+    const int R0 = ((blockIdx.x - parts.blk0[p]) * kQ4VecWaves + wave) * kQ4VecRows;
+    const int G = cols / 64, W8 = cols / 8, npc = cols / 32;   // 32-column pieces per row
+
+    // weights and group constants of this wave's rows, all in flight
+    u32x4_t wq[kQ4VecRows][KW];
+    float sv[kQ4VecRows][KW], bv[kQ4VecRows][KW];
+#pragma unroll
+    for (int r = 0; r < kQ4VecRows; ++r) {
+        const size_t row = static_cast<size_t>(min(R0 + r, rows - 1));
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            const int pc = min(lane + 64 * k, npc - 1);
+            wq[r][k] = *reinterpret_cast<const u32x4_t*>(w + row * W8 + 4 * pc);
+            sv[r][k] = elem<SB_DT>::load(scales, row * G + pc / 2);
+            bv[r][k] = elem<SB_DT>::load(biases, row * G + pc / 2);
+        }
+    }
+    // this lane's x: columns 32pc .. 32pc+31, as bf16-rounded floats in the
+    // order the nibble masks produce (even nibbles of a word, then odd)
+    float xe[KW][4][8];
+    float xs[KW];
+#pragma unroll
+    for (int k = 0; k < KW; ++k) {
+        const int pc = lane + 64 * k;
+        const bool live = pc < npc;
+        const int pcc = min(pc, npc - 1);
+        float v[32];
+        if (X_DT == 1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + 32 * pcc + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[8 * q + 2 * e] = __uint_as_float(u[e] << 16);
+                    v[8 * q + 2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 32 * pcc)[q];
+                v[4 * q] = bf16_to_f32(f32_to_bf16(f.x));
+                v[4 * q + 1] = bf16_to_f32(f32_to_bf16(f.y));
+                v[4 * q + 2] = bf16_to_f32(f32_to_bf16(f.z));
+                v[4 * q + 3] = bf16_to_f32(f32_to_bf16(f.w));
+            }
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) {
+            v[c] = live ? v[c] : 0.0f;
+            sum += v[c];
+        }
+        xs[k] = sum;
+        // word j of the piece holds columns 8j .. 8j+7 (nibble c lowest first):
+        // w & 0x0F0F0F0F gives columns 8j + 0, 2, 4, 6 in bytes 0..3, the odd
+        // ones come from w >> 4
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                xe[k][j][bb] = v[8 * j + 2 * bb];
+                xe[k][j][4 + bb] = v[8 * j + 2 * bb + 1];
+            }
+    }
+    float part[kQ4VecRows];
+#pragma unroll
+    for (int r = 0; r < kQ4VecRows; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            float dq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t wd = wq[r][k][j];
+                const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+                dq = fmaf(ubyte_f32<0>(lo), xe[k][j][0], dq);
+                dq = fmaf(ubyte_f32<1>(lo), xe[k][j][1], dq);
+                dq = fmaf(ubyte_f32<2>(lo), xe[k][j][2], dq);
+                dq = fmaf(ubyte_f32<3>(lo), xe[k][j][3], dq);
+                dq = fmaf(ubyte_f32<0>(hi), xe[k][j][4], dq);
+                dq = fmaf(ubyte_f32<1>(hi), xe[k][j][5], dq);
+                dq = fmaf(ubyte_f32<2>(hi), xe[k][j][6], dq);
+                dq = fmaf(ubyte_f32<3>(hi), xe[k][j][7], dq);
+            }
+            acc = fmaf(sv[r][k], dq, fmaf(bv[r][k], xs[k], acc));
+        }
+        part[r] = acc;
+    }
+    // reduce-scatter: lane ^ 32 and ^ 16 halve the four rows, then ^ 8 .. ^ 1
+    const bool b5 = lane & 32, b4 = lane & 16;
+    float q2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float keep = b5 ? part[2 + j] : part[j], give = b5 ? part[j] : part[2 + j];
+        q2[j] = keep + __shfl_xor(give, 32, 64);
+    }
+    float q1 = (b4 ? q2[1] : q2[0]) + __shfl_xor(b4 ? q2[0] : q2[1], 16, 64);
+    q1 += __shfl_xor(q1, 8, 64);
+    q1 += __shfl_xor(q1, 4, 64);
+    q1 += __shfl_xor(q1, 2, 64);
+    q1 += __shfl_xor(q1, 1, 64);
+    // lane 16 * (2 b5 + b4) holds row 2 b5 + b4
+    if ((lane & 15) == 0) {
+        const int r = R0 + (lane >> 4);
+        if (r < rows) {
+            if (parts.ybf16[p]) elem<1>::store(parts.y[p], r, q1);
+            else elem<0>::store(parts.y[p], r, q1);
+        }
+    }
+}
+
 // ---- many-token GEMM (prefill projections) -----------------------------------
 //
 // y[m, r] for batch >= kQ4GemmMinBatch, as
@@ -561,6 +701,35 @@ static hipError_t q4_allow_lds(int bytes) {
 hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                                 qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
     if (cols / 64 > kQ4MaxGroups || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return hipErrorInvalidValue;
+    if (batch == 1 && cols <= 4096) {
+        // one token: the vector-unit streaming path, 16 rows per workgroup
+        Q4Parts P{};
+        int blocks = 0;
+        constexpr int rwg = kQ4VecRows * kQ4VecWaves;
+        for (int i = 0; i < nparts; ++i) {
+            P.w[i] = parts[i].w;
+            P.s[i] = static_cast<const uint16_t*>(parts[i].scales);
+            P.b[i] = static_cast<const uint16_t*>(parts[i].biases);
+            P.y[i] = parts[i].y;
+            P.rows[i] = parts[i].rows;
+            P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
+            P.blk0[i] = blocks;
+            blocks += (parts[i].rows + rwg - 1) / rwg;
+        }
+        P.blk0[nparts] = blocks;
+        P.n = nparts;
+        const bool k2 = cols > 2048;
+        ProfScope prof(ctx, stream, "q4_matmul");
+#define QFF_Q4S(S, X) \
+    if (k2) q4_gemv1_kernel<S, X, 2><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols); \
+    else q4_gemv1_kernel<S, X, 1><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols)
+#define QFF_Q4S_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4S(S, 1); } else { QFF_Q4S(S, 0); }
+        if (sb_dtype == QFF_BF16) { QFF_Q4S_X(1); } else { QFF_Q4S_X(2); }
+#undef QFF_Q4S_X
+#undef QFF_Q4S
+        return hipGetLastError();
+    }
     // four row tiles per workgroup when x is read for several tokens over
     // enough rows to keep one workgroup per CU busy; one otherwise
     int total_rows = 0;
