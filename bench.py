@@ -275,8 +275,9 @@ def bench_c4(B, L, steps, warmup):
     """Config 4: attention-only stack of the 40-layer pattern (3 Gated DeltaNet
     + 1 GQA) x 10, hidden 2048, every projection affine-Q4 group 64, MoE
     replaced by identity: one decode step of B sequences at context L. Each
-    layer reads the synthetic hidden state (the MoE is identity and no
-    residual stream is modelled), so per-layer work is the workload's. The
+    layer is the reference's attention block: input RMSNorm fused into the
+    in-projections, the layer core, and the out-projection adding into the
+    residual stream in place (the hidden state the next layer reads). The
     step is captured once in a HIP graph and replayed (the serving loop's
     shape), so the timing is GPU time, not Python launch time."""
     import numpy as np
@@ -287,13 +288,13 @@ def bench_c4(B, L, steps, warmup):
     ctx = qff.Context(max_batch=B, max_ctx=L, max_prefill_tokens=64)
     dnp = {k: torch.from_numpy(v).cuda() for k, v in synth.deltanet_params().items()}
     gqp = {k: torch.from_numpy(v).cuda() for k, v in synth.gqa_params().items()}
-    x = bf16_randn((B, 2048), g)
+    x = bf16_randn((B, 2048), g)          # the residual stream
+    in_norm = torch.ones(2048, device="cuda")   # input-RMSNorm weights = 1
     qkv = torch.empty(B, 8192, dtype=torch.bfloat16, device="cuda")
     z = torch.empty(B, 4096, dtype=torch.bfloat16, device="cuda")
     a = torch.empty(B, 32, device="cuda")
     b = torch.empty(B, 32, device="cuda")
     core = torch.empty(B, 4096, dtype=torch.bfloat16, device="cuda")
-    y = torch.empty(B, 2048, dtype=torch.bfloat16, device="cuda")
     qg = torch.empty(B, 8192, dtype=torch.bfloat16, device="cuda")
     kn = torch.empty(B, 512, dtype=torch.bfloat16, device="cuda")
     vn = torch.empty(B, 512, dtype=torch.bfloat16, device="cuda")
@@ -316,14 +317,14 @@ def bench_c4(B, L, steps, warmup):
         # full-attention layer's q/gate, k and v likewise
         for kind, W, s1, s2 in layers:
             if kind == "dn":
-                qff.q4_matmul_parts(ctx, W[:4], x, outs=(qkv, z, b, a))
+                qff.q4_norm_matmul_parts(ctx, W[:4], x, in_norm, 1e-6, outs=(qkv, z, b, a))
                 qff.deltanet_decode(ctx, dnp, qkv, z, a, b, s1, s2, out=core)
-                qff.q4_matmul(ctx, *W[4], core, out=y)
+                qff.q4_matmul_parts(ctx, W[4:], core, outs=(x,), residuals=(x,))
             else:
-                qff.q4_matmul_parts(ctx, W[:3], x, outs=(qg, kn, vn))
+                qff.q4_norm_matmul_parts(ctx, W[:3], x, in_norm, 1e-6, outs=(qg, kn, vn))
                 qff.gqa_decode(ctx, gqp, qg.view(B, 16, 512), kn.view(B, 2, 256), vn.view(B, 2, 256), s1, s2,
                                pos, out=att)
-                qff.q4_matmul(ctx, *W[3], att.view(B, 4096), out=y)
+                qff.q4_matmul_parts(ctx, W[3:], att.view(B, 4096), outs=(x,), residuals=(x,))
 
     kt, cnt = kernel_times(ctx, step, 2)
     per_step_kernel_ms = {k: v * cnt[k] / 2 for k, v in kt.items()}

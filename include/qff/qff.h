@@ -116,7 +116,12 @@ int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
 
 /* One part of a grouped product: W [rows, cols] affine-Q4 as above (its own
  * scales/biases, sb_dtype of the call) and its output y [batch, rows] of
- * y_dtype. */
+ * y_dtype. residual, when not NULL, is [batch, rows] of y_dtype and the part
+ * writes y = residual + x W^T: the out-projection's residual add
+ * (qwen_residual_add_f32, deltanet.metal:454-463, dispatched after the out
+ * projection at QwenQ4ActiveExpertStreamingRunner.swift:1034-1040 and
+ * 1162-1166) folded into the product's store. residual may be y itself;
+ * any other overlap of residual and y is undefined. */
 typedef struct qff_q4_part {
     const uint32_t* w;
     const void* scales;
@@ -124,6 +129,7 @@ typedef struct qff_q4_part {
     int rows;
     void* y;
     qff_dtype y_dtype;
+    const void* residual;
 } qff_q4_part;
 
 #define QFF_Q4_MAX_PARTS 8
@@ -139,6 +145,22 @@ typedef struct qff_q4_part {
 int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts,
                         int nparts, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
                         int cols, int batch);
+
+/* The layer's decode/prefill front-end: RMSNorm of each token of x, then
+ * the grouped product of qff_q4_matmul_parts on the normalised rows,
+ *   xn[m, c] = x[m, c] * rsqrt(mean_c x[m, c]^2 + eps) * norm_w[c],
+ *   y_p = xn W_p^T (+ residual_p),
+ * in one pass over the weights (no normalised copy of x is written).
+ * Replaces qwen_rmsnorm_f32 (deltanet.metal:18-53, weight used as is, mean
+ * over the row) followed by the in-projections, as dispatched at
+ * QwenQ4ActiveExpertStreamingRunner.swift:973-997 (DeltaNet layer) and
+ * 1043-1074 (full-attention layer). norm_w [cols] of norm_dtype (F32 or
+ * BF16). The product rounds x[m, c] * norm_w[c] to bf16 and applies the
+ * per-token inverse RMS to the fp32 row sums. */
+int qff_q4_norm_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts,
+                             int nparts, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
+                             const void* norm_w, qff_dtype norm_dtype, float eps,
+                             int cols, int batch);
 
 /* ---------------------------------------------------------------- DeltaNet */
 

@@ -37,7 +37,8 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_d = take(S * 8 * sizeof(float));
     L.gqa_o = take(S * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
-    L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 64 * sizeof(float));
+    L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * (64 + 1) * sizeof(float));   // 64 group sums + inverse RMS
+    L.q4_xn = take(static_cast<size_t>(kQ4GemmMinBatch - 1) * 4096 * sizeof(uint16_t));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(float));
     L.dn_o = take(B * 4096 * sizeof(float));
@@ -158,6 +159,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_qb = u16(L.gqa_qb);
     c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
+    c->q4_xn = u16(L.q4_xn);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
     c->dn_o = reinterpret_cast<float*>(base + L.dn_o);
     c->sched = reinterpret_cast<unsigned*>(base + L.sched);
@@ -261,8 +263,8 @@ int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w, const vo
     return QFF_OK;
 }
 
-int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts, int nparts,
-                        qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
+static int check_q4_parts(const qff_ctx* ctx, const qff_q4_part* parts, int nparts, qff_dtype sb_dtype,
+                          const void* x, qff_dtype x_dtype, int cols, int batch) {
     if (!ctx || !parts || !x || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return QFF_ERR_INVALID_ARG;
     if (sb_dtype != QFF_F16 && sb_dtype != QFF_BF16) return QFF_ERR_INVALID_ARG;
     if (!dtype_ok(x_dtype) || cols <= 0 || batch <= 0) return QFF_ERR_INVALID_ARG;
@@ -272,13 +274,28 @@ int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* pa
             return QFF_ERR_INVALID_ARG;
     }
     if (cols % 64 != 0 || cols > 4096) return QFF_ERR_UNSUPPORTED;
-    if (batch >= kQ4GemmMinBatch) {
-        for (int i = 0; i < nparts; ++i)
-            QFF_CHECK_HIP(launch_q4_matmul(ctx, stream, parts[i].w, parts[i].scales, parts[i].biases, sb_dtype,
-                                           x, x_dtype, parts[i].y, parts[i].y_dtype, parts[i].rows, cols, batch));
-        return QFF_OK;
-    }
-    QFF_CHECK_HIP(launch_q4_gemv_parts(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, cols, batch));
+    return QFF_OK;
+}
+
+int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts, int nparts,
+                        qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
+    const int st = check_q4_parts(ctx, parts, nparts, sb_dtype, x, x_dtype, cols, batch);
+    if (st != QFF_OK) return st;
+    QFF_CHECK_HIP(launch_q4_parts(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, Q4Norm{}, cols, batch));
+    return QFF_OK;
+}
+
+int qff_q4_norm_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts, int nparts,
+                             qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const void* norm_w,
+                             qff_dtype norm_dtype, float eps, int cols, int batch) {
+    const int st = check_q4_parts(ctx, parts, nparts, sb_dtype, x, x_dtype, cols, batch);
+    if (st != QFF_OK) return st;
+    if (!norm_w || !dtype_ok(norm_dtype) || !(eps >= 0.0f)) return QFF_ERR_INVALID_ARG;
+    Q4Norm norm;
+    norm.w = norm_w;
+    norm.wbf16 = norm_dtype == QFF_BF16;
+    norm.eps = eps;
+    QFF_CHECK_HIP(launch_q4_parts(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, batch));
     return QFF_OK;
 }
 

@@ -38,9 +38,12 @@ struct qff_ctx {
     float* gqa_o = nullptr;       // [gqa_slots(cfg) * 8 * 256]
     // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
     uint16_t* gqa_qb = nullptr;
-    // Many-token Q4 products: per-token group sums [q4_xs_tokens][64] fp32.
+    // Many-token Q4 products: per-token group sums [64 + 1][q4_xs_tokens] fp32
+    // (row G after the groups: the inverse RMS of a normed product).
     float* q4_xs = nullptr;
     int q4_xs_tokens = 0;
+    // Normed decode-batch Q4 products: bf16(x w_norm) [32][4096].
+    uint16_t* q4_xn = nullptr;
     // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
     // chunk intermediates.
     float* pf_o = nullptr;
@@ -69,7 +72,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, q4_xn, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
@@ -133,10 +136,18 @@ hipError_t launch_q4_dequant(hipStream_t stream, const uint32_t* w, const void* 
 hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
                             const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
                             void* y, qff_dtype y_dtype, int rows, int cols, int batch);
-// Decode-batch product over up to QFF_Q4_MAX_PARTS parts in one launch
-// (batch < the GEMM threshold).
-hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
-                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch);
+// RMSNorm of each token of x folded into a Q4 product:
+// xn = x * rsqrt(mean(x^2) + eps) * w; w == nullptr means no norm.
+struct Q4Norm {
+    const void* w = nullptr;
+    int wbf16 = 0;
+    float eps = 0.0f;
+};
+// Product over up to QFF_Q4_MAX_PARTS parts sharing x: one launch for decode
+// batches, one group-sum pass plus one tiled launch per part for many tokens.
+hipError_t launch_q4_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                           qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm, int cols,
+                           int batch);
 constexpr int kQ4GemmMinBatch = 33;   // batches at least this large take the tiled GEMM
 hipError_t launch_kv_append(hipStream_t stream, const float* k, const float* v, void* k_cache,
                             void* v_cache, qff_dtype cache_dtype, int pos, int max_seq);

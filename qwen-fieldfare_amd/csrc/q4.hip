@@ -76,8 +76,7 @@ __device__ __forceinline__ u32x4_t interleave8(u32x4_t v) {
 // The waves' partial sums meet in LDS. RT = 4 reads x a quarter as often
 // per weight byte (several tokens over long matrices); RT = 1 gives the most
 // workgroups (batch 1, short matrices).
-constexpr int kQ4GemvMaxWaves = 8;
-constexpr int kQ4GemvGroupsPerWave = 8;
+constexpr int kQ4GemvMaxWaves = 16;
 
 // Q4Parts: the parts of one launch (a single product is one part):
 // workgroups blk0[p] .. blk0[p+1]-1 take part p's row blocks.
@@ -88,27 +87,64 @@ struct Q4Parts {
     void* y[QFF_Q4_MAX_PARTS];
     int rows[QFF_Q4_MAX_PARTS];
     int ybf16[QFF_Q4_MAX_PARTS];
+    const void* res[QFF_Q4_MAX_PARTS];   // residual of y's dtype, or null
     int blk0[QFF_Q4_MAX_PARTS + 1];
     int n;
 };
 
-__host__ __device__ constexpr int q4_gemv_waves(int cols) { return cols >= 4096 ? 8 : cols >= 512 ? cols / 512 : 1; }
-__host__ __device__ constexpr int q4_lds_stride(int cols) { return cols / 8 + 8; }   // dwords per staged row
-
-template <int RT, int NBT>
-__host__ __device__ constexpr int q4_gemv_lds_bytes(int cols) {
-    return (16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8) >
-                   q4_gemv_waves(cols) * RT * NBT * 64 * 16
-               ? 16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8
-               : q4_gemv_waves(cols) * RT * NBT * 64 * 16;
+// y[i] of part p = v (+ residual[i]), in the part's output dtype
+__device__ __forceinline__ void q4_store(const Q4Parts& parts, int p, size_t i, float v) {
+    const bool bf = parts.ybf16[p];
+    if (parts.res[p]) v += bf ? elem<1>::load(parts.res[p], i) : elem<0>::load(parts.res[p], i);
+    if (bf) elem<1>::store(parts.y[p], i, v);
+    else elem<0>::store(parts.y[p], i, v);
 }
 
-template <int SB_DT, int X_DT, int NBT, int RT>
+// N consecutive RMSNorm weights from column c (N a multiple of 8, c of 8),
+// f32 or bf16 without a branch on the dtype (a branch around loads makes the
+// compiler wait for every load in flight at the join): per 8 weights two
+// 16-B loads, the second a repeat of the first for bf16, and selects.
+template <int N>
+__device__ __forceinline__ void q4_norm_weights(const Q4Norm& nrm, int c, float (&wn)[N]) {
+    const bool bf = nrm.wbf16;
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) {
+        const char* base = static_cast<const char*>(nrm.w) + static_cast<size_t>(c + 8 * q) * (bf ? 2 : 4);
+        const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(base);
+        const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(base + (bf ? 0 : 16));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t f = e < 4 ? lo[e] : hi[e - 4];
+            const uint32_t h = (e & 1) ? (lo[e >> 1] & 0xffff0000u) : (lo[e >> 1] << 16);
+            wn[8 * q + e] = __uint_as_float(bf ? h : f);
+        }
+    }
+}
+
+// Groups per wave: 2 up to 2048 columns, 4 up to 4096 (at most 16 waves).
+__host__ __device__ constexpr int q4_gemv_gpw(int cols) { return cols > 2048 ? 4 : 2; }
+template <int GPW>
+__host__ __device__ constexpr int q4_gemv_waves(int cols) { return (cols / 64 + GPW - 1) / GPW; }
+__host__ __device__ constexpr int q4_lds_stride(int cols) { return cols / 8 + 8; }   // dwords per staged row
+
+template <int RT, int NBT, int GPW>
+__host__ __device__ constexpr int q4_gemv_lds_bytes(int cols) {
+    return (16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8) >
+                   q4_gemv_waves<GPW>(cols) * RT * NBT * 64 * 16
+               ? 16 * RT * q4_lds_stride(cols) * 4 + 16 * RT * (cols / 64) * 8
+               : q4_gemv_waves<GPW>(cols) * RT * NBT * 64 * 16;
+}
+
+template <int SB_DT, int X_DT, int NBT, int RT, bool RS, int GPW>
 __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
-                                                                       int cols, int batch) {
+                                                                       int cols, int batch,
+                                                                       const float* __restrict__ rs) {
     constexpr int RW = 16 * RT;                     // rows per workgroup
+    // per thread at most PPT weight pieces and SBT scale/bias entries:
+    // RW * (cols / 32) / (64 nw) <= RW GPW / 32 with nw = ceil(G / GPW)
+    constexpr int PPT = RW * GPW / 32, SBT = (RW * GPW + 63) / 64;
     const int G = cols / 64, W8 = cols / 8, S = q4_lds_stride(cols);
-    const int nw = q4_gemv_waves(cols), NT = 64 * nw;
+    const int nw = q4_gemv_waves<GPW>(cols), NT = 64 * nw;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
     int p = 0;
@@ -128,28 +164,28 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     f32x4_t* part = reinterpret_cast<f32x4_t*>(q4lds);
 
     // weight pieces (16 B): piece q -> row q / (W8/4), words 4 (q % (W8/4));
-    // at most RW/4 per thread (NT >= W8), clamped so every load is issued
+    // at most PPT per thread, clamped so every load is issued
     const int ppr = W8 / 4, npieces = RW * ppr;
-    u32x4_t wp[RW / 4];
+    u32x4_t wp[PPT];
 #pragma unroll
-    for (int i = 0; i < RW / 4; ++i) {
+    for (int i = 0; i < PPT; ++i) {
         const int q = min(t + NT * i, npieces - 1);
         const int r = q / ppr, c4 = q - r * ppr;
         wp[i] = *reinterpret_cast<const u32x4_t*>(w + static_cast<size_t>(min(R0 + r, rows - 1)) * W8 + 4 * c4);
     }
-    // scales/biases: at most RW/8 entries per thread (NT >= 8 G)
-    float sreg[RW / 8], breg[RW / 8];
+    // scales/biases: at most SBT entries per thread
+    float sreg[SBT], breg[SBT];
 #pragma unroll
-    for (int k = 0; k < RW / 8; ++k) {
+    for (int k = 0; k < SBT; ++k) {
         const int idx = min(t + NT * k, RW * G - 1);
         const size_t gi = static_cast<size_t>(min(R0 + idx / G, rows - 1)) * G + idx % G;
         sreg[k] = elem<SB_DT>::load(scales, gi);
         breg[k] = elem<SB_DT>::load(biases, gi);
     }
     // this lane's x (16 values per group and token tile): bf16 activations
-    // for all 8 groups of its wave up front; fp32 ones (converted to bf16
+    // for all GPW groups of its wave up front; fp32 ones (converted to bf16
     // as they arrive) group by group in the product loop
-    const int g0 = wave * kQ4GemvGroupsPerWave, gn = min(kQ4GemvGroupsPerWave, G - g0);
+    const int g0 = wave * GPW, gn = min(GPW, G - g0);
     auto load_x = [&](int i, u32x4_t (&xo2)[NBT][2]) {
         const int g = min(g0 + i, G - 1);
 #pragma unroll
@@ -168,14 +204,14 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
             }
         }
     };
-    constexpr int kXPre = X_DT == 1 ? kQ4GemvGroupsPerWave : 1;
+    constexpr int kXPre = X_DT == 1 ? GPW : 1;
     u32x4_t xv[kXPre][NBT][2];
     if (X_DT == 1) {
 #pragma unroll
         for (int i = 0; i < kXPre; ++i) load_x(i, xv[i]);
     }
 #pragma unroll
-    for (int i = 0; i < RW / 4; ++i) {
+    for (int i = 0; i < PPT; ++i) {
         const int q = t + NT * i;
         if (q < npieces) {
             const int r = q / ppr, c4 = q - r * ppr;
@@ -183,7 +219,7 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         }
     }
 #pragma unroll
-    for (int k = 0; k < RW / 8; ++k) {
+    for (int k = 0; k < SBT; ++k) {
         const int idx = t + NT * k;
         if (idx < RW * G) sb[idx] = make_float2(sreg[k], breg[k] - 128.0f * sreg[k]);
     }
@@ -194,11 +230,11 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) acc[rt][bt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // all 8 groups unrolled (groups past the row end, only for cols < 512,
-    // read group G-1 and are masked), so the LDS reads, shuffles and MFMAs of
-    // different groups overlap
+    // the wave's GPW groups unrolled (groups past the row end read group
+    // G-1 and are masked), so the LDS reads, shuffles and MFMAs of different
+    // groups overlap
 #pragma unroll
-    for (int i = 0; i < kQ4GemvGroupsPerWave; ++i) {
+    for (int i = 0; i < GPW; ++i) {
         const int g = min(g0 + i, G - 1);
         const float keep = i < gn ? 1.0f : 0.0f;
         float xsum[NBT];
@@ -254,13 +290,11 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         for (int ww = 1; ww < nw; ++ww) v += part[(ww * RT * NBT + tile) * 64 + lane];
         const int m = 16 * bt + n;
         if (m < batch) {
+            if (RS) v *= rs[m];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = R0 + 16 * rt + 4 * kb + j;
-                if (r < rows) {
-                    if (parts.ybf16[p]) elem<1>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
-                    else elem<0>::store(parts.y[p], static_cast<size_t>(m) * rows + r, v[j]);
-                }
+                if (r < rows) q4_store(parts, p, static_cast<size_t>(m) * rows + r, v[j]);
             }
         }
     }
@@ -268,25 +302,36 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
 
 // ---- single-token product on the vector units ---------------------------------
 //
-// Batch 1 is latency bound, so this path has no LDS staging, no barrier and
-// no cross-wave reduction: a wave streams whole weight rows, one 16-B load
-// per lane per 2048 columns (lane l takes columns 32l .. 32l+31 of each
-// 2048), all RPW rows' loads in flight at once, and multiplies on the vector
-// units: the nibbles of a word become floats with two masks and byte
-// conversions, y_lane = s (sum q x) + b (sum x) over the lane's half group.
-// The RPW row sums meet in a reduce-scatter over the wave (7 shuffles).
-// x is rounded to bf16, as on the matrix-core path.
-// byte I of v as a float (one v_cvt_f32_ubyteI)
-template <int I>
-__device__ __forceinline__ float ubyte_f32(uint32_t v) { return static_cast<float>((v >> (8 * I)) & 0xffu); }
-
+// Batch 1 is latency bound, so this path streams the weights straight into
+// registers (no LDS staging of weights): a wave takes kQ4VecRows whole rows,
+// one 16-B load per lane per 2048 columns (lane l takes the 32-column piece
+// l of each 2048), all rows' loads in flight from the first instruction.
+// Meanwhile the workgroup prepares x once for its four waves: each thread
+// converts 8 columns to bf16 (with NORM: bf16(x w_norm), plus its share of
+// sum x^2), stores them in LDS in the pair order of the nibble conversion
+// below, and the 32-column piece sums; one barrier. Products run on the
+// vector units: the nibbles of a word become four bf16 pairs 128 + q with
+// one shift and one and-or each (pair h = columns h and h + 4 of the word),
+// and v_dot2_f32_bf16 takes a pair of them against the matching pair of x,
+// so per group and row sum_c W x = s P + (b - 128 s) X over the lane's half
+// group (P = sum (128 + q) x, X = sum x). The row sums meet in a
+// reduce-scatter over the wave (6 shuffles); with NORM they are scaled by
+// the token's inverse RMS.
 constexpr int kQ4VecRows = 4;      // rows per wave
 constexpr int kQ4VecWaves = 4;     // waves per workgroup
 
-template <int SB_DT, int X_DT, int KW>
+typedef __bf16 q4_bf16x2_t __attribute__((ext_vector_type(2)));
+
+// c + a.lo b.lo + a.hi b.hi (bf16 pairs), v_dot2_f32_bf16
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(q4_bf16x2_t, a), __builtin_bit_cast(q4_bf16x2_t, b),
+                                           c, false);
+}
+
+template <int SB_DT, int X_DT, int KW, bool NORM>
 __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts parts, const void* __restrict__ x,
-                                                                    int cols) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                                                    int cols, Q4Norm nrm) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     int p = 0;
 #pragma unroll
     for (int i = 1; i < QFF_Q4_MAX_PARTS; ++i) p += (i < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[i]);
@@ -296,6 +341,30 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
     const int rows = parts.rows[p];
     const int R0 = ((blockIdx.x - parts.blk0[p]) * kQ4VecWaves + wave) * kQ4VecRows;
     const int G = cols / 64, W8 = cols / 8, npc = cols / 32;   // 32-column pieces per row
+
+    // x (and the norm weights) first: the workgroup's preparation below waits
+    // for these loads only, while the weight rows are still arriving.
+    // Slice i = columns 8i .. 8i+7 of x.
+    constexpr int NS = KW * 256 / (64 * kQ4VecWaves);   // slices per thread
+    float v[NS][8], wn[NS][8];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int ic = min(t + 64 * kQ4VecWaves * k, W8 - 1);
+        if (X_DT == 1) {
+            const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + 8 * ic);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[k][2 * e] = __uint_as_float(u[e] << 16);
+                v[k][2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+            }
+        } else {
+            const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 8 * ic);
+            const float4 f0 = f[0], f1 = f[1];
+            v[k][0] = f0.x; v[k][1] = f0.y; v[k][2] = f0.z; v[k][3] = f0.w;
+            v[k][4] = f1.x; v[k][5] = f1.y; v[k][6] = f1.z; v[k][7] = f1.w;
+        }
+        if (NORM) q4_norm_weights<8>(nrm, 8 * ic, wn[k]);
+    }
 
     // weights and group constants of this wave's rows, all in flight
     u32x4_t wq[kQ4VecRows][KW];
@@ -311,77 +380,71 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
             bv[r][k] = elem<SB_DT>::load(biases, row * G + pc / 2);
         }
     }
-    // this lane's x: columns 32pc .. 32pc+31, as bf16-rounded floats in the
-    // order the nibble masks produce (even nibbles of a word, then odd)
-    float xe[KW][4][8];
-    float xs[KW];
+
+    // x once per workgroup: slice i -> xl[i] as the four bf16 pairs
+    // (x0 x4, x1 x5, x2 x6, x3 x7); xsl[i / 4] = its 32-column piece's sum
+    __shared__ u32x4_t xl[64 * KW * 4];
+    __shared__ float xsl[64 * KW];
+    __shared__ float ssl[kQ4VecWaves];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int i = t + 64 * kQ4VecWaves * k;
+        const bool live = i < W8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = live ? v[k][e] : 0.0f;
+        if (NORM) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                ss = fmaf(v[k][e], v[k][e], ss);
+                v[k][e] *= wn[k][e];
+            }
+        }
+        u32x4_t xb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xb[e] = pack_bf16x2(v[k][e], v[k][e + 4]);   // exact for bf16 x, no norm
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += __uint_as_float(xb[e] << 16) + __uint_as_float(xb[e] & 0xffff0000u);
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (live) {
+            xl[i] = xb;
+            if ((i & 3) == 0) xsl[i >> 2] = sum;
+        }
+    }
+    if (NORM) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) ssl[wave] = ss;
+    }
+    __syncthreads();
+
+    float part[kQ4VecRows];
+#pragma unroll
+    for (int r = 0; r < kQ4VecRows; ++r) part[r] = 0.0f;
 #pragma unroll
     for (int k = 0; k < KW; ++k) {
         const int pc = lane + 64 * k;
         const bool live = pc < npc;
         const int pcc = min(pc, npc - 1);
-        float v[32];
-        if (X_DT == 1) {
+        u32x4_t xv[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + 32 * pcc + 8 * q);
+        for (int j = 0; j < 4; ++j) xv[j] = xl[4 * pcc + j];
+        const float xs = live ? xsl[pcc] : 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[8 * q + 2 * e] = __uint_as_float(u[e] << 16);
-                    v[8 * q + 2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 32 * pcc)[q];
-                v[4 * q] = bf16_to_f32(f32_to_bf16(f.x));
-                v[4 * q + 1] = bf16_to_f32(f32_to_bf16(f.y));
-                v[4 * q + 2] = bf16_to_f32(f32_to_bf16(f.z));
-                v[4 * q + 3] = bf16_to_f32(f32_to_bf16(f.w));
-            }
-        }
-        float sum = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 32; ++c) {
-            v[c] = live ? v[c] : 0.0f;
-            sum += v[c];
-        }
-        xs[k] = sum;
-        // word j of the piece holds columns 8j .. 8j+7 (nibble c lowest first):
-        // w & 0x0F0F0F0F gives columns 8j + 0, 2, 4, 6 in bytes 0..3, the odd
-        // ones come from w >> 4
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                xe[k][j][bb] = v[8 * j + 2 * bb];
-                xe[k][j][4 + bb] = v[8 * j + 2 * bb + 1];
-            }
-    }
-    float part[kQ4VecRows];
-#pragma unroll
-    for (int r = 0; r < kQ4VecRows; ++r) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KW; ++k) {
+        for (int r = 0; r < kQ4VecRows; ++r) {
             float dq = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t wd = wq[r][k][j];
-                const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
-                dq = fmaf(ubyte_f32<0>(lo), xe[k][j][0], dq);
-                dq = fmaf(ubyte_f32<1>(lo), xe[k][j][1], dq);
-                dq = fmaf(ubyte_f32<2>(lo), xe[k][j][2], dq);
-                dq = fmaf(ubyte_f32<3>(lo), xe[k][j][3], dq);
-                dq = fmaf(ubyte_f32<0>(hi), xe[k][j][4], dq);
-                dq = fmaf(ubyte_f32<1>(hi), xe[k][j][5], dq);
-                dq = fmaf(ubyte_f32<2>(hi), xe[k][j][6], dq);
-                dq = fmaf(ubyte_f32<3>(hi), xe[k][j][7], dq);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) dq = dot2_bf16(((wd >> (4 * h)) & 0x000F000Fu) | 0x43004300u, xv[j][h], dq);
             }
-            acc = fmaf(sv[r][k], dq, fmaf(bv[r][k], xs[k], acc));
+            // pieces past the row end (cols < 2048) hold a copy: weight zero
+            const float sk = live ? sv[r][k] : 0.0f, bk = live ? bv[r][k] : 0.0f;
+            part[r] = fmaf(sk, dq, fmaf(fmaf(-128.0f, sk, bk), xs, part[r]));
         }
-        part[r] = acc;
     }
     // reduce-scatter: lane ^ 32 and ^ 16 halve the four rows, then ^ 8 .. ^ 1
     const bool b5 = lane & 32, b4 = lane & 16;
@@ -396,13 +459,16 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
     q1 += __shfl_xor(q1, 4, 64);
     q1 += __shfl_xor(q1, 2, 64);
     q1 += __shfl_xor(q1, 1, 64);
+    if (NORM) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kQ4VecWaves; ++ww) sq += ssl[ww];
+        q1 *= rsqrtf(sq / static_cast<float>(cols) + nrm.eps);
+    }
     // lane 16 * (2 b5 + b4) holds row 2 b5 + b4
     if ((lane & 15) == 0) {
         const int r = R0 + (lane >> 4);
-        if (r < rows) {
-            if (parts.ybf16[p]) elem<1>::store(parts.y[p], r, q1);
-            else elem<0>::store(parts.y[p], r, q1);
-        }
+        if (r < rows) q4_store(parts, p, r, q1);
     }
 }
 
@@ -431,46 +497,84 @@ constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
 
 // X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
 // lane l sums half-groups l, l + 64 (32 columns each), pairs of lanes combine.
-template <int X_DT>
+// With NORM the summed values are bf16(x w_norm), row G of xs takes the
+// token's inverse RMS, rsqrt(mean(x^2) + eps), from the same pass, and xn
+// (when not null, [batch, cols]) the bf16(x w_norm) values themselves.
+template <int X_DT, bool NORM>
 __global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x, float* __restrict__ xs, int cols,
-                                                      int batch, int xs_stride) {
+                                                      int batch, int xs_stride, Q4Norm nrm,
+                                                      uint16_t* __restrict__ xn) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = cols / 64;
     if (m >= batch) return;
+    float ss = 0.0f;
     for (int hg0 = 0; hg0 < 2 * G; hg0 += 64) {
         const int hg = hg0 + lane;
         float acc = 0.0f;
         if (hg < 2 * G) {
             const size_t o = static_cast<size_t>(m) * cols + 32 * hg;
+            float v[32];
+            if (X_DT == 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (X_DT == 1) {
-                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + o + 8 * i);
+                for (int i = 0; i < 4; ++i) {
+                    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + o + 8 * i);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc += __uint_as_float(v[j] << 16) + __uint_as_float(v[j] & 0xffff0000u);
-                } else {
-                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + o + 8 * i);
-                    const float4 a = p[0], b = p[1];
-                    acc += bf16_to_f32(f32_to_bf16(a.x)) + bf16_to_f32(f32_to_bf16(a.y)) +
-                           bf16_to_f32(f32_to_bf16(a.z)) + bf16_to_f32(f32_to_bf16(a.w)) +
-                           bf16_to_f32(f32_to_bf16(b.x)) + bf16_to_f32(f32_to_bf16(b.y)) +
-                           bf16_to_f32(f32_to_bf16(b.z)) + bf16_to_f32(f32_to_bf16(b.w));
+                    for (int j = 0; j < 4; ++j) {
+                        v[8 * i + 2 * j] = __uint_as_float(u[j] << 16);
+                        v[8 * i + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+                    }
                 }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + o)[i];
+                    v[4 * i] = f.x;
+                    v[4 * i + 1] = f.y;
+                    v[4 * i + 2] = f.z;
+                    v[4 * i + 3] = f.w;
+                }
+            }
+            if (NORM) {
+                float wn[32];
+                q4_norm_weights<32>(nrm, 32 * hg, wn);
+#pragma unroll
+                for (int c = 0; c < 32; ++c) {
+                    ss = fmaf(v[c], v[c], ss);
+                    v[c] *= wn[c];
+                }
+            }
+            if (NORM || X_DT == 0) {
+#pragma unroll
+                for (int c = 0; c < 32; ++c) v[c] = bf16_to_f32(f32_to_bf16(v[c]));
+            }
+#pragma unroll
+            for (int c = 0; c < 32; ++c) acc += v[c];
+            if (NORM && xn) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<u32x4_t*>(xn + o + 8 * i) =
+                        u32x4_t{pack_bf16x2(v[8 * i], v[8 * i + 1]), pack_bf16x2(v[8 * i + 2], v[8 * i + 3]),
+                                pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7])};
             }
         }
         acc += __shfl_xor(acc, 1, 64);
         if ((lane & 1) == 0 && hg < 2 * G) xs[static_cast<size_t>(hg >> 1) * xs_stride + m] = acc;
     }
+    if (NORM) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) xs[static_cast<size_t>(G) * xs_stride + m] = rsqrtf(ss / static_cast<float>(cols) + nrm.eps);
+    }
 }
 
-template <int SB_DT, int X_DT, int Y_DT>
+template <int SB_DT, int X_DT, int Y_DT, bool NORM>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint16_t* __restrict__ biases,
                                                       const void* __restrict__ x, const float* __restrict__ xs,
-                                                      int xs_stride, void* __restrict__ y, int rows, int cols,
-                                                      int batch) {
+                                                      int xs_stride, void* __restrict__ y,
+                                                      const void* __restrict__ res, int rows, int cols,
+                                                      int batch, Q4Norm nrm) {
     const int G = cols / 64;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
@@ -500,7 +604,32 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict
         wreg = *reinterpret_cast<const u32x4_t*>(wsrc + 8 * g);
         xsreg = xs[static_cast<size_t>(g) * xs_stride + xsm];
         const size_t xo = static_cast<size_t>(xm) * cols + 64 * g + 32 * shalf;
-        if (X_DT == 1) {
+        if (NORM) {
+            // bf16(x w_norm); the token's inverse RMS scales the result
+            float wn[32];
+            q4_norm_weights<32>(nrm, 64 * g + 32 * shalf, wn);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v[8];
+                if (X_DT == 1) {
+                    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * i);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        v[2 * j] = __uint_as_float(u[j] << 16);
+                        v[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+                    }
+                } else {
+                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo + 8 * i);
+                    const float4 a = p[0], b = p[1];
+                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+                }
+                xreg[i] = u32x4_t{pack_bf16x2(v[0] * wn[8 * i], v[1] * wn[8 * i + 1]),
+                                  pack_bf16x2(v[2] * wn[8 * i + 2], v[3] * wn[8 * i + 3]),
+                                  pack_bf16x2(v[4] * wn[8 * i + 4], v[5] * wn[8 * i + 5]),
+                                  pack_bf16x2(v[6] * wn[8 * i + 6], v[7] * wn[8 * i + 7])};
+            }
+        } else if (X_DT == 1) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 xreg[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * i);
@@ -611,10 +740,16 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict
     for (int mt = 0; mt < 4; ++mt) {
         const int m = M0 + 64 * wm + 16 * mt + n;
         if (m >= batch) continue;
+        const float rs = NORM ? xs[static_cast<size_t>(G) * xs_stride + m] : 1.0f;
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const int r = R0 + 64 * wr + 16 * rt + 4 * kb;
             const size_t o = static_cast<size_t>(m) * rows + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (NORM) acc[rt][mt][i] *= rs;
+                if (res && r + i < rows) acc[rt][mt][i] += elem<Y_DT>::load(res, o + i);
+            }
             if (r + 3 < rows && (rows & 3) == 0) {
                 if (Y_DT == 1)
                     *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
@@ -641,44 +776,6 @@ hipError_t launch_q4_dequant(hipStream_t stream, const uint32_t* w, const void* 
     return hipGetLastError();
 }
 
-hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
-                            const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
-                            void* y, qff_dtype y_dtype, int rows, int cols, int batch) {
-    if (cols / 64 > kQ4MaxGroups) return hipErrorInvalidValue;
-    const uint16_t* s = static_cast<const uint16_t*>(scales);
-    const uint16_t* b = static_cast<const uint16_t*>(biases);
-    if (batch >= kQ4GemmMinBatch) {
-        // token slices of at most the workspace's capacity for group sums
-        for (int m0 = 0; m0 < batch; m0 += ctx->q4_xs_tokens) {
-            const int mb = min(ctx->q4_xs_tokens, batch - m0);
-            const void* xm = static_cast<const char*>(x) + static_cast<size_t>(m0) * cols * (x_dtype == QFF_BF16 ? 2 : 4);
-            void* ym = static_cast<char*>(y) + static_cast<size_t>(m0) * rows * (y_dtype == QFF_BF16 ? 2 : 4);
-            {
-                ProfScope prof(ctx, stream, "q4_xsum");
-                if (x_dtype == QFF_BF16)
-                    q4_xsum_kernel<1><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb, ctx->q4_xs_tokens);
-                else
-                    q4_xsum_kernel<0><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb, ctx->q4_xs_tokens);
-            }
-            const dim3 grid((rows + 127) / 128, (mb + 127) / 128);
-            ProfScope prof(ctx, stream, "q4_gemm");
-#define QFF_Q4G(S, X, Y) \
-    q4_gemm_kernel<S, X, Y><<<grid, 256, 0, stream>>>(w, s, b, xm, ctx->q4_xs, ctx->q4_xs_tokens, ym, rows, cols, mb)
-#define QFF_Q4G_Y(S, X) \
-    if (y_dtype == QFF_BF16) QFF_Q4G(S, X, 1); else QFF_Q4G(S, X, 0)
-#define QFF_Q4G_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4G_Y(S, 1); } else { QFF_Q4G_Y(S, 0); }
-            if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
-#undef QFF_Q4G_X
-#undef QFF_Q4G_Y
-#undef QFF_Q4G
-        }
-        return hipGetLastError();
-    }
-    const qff_q4_part part{w, scales, biases, rows, y, y_dtype};
-    return launch_q4_gemv_parts(ctx, stream, &part, 1, sb_dtype, x, x_dtype, cols, batch);
-}
-
 // Dynamic LDS past 64 KB needs the kernel's attribute raised (once per
 // kernel instantiation and size).
 template <auto Kernel>
@@ -698,31 +795,83 @@ static hipError_t q4_allow_lds(int bytes) {
         if (e_ != hipSuccess) return e_; \
     } while (0)
 
-hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
-                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, int cols, int batch) {
-    if (cols / 64 > kQ4MaxGroups || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return hipErrorInvalidValue;
-    if (batch == 1 && cols <= 4096) {
-        // one token: the vector-unit streaming path, 16 rows per workgroup
-        Q4Parts P{};
-        int blocks = 0;
-        constexpr int rwg = kQ4VecRows * kQ4VecWaves;
-        for (int i = 0; i < nparts; ++i) {
-            P.w[i] = parts[i].w;
-            P.s[i] = static_cast<const uint16_t*>(parts[i].scales);
-            P.b[i] = static_cast<const uint16_t*>(parts[i].biases);
-            P.y[i] = parts[i].y;
-            P.rows[i] = parts[i].rows;
-            P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
-            P.blk0[i] = blocks;
-            blocks += (parts[i].rows + rwg - 1) / rwg;
+// The parts laid end to end, rpb rows per workgroup.
+static Q4Parts q4_pack_parts(const qff_q4_part* parts, int nparts, int rpb, int& blocks) {
+    Q4Parts P{};
+    blocks = 0;
+    for (int i = 0; i < nparts; ++i) {
+        P.w[i] = parts[i].w;
+        P.s[i] = static_cast<const uint16_t*>(parts[i].scales);
+        P.b[i] = static_cast<const uint16_t*>(parts[i].biases);
+        P.y[i] = parts[i].y;
+        P.res[i] = parts[i].residual;
+        P.rows[i] = parts[i].rows;
+        P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
+        P.blk0[i] = blocks;
+        blocks += (parts[i].rows + rpb - 1) / rpb;
+    }
+    P.blk0[nparts] = blocks;
+    P.n = nparts;
+    return P;
+}
+
+// Many tokens: group sums (and inverse RMS) once per token slice, then one
+// tiled launch per part.
+template <bool NORM>
+static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm,
+                                int cols, int batch) {
+    for (int m0 = 0; m0 < batch; m0 += ctx->q4_xs_tokens) {
+        const int mb = min(ctx->q4_xs_tokens, batch - m0);
+        const void* xm = static_cast<const char*>(x) + static_cast<size_t>(m0) * cols * (x_dtype == QFF_BF16 ? 2 : 4);
+        {
+            ProfScope prof(ctx, stream, "q4_xsum");
+            if (x_dtype == QFF_BF16)
+                q4_xsum_kernel<1, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
+                                                                        ctx->q4_xs_tokens, norm, nullptr);
+            else
+                q4_xsum_kernel<0, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
+                                                                        ctx->q4_xs_tokens, norm, nullptr);
         }
-        P.blk0[nparts] = blocks;
-        P.n = nparts;
+        for (int i = 0; i < nparts; ++i) {
+            const qff_q4_part& q = parts[i];
+            const size_t yoff = static_cast<size_t>(m0) * q.rows * (q.y_dtype == QFF_BF16 ? 2 : 4);
+            void* ym = static_cast<char*>(q.y) + yoff;
+            const void* rm = q.residual ? static_cast<const char*>(q.residual) + yoff : nullptr;
+            const uint16_t* s = static_cast<const uint16_t*>(q.scales);
+            const uint16_t* b = static_cast<const uint16_t*>(q.biases);
+            const dim3 grid((q.rows + 127) / 128, (mb + 127) / 128);
+            ProfScope prof(ctx, stream, "q4_gemm");
+#define QFF_Q4G(S, X, Y)                                                                                 \
+    q4_gemm_kernel<S, X, Y, NORM><<<grid, 256, 0, stream>>>(q.w, s, b, xm, ctx->q4_xs, ctx->q4_xs_tokens, \
+                                                            ym, rm, q.rows, cols, mb, norm)
+#define QFF_Q4G_Y(S, X) \
+    if (q.y_dtype == QFF_BF16) QFF_Q4G(S, X, 1); else QFF_Q4G(S, X, 0)
+#define QFF_Q4G_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4G_Y(S, 1); } else { QFF_Q4G_Y(S, 0); }
+            if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
+#undef QFF_Q4G_X
+#undef QFF_Q4G_Y
+#undef QFF_Q4G
+        }
+    }
+    return hipGetLastError();
+}
+
+// Decode batches: one launch over all parts.
+template <bool NORM>
+static hipError_t q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                                qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm,
+                                int cols, int batch) {
+    int blocks = 0;
+    if (batch == 1) {
+        // one token: the vector-unit streaming path
         const bool k2 = cols > 2048;
+        const Q4Parts P = q4_pack_parts(parts, nparts, kQ4VecRows * kQ4VecWaves, blocks);
         ProfScope prof(ctx, stream, "q4_matmul");
-#define QFF_Q4S(S, X) \
-    if (k2) q4_gemv1_kernel<S, X, 2><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols); \
-    else q4_gemv1_kernel<S, X, 1><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols)
+#define QFF_Q4S(S, X)                                                                                   \
+    if (k2) q4_gemv1_kernel<S, X, 2, NORM><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols, norm); \
+    else q4_gemv1_kernel<S, X, 1, NORM><<<blocks, 64 * kQ4VecWaves, 0, stream>>>(P, x, cols, norm)
 #define QFF_Q4S_X(S) \
     if (x_dtype == QFF_BF16) { QFF_Q4S(S, 1); } else { QFF_Q4S(S, 0); }
         if (sb_dtype == QFF_BF16) { QFF_Q4S_X(1); } else { QFF_Q4S_X(2); }
@@ -730,48 +879,81 @@ hipError_t launch_q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
 #undef QFF_Q4S
         return hipGetLastError();
     }
+    // 2..32 tokens with the norm: one pass writes bf16(x w_norm) and the
+    // inverse RMS of each token to workspace, the product reads those and
+    // scales its row sums
+    const float* rs = nullptr;
+    if (NORM) {
+        {
+            ProfScope prof(ctx, stream, "q4_xsum");
+            if (x_dtype == QFF_BF16)
+                q4_xsum_kernel<1, true><<<(batch + 3) / 4, 256, 0, stream>>>(x, ctx->q4_xs, cols, batch,
+                                                                           ctx->q4_xs_tokens, norm, ctx->q4_xn);
+            else
+                q4_xsum_kernel<0, true><<<(batch + 3) / 4, 256, 0, stream>>>(x, ctx->q4_xs, cols, batch,
+                                                                           ctx->q4_xs_tokens, norm, ctx->q4_xn);
+        }
+        x = ctx->q4_xn;
+        x_dtype = QFF_BF16;
+        rs = ctx->q4_xs + static_cast<size_t>(cols / 64) * ctx->q4_xs_tokens;
+    }
     // four row tiles per workgroup when x is read for several tokens over
     // enough rows to keep one workgroup per CU busy; one otherwise
     int total_rows = 0;
     for (int i = 0; i < nparts; ++i) total_rows += parts[i].rows;
-    const bool rt4 = batch >= 2 && cols <= 2048 && total_rows >= 8192;
-    const int rw = rt4 ? 64 : 16;
-    Q4Parts P{};
-    int blocks = 0;
-    for (int i = 0; i < nparts; ++i) {
-        P.w[i] = parts[i].w;
-        P.s[i] = static_cast<const uint16_t*>(parts[i].scales);
-        P.b[i] = static_cast<const uint16_t*>(parts[i].biases);
-        P.y[i] = parts[i].y;
-        P.rows[i] = parts[i].rows;
-        P.ybf16[i] = parts[i].y_dtype == QFF_BF16;
-        P.blk0[i] = blocks;
-        blocks += (parts[i].rows + rw - 1) / rw;
-    }
-    P.blk0[nparts] = blocks;
-    P.n = nparts;
+    const bool rt4 = cols <= 2048 && total_rows >= 8192;
+    const Q4Parts P = q4_pack_parts(parts, nparts, rt4 ? 64 : 16, blocks);
     const int nbt = (batch + 15) / 16;
-    const int threads = 64 * q4_gemv_waves(cols);
+    const bool g4 = q4_gemv_gpw(cols) == 4;
     ProfScope prof(ctx, stream, "q4_matmul");
-#define QFF_Q4V(S, X, NB)                                                                          \
-    if (rt4) {                                                                                     \
-        QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, 4>>(q4_gemv_lds_bytes<4, NB>(cols)))); \
-        q4_gemv_kernel<S, X, NB, 4><<<blocks, threads, q4_gemv_lds_bytes<4, NB>(cols), stream>>>(     \
-            P, x, cols, batch);                                                                    \
-    } else {                                                                                       \
-        QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, 1>>(q4_gemv_lds_bytes<1, NB>(cols)))); \
-        q4_gemv_kernel<S, X, NB, 1><<<blocks, threads, q4_gemv_lds_bytes<1, NB>(cols), stream>>>(     \
-            P, x, cols, batch);                                                                    \
+#define QFF_Q4V1(S, X, NB, RTT, GP)                                                                        \
+    {                                                                                                      \
+        const int bytes = q4_gemv_lds_bytes<RTT, NB, GP>(cols);                                            \
+        QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, RTT, NORM, GP>>(bytes)));                  \
+        q4_gemv_kernel<S, X, NB, RTT, NORM, GP><<<blocks, 64 * q4_gemv_waves<GP>(cols), bytes, stream>>>(   \
+            P, x, cols, batch, rs);                                                                        \
+    }
+#define QFF_Q4V(S, X, NB)                                        \
+    if (rt4) {                                                   \
+        if (g4) QFF_Q4V1(S, X, NB, 4, 4) else QFF_Q4V1(S, X, NB, 4, 2) \
+    } else {                                                     \
+        if (g4) QFF_Q4V1(S, X, NB, 1, 4) else QFF_Q4V1(S, X, NB, 1, 2) \
     }
 #define QFF_Q4V_B(S, X) \
     if (nbt == 1) { QFF_Q4V(S, X, 1); } else { QFF_Q4V(S, X, 2); }
-#define QFF_Q4V_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4V_B(S, 1); } else { QFF_Q4V_B(S, 0); }
+#define QFF_Q4V_X(S)                   \
+    if constexpr (NORM) {              \
+        QFF_Q4V_B(S, 1);               \
+    } else if (x_dtype == QFF_BF16) {  \
+        QFF_Q4V_B(S, 1);               \
+    } else {                           \
+        QFF_Q4V_B(S, 0);               \
+    }
     if (sb_dtype == QFF_BF16) { QFF_Q4V_X(1); } else { QFF_Q4V_X(2); }
 #undef QFF_Q4V_X
 #undef QFF_Q4V_B
 #undef QFF_Q4V
+#undef QFF_Q4V1
     return hipGetLastError();
+}
+
+hipError_t launch_q4_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
+                           qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm, int cols,
+                           int batch) {
+    if (cols / 64 > kQ4MaxGroups || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return hipErrorInvalidValue;
+    const bool nrm = norm.w != nullptr;
+    if (batch >= kQ4GemmMinBatch)
+        return nrm ? q4_gemm_parts<true>(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, batch)
+                   : q4_gemm_parts<false>(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, batch);
+    return nrm ? q4_gemv_parts<true>(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, batch)
+               : q4_gemv_parts<false>(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, batch);
+}
+
+hipError_t launch_q4_matmul(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
+                            const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
+                            void* y, qff_dtype y_dtype, int rows, int cols, int batch) {
+    const qff_q4_part part{w, scales, biases, rows, y, y_dtype, nullptr};
+    return launch_q4_parts(ctx, stream, &part, 1, sb_dtype, x, x_dtype, Q4Norm{}, cols, batch);
 }
 
 }  // namespace qff

@@ -35,7 +35,8 @@ class GqaParams(ctypes.Structure):
 
 
 class Q4Part(ctypes.Structure):
-    _fields_ = [("w", _vp), ("scales", _vp), ("biases", _vp), ("rows", _i), ("y", _vp), ("y_dtype", _i)]
+    _fields_ = [("w", _vp), ("scales", _vp), ("biases", _vp), ("rows", _i), ("y", _vp), ("y_dtype", _i),
+                ("residual", _vp)]
 
 
 Q4_MAX_PARTS = 8
@@ -55,6 +56,7 @@ SIGNATURES = {
     "qff_q4_dequant": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i],
     "qff_q4_matmul": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i],
     "qff_q4_matmul_parts": [_vp, _vp, ctypes.POINTER(Q4Part), _i, _i, _vp, _i, _i, _i],
+    "qff_q4_norm_matmul_parts": [_vp, _vp, ctypes.POINTER(Q4Part), _i, _i, _vp, _i, _vp, _i, _f, _i, _i],
     "qff_deltanet_decode": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp, _vp,
                             _vp, _vp, _i, _i],
     "qff_deltanet_prefill": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp,

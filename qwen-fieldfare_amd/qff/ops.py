@@ -87,10 +87,7 @@ def q4_matmul(ctx: Context, w, scales, biases, x: torch.Tensor, out=None,
     return out
 
 
-def q4_matmul_parts(ctx: Context, parts, x: torch.Tensor, outs=None, out_dtypes=None):
-    """One launch of y_p = x W_p^T for every part (w, scales, biases) in
-    `parts` (all with the same cols and scale dtype), sharing x [batch, cols].
-    Returns the list of outputs [batch, rows_p]."""
+def _q4_parts(parts, x, outs, out_dtypes, residuals):
     if not 1 <= len(parts) <= Q4_MAX_PARTS:
         raise ValueError(f"1 .. {Q4_MAX_PARTS} parts")
     cols = parts[0][0].shape[1] * 8
@@ -107,10 +104,36 @@ def q4_matmul_parts(ctx: Context, parts, x: torch.Tensor, outs=None, out_dtypes=
         else:
             dt = out_dtypes[i] if out_dtypes is not None else torch.float32
             out = torch.empty(batch, rows, dtype=dt, device=x.device)
-        arr[i] = Q4Part(_ptr(w), _ptr(s), _ptr(b), rows, _ptr(out), _code(out))
+        r = residuals[i] if residuals is not None else None
+        if r is not None and (r.dtype != out.dtype or r.numel() != out.numel()):
+            raise ValueError("a residual must match its output's dtype and size")
+        arr[i] = Q4Part(_ptr(w), _ptr(s), _ptr(b), rows, _ptr(out), _code(out), _ptr(r) if r is not None else None)
         res.append(out)
+    return arr, res, x2, cols, batch
+
+
+def q4_matmul_parts(ctx: Context, parts, x: torch.Tensor, outs=None, out_dtypes=None, residuals=None):
+    """One launch of y_p = x W_p^T (+ residual_p) for every part (w, scales,
+    biases) in `parts` (all with the same cols and scale dtype), sharing x
+    [batch, cols]. `residuals`: per part None or a tensor of the output's
+    dtype and shape (may be the output itself). Returns the outputs
+    [batch, rows_p]."""
+    arr, res, x2, cols, batch = _q4_parts(parts, x, outs, out_dtypes, residuals)
     check("qff_q4_matmul_parts", lib().qff_q4_matmul_parts(ctx.handle, _stream(), arr, len(parts),
                                                            _code(parts[0][1]), _ptr(x2), _code(x2), cols, batch))
+    return res
+
+
+def q4_norm_matmul_parts(ctx: Context, parts, x: torch.Tensor, norm_w: torch.Tensor, eps: float = 1e-6,
+                         outs=None, out_dtypes=None, residuals=None):
+    """The layer front-end: RMSNorm of each token of x (weight norm_w [cols],
+    f32 or bf16, eps) feeding the grouped product of q4_matmul_parts."""
+    arr, res, x2, cols, batch = _q4_parts(parts, x, outs, out_dtypes, residuals)
+    if norm_w.numel() != cols:
+        raise ValueError("norm_w must have cols entries")
+    check("qff_q4_norm_matmul_parts", lib().qff_q4_norm_matmul_parts(
+        ctx.handle, _stream(), arr, len(parts), _code(parts[0][1]), _ptr(x2), _code(x2), _ptr(norm_w),
+        _code(norm_w), eps, cols, batch))
     return res
 
 

@@ -6,7 +6,16 @@ qff_q4_matmul is checked against an fp64 product of the dequantized matrix:
 with bf16 activations (exact MFMA operands) the relative Frobenius error must
 stay <= 1e-5 (fp32 accumulation order only); with fp32 activations, which the
 matrix cores take rounded to bf16, <= 1e-2 against the reference's own fp32
-factored order (deltanet.metal:816-861)."""
+factored order (deltanet.metal:816-861).
+
+qff_q4_norm_matmul_parts (RMSNorm, deltanet.metal:18-53, feeding the
+products) is checked twice: against a mirror of its own arithmetic
+(bf16(x w_norm) in fp32, inverse RMS in fp64, fp64 product), rel <= 1e-5 for
+fp32 outputs, and against the oracle's RMSNorm (pinned by the reference's
+KAT) followed by an fp64 product, rel <= 1e-2 (bf16 rounding of the normed
+activations). Tokens carry different scales so a norm taken from the wrong
+token shows. The residual store (y = residual + x W^T) must equal the
+product plus the residual bit for bit with fp32 outputs, in place too."""
 import numpy as np
 import pytest
 import torch
@@ -47,7 +56,10 @@ def _rel(a, b):
                                              (8192, 2048, 2), (8200, 2048, 17), (9216, 2048, 32),
                                              # many-token GEMM path (batch >= 64), ragged tiles included
                                              (512, 2048, 64), (100, 2048, 300), (8192, 2048, 256),
-                                             (2048, 4096, 130), (512, 2048, 8192)])
+                                             (2048, 4096, 130), (512, 2048, 8192),
+                                             # column counts that are not a multiple of 512
+                                             (300, 576, 5), (200, 3136, 17), (64, 1088, 2),
+                                             (8192, 1088, 4), (40, 192, 1), (40, 3136, 1)])
 def test_q4_matmul_bf16_activations(hip, rows, cols, batch):
     import qff
     print(f"q4_matmul {rows}x{cols} batch={batch}", flush=True)
@@ -155,5 +167,96 @@ def test_q4_matmul_parts_rejects_bad_calls(hip):
     with pytest.raises(ValueError):
         qff.q4_matmul_parts(ctx, [(w, s, b)] * 9, x)
     arr = (Q4Part * 1)()
-    arr[0] = Q4Part(w.data_ptr(), s.data_ptr(), b.data_ptr(), 0, x.data_ptr(), 0)   # rows = 0
+    arr[0] = Q4Part(w.data_ptr(), s.data_ptr(), b.data_ptr(), 0, x.data_ptr(), 0, None)   # rows = 0
     assert lib().qff_q4_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, 128, 1) == -1
+
+
+def _norm_mirror(x, wn, eps):
+    """bf16(x w_norm) as the product forms it (fp32 multiply, RNE to bf16)
+    and the inverse RMS of each token in fp64."""
+    x64 = x.astype(np.float64)
+    r = 1.0 / np.sqrt((x64 * x64).mean(axis=1) + eps)
+    xq = O.round_bf16((x.astype(np.float32) * wn.astype(np.float32)).astype(np.float32))
+    return xq.astype(np.float64), r
+
+
+@pytest.mark.parametrize("batch,cols,xdt,ndt", [(1, 2048, "bf16", "f32"), (1, 4096, "f32", "bf16"),
+                                                (3, 2048, "bf16", "bf16"), (16, 2048, "bf16", "f32"),
+                                                (32, 4096, "f32", "f32"), (40, 2048, "bf16", "f32"),
+                                                (300, 2048, "f32", "bf16"), (1, 128, "bf16", "f32")])
+def test_q4_norm_matmul_parts(hip, batch, cols, xdt, ndt):
+    import qff
+    print(f"q4_norm_matmul_parts batch={batch} cols={cols} x={xdt} norm={ndt}", flush=True)
+    rng = np.random.default_rng(7 * batch + cols)
+    scale = 2.0 ** (np.arange(batch) % 5 - 2)
+    x = (rng.standard_normal((batch, cols)) * scale[:, None]).astype(np.float32)
+    if xdt == "bf16":
+        x = O.round_bf16(x)
+    wn = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    if ndt == "bf16":
+        wn = O.round_bf16(wn)
+    eps = 1e-6
+    shapes = [(1056, torch.bfloat16), (32, torch.float32), (100, torch.float32)]
+    ws = [synth.q4_weight(r, cols, seed=r + batch) for r, _ in shapes]
+    parts = [_w_gpu(w, s, b, "f16") for w, s, b in ws]
+    xt = bf16_tensor(O.f32_to_bf16(x)) if xdt == "bf16" else f32_tensor(x)
+    nt = bf16_tensor(O.f32_to_bf16(wn)) if ndt == "bf16" else f32_tensor(wn)
+    ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=512)
+    outs = qff.q4_norm_matmul_parts(ctx, parts, xt, nt, eps, out_dtypes=[dt for _, dt in shapes])
+    torch.cuda.synchronize()
+    xq, r = _norm_mirror(x, wn, eps)
+    xn = np.stack([O.rmsnorm(x[m], wn, eps, prec=64) for m in range(batch)]).astype(np.float64)
+    for o, (w, s, b), (_, dt) in zip(outs, ws, shapes):
+        dense = O.q4_dequant(w, s, b, O.F16).astype(np.float64)
+        got = to_np(o)
+        assert _rel(got, r[:, None] * (xq @ dense.T)) <= (1e-5 if dt == torch.float32 else 4e-3)
+        assert _rel(got, xn @ dense.T) <= 1e-2
+
+
+@pytest.mark.parametrize("batch", [1, 7, 33])
+def test_q4_matmul_parts_residual(hip, batch):
+    """y = residual + x W^T: fp32 outputs equal the plain product plus the
+    residual bit for bit (one fp32 add), also when the residual is y itself;
+    bf16 outputs match the fp64 sum."""
+    import qff
+    print(f"q4_matmul_parts residual batch={batch}", flush=True)
+    cols, rows = 2048, 640
+    w, s, b = synth.q4_weight(rows, cols, seed=5 + batch)
+    part = _w_gpu(w, s, b, "bf16")
+    rng = np.random.default_rng(batch)
+    xb = O.f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32))
+    x = bf16_tensor(xb)
+    res = f32_tensor(rng.standard_normal((batch, rows)).astype(np.float32) * 30)
+    ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=64)
+    plain = qff.q4_matmul_parts(ctx, [part], x)[0]
+    added = qff.q4_matmul_parts(ctx, [part], x, residuals=[res])[0]
+    inplace = res.clone()
+    qff.q4_matmul_parts(ctx, [part], x, outs=[inplace], residuals=[inplace])
+    res_bf = res.to(torch.bfloat16)
+    out_bf = qff.q4_matmul_parts(ctx, [part], x, out_dtypes=[torch.bfloat16], residuals=[res_bf])[0]
+    torch.cuda.synchronize()
+    assert torch.equal(added, plain + res)
+    assert torch.equal(inplace, added)
+    ref = to_np(res_bf).astype(np.float64) + O.bf16_to_f32(xb).astype(np.float64) @ \
+        O.q4_dequant(w, s, b, O.BF16).astype(np.float64).T
+    assert _rel(to_np(out_bf), ref) <= 4e-3
+
+
+def test_q4_norm_matmul_parts_rejects_bad_calls(hip):
+    import qff
+    from qff._lib import Q4Part, lib
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=1)
+    w, s, b = _w_gpu(*synth.q4_weight(64, 128, seed=3), "f16")
+    x = torch.zeros(1, 128, dtype=torch.bfloat16, device=DEV)
+    y = torch.zeros(1, 64, device=DEV)
+    arr = (Q4Part * 1)()
+    arr[0] = Q4Part(w.data_ptr(), s.data_ptr(), b.data_ptr(), 64, y.data_ptr(), 0, None)
+    nw = torch.ones(128, device=DEV)
+    L = lib()
+    assert L.qff_q4_norm_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, None, 0, 1e-6, 128, 1) == -1
+    assert L.qff_q4_norm_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, nw.data_ptr(), 0, -1.0,
+                                      128, 1) == -1
+    assert L.qff_q4_norm_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, nw.data_ptr(), 0, 1e-6,
+                                      96, 1) == -2
+    with pytest.raises(ValueError):
+        qff.q4_norm_matmul_parts(ctx, [(w, s, b)], x, torch.ones(64, device=DEV))
