@@ -62,19 +62,48 @@ __device__ __forceinline__ float softplus(float x) {
     return log1pf(expf(x));
 }
 
-// Butterfly sum over aligned groups of `W` lanes (W a power of two <= 64);
-// every lane of the group ends with the group total.
+// Cross-lane moves for reductions over aligned lane groups, on the DPP and
+// swizzle paths rather than LDS permutes: lane ^ 1 and lane ^ 2 (quad
+// permutes), the mirror of a half row (8 lanes) and of a row (16 lanes),
+// lane ^ 16 within 32 (swizzle), and the two 32-lane halves (permlane32
+// swap). After the quad steps every lane of a quad holds the same value, so
+// the mirrors pair each quad with the other one of its half row / row just
+// as lane ^ 4 and lane ^ 8 would.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));   // and 0x1f, xor 0x10
+}
+
+// Sum over aligned groups of `W` lanes (W a power of two <= 64, all lanes of
+// the group active); every lane of the group ends with the same total.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (W >= 2) v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    if (W >= 4) v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    if (W >= 8) v += dpp_mov<0x141>(v);   // row_half_mirror
+    if (W >= 16) v += dpp_mov<0x140>(v);  // row_mirror
+    if (W >= 32) v += swizzle_xor16(v);
+    if (W >= 64) {
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // lower half + upper half, in every lane
+    }
     return v;
 }
 
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int m = W / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    if (W >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+    if (W >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+    if (W >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+    if (W >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+    if (W >= 32) v = fmaxf(v, swizzle_xor16(v));
+    if (W >= 64) {
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    }
     return v;
 }
 

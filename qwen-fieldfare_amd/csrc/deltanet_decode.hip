@@ -55,18 +55,34 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     __shared__ float v_s[256], o_s[256], red[16], gb[4];
 
     // ---- phase 1: conv + SiLU (deltanet.metal:120-137), L2 norms (:282-305) ----
+    // Its loads go first, then the phase-2 state loads, which do not depend
+    // on phase 1 and stream while it computes (loads complete in issue order,
+    // so phase 1 waits for its own loads only).
     const size_t seq_ch = static_cast<size_t>(seq) * 8192;
-    float y = 0.0f;
+    // threads 512+ load a clamped channel too (no branch around the loads)
+    const int ch = min(t < 128 ? kh * 128 + t : t < 256 ? 2048 + kh * 128 + (t - 128) : 4096 + kh * 256 + (t - 256),
+                       8191);
+    float4* sp = reinterpret_cast<float4*>(conv_state) + seq_ch + ch;
+    const float4 st = *sp;
+    const float4 w4 = reinterpret_cast<const float4*>(conv_w)[ch];
+    const float xin = elem<IN_DT>::load(qkv, seq_ch + ch);
+    const int hg = 2 * kh + (t & 1), sg = seq * 32 + hg;   // gate inputs (used by threads 0, 1)
+    const float a_in = a[sg], b_in = b[sg], alog = a_log[hg], dtb = dt_bias[hg];
+    __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the state stream
+    const int hsel = wave >> 3;                 // 0: head 2kh, 1: head 2kh+1
+    const int h = 2 * kh + hsel;
+    const int col4 = lane & 31;
+    const int rbase = (wave & 7) * 16 + (lane >> 5);
+    float4* S = reinterpret_cast<float4*>(ssm_state) + (static_cast<size_t>(seq) * 32 + h) * (128 * 32);
+    float4 s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = S[(rbase + 2 * i) * 32 + col4];
+    __builtin_amdgcn_sched_barrier(0);
+    // computed by every thread (used by 0-511) so the loads stay where they are
+    const float4 ns = make_float4(st.y, st.z, st.w, xin);
+    float y = silu(ns.x * w4.x + ns.y * w4.y + ns.z * w4.z + ns.w * w4.w);
     if (t < 512) {
-        const int ch = t < 128 ? kh * 128 + t
-                     : t < 256 ? 2048 + kh * 128 + (t - 128)
-                               : 4096 + kh * 256 + (t - 256);
-        float4* sp = reinterpret_cast<float4*>(conv_state) + seq_ch + ch;
-        const float4 st = *sp;
-        const float4 w4 = reinterpret_cast<const float4*>(conv_w)[ch];
-        const float4 ns = make_float4(st.y, st.z, st.w, elem<IN_DT>::load(qkv, seq_ch + ch));
         *sp = ns;
-        y = silu(ns.x * w4.x + ns.y * w4.y + ns.z * w4.z + ns.w * w4.w);
         if (t >= 256) v_s[t - 256] = y;
     }
     if (t < 256) {
@@ -75,9 +91,8 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     }
     if (t < 2) {
         // per value head: beta = sigmoid(b), g = exp(-exp(A_log) softplus(a + dt_bias))
-        const int h = 2 * kh + t, sh = seq * 32 + h;
-        gb[2 * t] = expf(-expf(a_log[h]) * softplus(a[sh] + dt_bias[h]));
-        gb[2 * t + 1] = sigmoid(b[sh]);
+        gb[2 * t] = expf(-expf(alog) * softplus(a_in + dtb));
+        gb[2 * t + 1] = sigmoid(b_in);
     }
     __syncthreads();
     if (t < 256) {
@@ -90,17 +105,9 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
 
     // ---- phase 2: gated delta rule, 16 rows per wave --------------------------
     // QwenDeltaNetKernel.swift:86-124; deltanet.metal:307-335.
-    const int hsel = wave >> 3;                 // 0: head 2kh, 1: head 2kh+1
-    const int h = 2 * kh + hsel;
-    const int col4 = lane & 31;
-    const int rbase = (wave & 7) * 16 + (lane >> 5);
     const float4 k4 = reinterpret_cast<const float4*>(k_s)[col4];
     const float4 q4 = reinterpret_cast<const float4*>(q_s)[col4];
     const float g = gb[2 * hsel], beta = gb[2 * hsel + 1];
-    float4* S = reinterpret_cast<float4*>(ssm_state) + (static_cast<size_t>(seq) * 32 + h) * (128 * 32);
-    float4 s[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = S[(rbase + 2 * i) * 32 + col4];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         float4 v = s[i];
