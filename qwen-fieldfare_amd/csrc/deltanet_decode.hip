@@ -68,6 +68,8 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     const float xin = elem<IN_DT>::load(qkv, seq_ch + ch);
     const int hg = 2 * kh + (t & 1), sg = seq * 32 + hg;   // gate inputs (used by threads 0, 1)
     const float a_in = a[sg], b_in = b[sg], alog = a_log[hg], dtb = dt_bias[hg];
+    const size_t oi = static_cast<size_t>(seq) * 4096 + kh * 256 + (t & 255);   // phase-3 output index
+    const float zin = elem<IN_DT>::load(z, oi), nw = norm_w[t & 127];
     __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the state stream
     const int hsel = wave >> 3;                 // 0: head 2kh, 1: head 2kh+1
     const int h = 2 * kh + hsel;
@@ -81,10 +83,7 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     // computed by every thread (used by 0-511) so the loads stay where they are
     const float4 ns = make_float4(st.y, st.z, st.w, xin);
     float y = silu(ns.x * w4.x + ns.y * w4.y + ns.z * w4.z + ns.w * w4.w);
-    if (t < 512) {
-        *sp = ns;
-        if (t >= 256) v_s[t - 256] = y;
-    }
+    if (t >= 256 && t < 512) v_s[t - 256] = y;
     if (t < 256) {
         const float ss = group_sum<64>(y * y);
         if (lane == 0) red[wave] = ss;
@@ -123,6 +122,10 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     }
     __syncthreads();
 
+    // the conv-state rewrite waits until here: a store pending at the phase-1
+    // barriers would make them wait for the state loads issued before it
+    if (t < 512) *sp = ns;
+
     // ---- phase 3: gated RMSNorm (QwenDeltaNetKernel.swift:127-151) ------------
     float o = 0.0f;
     if (t < 256) {
@@ -134,8 +137,7 @@ __global__ __launch_bounds__(1024) void deltanet_decode_kernel(
     if (t < 256) {
         const float tot = t < 128 ? red[4] + red[5] : red[6] + red[7];
         const float inv = 1.0f / sqrtf(tot / 128.0f + eps);
-        const size_t oi = static_cast<size_t>(seq) * 4096 + kh * 256 + t;
-        elem<OUT_DT>::store(out, oi, o * inv * norm_w[t & 127] * silu(elem<IN_DT>::load(z, oi)));
+        elem<OUT_DT>::store(out, oi, o * inv * nw * silu(zin));
     }
 }
 

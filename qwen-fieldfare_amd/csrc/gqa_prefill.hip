@@ -154,20 +154,27 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
         const bool more = kt + 1 < ntiles;
         if (more) tile_load(regs, k_cache, v_cache, kvh, (kt + 1) * kPfKT, kv_end, t);
         const int p0 = kt * kPfKT;
-        // S^T = K Q^T for kPfKT/16 position tiles; each half's 8 K operands
-        // are read before its MFMAs, so the LDS latency is paid twice a tile
+        // S^T = K Q^T for kPfKT/16 position tiles, 32 dims at a time: the K
+        // operands of the next 32 dims are read while the four independent
+        // MFMAs of these run
         constexpr int NPT = kPfKT / 16;
         f32x4_t s[NPT];
 #pragma unroll
         for (int pt = 0; pt < NPT; ++pt) s[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        u32x4_t ka[2][NPT];
 #pragma unroll
-        for (int pt = 0; pt < NPT; ++pt) {
-            u32x4_t ka[8];
+        for (int pt = 0; pt < NPT; ++pt)
+            ka[0][pt] = *reinterpret_cast<const u32x4_t*>(&Ks[cur][(16 * pt + n) * kKStride + 8 * kb]);
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-                ka[jj] = *reinterpret_cast<const u32x4_t*>(&Ks[cur][(16 * pt + n) * kKStride + 32 * jj + 8 * kb]);
+        for (int jj = 0; jj < 8; ++jj) {
+            if (jj + 1 < 8) {
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) s[pt] = mfma_16x16x32_bf16(ka[jj], qreg[jj], s[pt]);
+                for (int pt = 0; pt < NPT; ++pt)
+                    ka[(jj + 1) & 1][pt] = *reinterpret_cast<const u32x4_t*>(
+                        &Ks[cur][(16 * pt + n) * kKStride + 32 * (jj + 1) + 8 * kb]);
+            }
+#pragma unroll
+            for (int pt = 0; pt < NPT; ++pt) s[pt] = mfma_16x16x32_bf16(ka[jj & 1][pt], qreg[jj], s[pt]);
         }
         // softmax (base 2); lane holds q row n, positions p0 + 16pt + 4kb + i
         float tmax = -INFINITY;
