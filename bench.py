@@ -346,6 +346,42 @@ def bench_c4(B, L, steps, warmup):
             "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS if nbytes else None}
 
 
+def bench_router(ctx, B, steps, warmup, sets=64):
+    """MoE router of B tokens (the reference's decode step: 256 experts,
+    hidden 2048, Q8 weights): logits and top-8. Rotates over weight sets so
+    the 0.56 MB of weights come from HBM."""
+    import numpy as np
+    import torch
+    import qff
+    from qff import synth
+    ws = []
+    for i in range(sets):
+        w, sc, bi = synth.q8_weight(256, 2048, seed=500 + i) if i < 2 else (ws[i % 2][3], None, None)
+        if i < 2:
+            ws.append((torch.from_numpy(w.view(np.int32)).cuda(),
+                       torch.from_numpy(sc.view(np.int16)).view(torch.bfloat16).cuda(),
+                       torch.from_numpy(bi.view(np.int16)).view(torch.bfloat16).cuda(), w))
+        else:
+            src = ws[i % 2]
+            ws.append((src[0].clone(), src[1].clone(), src[2].clone(), src[3]))
+    g = torch.Generator(device="cuda").manual_seed(B)
+    x = torch.randn(B, 2048, generator=g, device="cuda")
+    lg = torch.empty(B, 256, device="cuda")
+    idx = torch.empty(B, 8, dtype=torch.int32, device="cuda")
+    scr = torch.empty(B, 8, device="cuda")
+
+    def step(i):
+        w, sc, bi, _ = ws[i % sets]
+        qff.router_top8(ctx, w, sc, bi, x, logits=lg, indices=idx, scores=scr)
+
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    kt, _ = kernel_times(ctx, step, min(steps, 64))
+    nbytes = 256 * 2048 + 2 * 256 * 32 * 2 + B * 2048 * 4
+    k = kt["router_logits"] + kt["router_top8"]
+    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "kernels_us": {k_: v * 1e3 for k_, v in kt.items()},
+            "GBps": nbytes / (k * 1e-3) / 1e9}
+
+
 def cpu_baseline_c1(min_s=10.0, max_reps=12):
     """The fp32 reference-order oracle (sequential, one thread) on the
     config-1 workload: whole 4096-token sequences from zero state, repeated
@@ -400,7 +436,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4,dnb")
+    ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4,dnb,rt")
     ap.add_argument("--copy-probe", action="store_true", help="also run one copy of known size "
                     "(calibrates FETCH_SIZE / WRITE_SIZE in a counter run)")
     args = ap.parse_args()
@@ -411,7 +447,7 @@ def main():
     import torch
     import qff
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "c3", "c4", "dnb"}
+    only = set(args.only.split(",")) if args.only else {"c0", "c1", "c2", "c3", "c4", "dnb", "rt"}
     ctx = qff.Context(max_batch=32, max_ctx=8192, max_prefill_tokens=8192)
     configs = {}
     if "c0" in only:
@@ -421,6 +457,10 @@ def main():
         for B in (16, 32):
             log(f"DeltaNet decode B={B}")
             configs[f"deltanet_decode_b{B}"] = bench_dn_decode_batch(ctx, B, max(args.steps * 5, 100), args.warmup)
+    if "rt" in only:
+        for B in (1, 16):
+            log(f"MoE router B={B}")
+            configs[f"router_top8_b{B}"] = bench_router(ctx, B, max(args.steps * 10, 200), args.warmup)
     if "c2" in only:
         for B in (1, 8, 32):
             log(f"config 2: GQA decode B={B}")

@@ -162,6 +162,35 @@ int qff_q4_norm_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_par
                              const void* norm_w, qff_dtype norm_dtype, float eps,
                              int cols, int batch);
 
+/* ------------------------------------------------------------- MoE router */
+
+/* MLX affine Q8, group 64: element c of row r is byte c % 4 (lowest first)
+ * of uint32 word w[r*(cols/4) + c/4], i.e. byte c of the row; value = byte *
+ * scale + bias with scale/bias [rows, cols/64] of sb_dtype (QFF_BF16 or
+ * QFF_F16). Test hook: writes the dequantized fp32 matrix [rows, cols],
+ * bit-exact with the closed form of deltanet.metal:863-900 (byte * scale is
+ * exact in fp32, so each value is one rounding). */
+int qff_q8_dequant(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
+                   const void* scales, const void* biases, qff_dtype sb_dtype,
+                   float* out, int rows, int cols);
+
+/* The MoE router of `batch` tokens: logits[m, e] = sum_c W[e, c] x[m, c]
+ * with W [experts, cols] affine-Q8 as above, accumulated in fp32 in the
+ * factored form scale * sum(q x) + bias * sum(x) per group; then per token
+ * the eight largest logits in descending order (equal logits: lower expert
+ * index first) into indices [batch, 8], and their routing weights into
+ * scores [batch, 8]: softmax over all `experts` logits shifted by the
+ * largest, the eight probabilities divided by their sum. x [batch, cols] of
+ * x_dtype (F32 or BF16), logits [batch, experts] fp32 (written). Replaces
+ * qwen_router_q8_logits_simd_f32 + qwen_router_top8_logits_f32
+ * (deltanet.metal:2229-2329) as dispatched at
+ * QwenQ4ActiveExpertStreamingRunner.swift:1177-1190 (experts 256, cols
+ * 2048). Requires 8 <= experts <= 256 and cols a multiple of 64, <= 4096. */
+int qff_router_top8(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
+                    const void* scales, const void* biases, qff_dtype sb_dtype,
+                    const void* x, qff_dtype x_dtype, float* logits,
+                    int32_t* indices, float* scores, int experts, int cols, int batch);
+
 /* ---------------------------------------------------------------- DeltaNet */
 
 /* Per-layer constants of a Gated DeltaNet layer (fp32, device pointers),

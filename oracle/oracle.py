@@ -79,6 +79,9 @@ def _declare(L):
     L.qffo_round_to.restype = _f
     L.qffo_round_to.argtypes = [_f, _i]
     L.qffo_q4_dequant.argtypes = [_vp, _vp, _vp, _i, _i, _i, _fp]
+    L.qffo_q8_dequant.argtypes = [_vp, _vp, _vp, _i, _i, _i, _fp]
+    L.qffo_router_logits.argtypes = [_vp, _vp, _vp, _i, _fp, _i, _i, _fp]
+    L.qffo_router_top8.argtypes = [_fp, _i, _vp, _fp]
     L.qffo_kv_append.argtypes = [_fp, _fp, _vp, _vp, _i, _i, _i, _i, _i]
     L.qffo_attention_gate.argtypes = [_vp, _fp, _i, _fp]
     L.qffo_gqa_append_kv.argtypes = [_fp, _fp, _fp, _f, _i, _f, _vp, _vp, _i, _i, _i]
@@ -354,3 +357,38 @@ def q4_matvec(w, scales, biases, x, sb_dtype=F16, prec=32):
     getattr(lib(), "qffo_q4_matvec" + s)(w.ctypes.data, _p(sc, P), _p(bi, P), _p(x, P), rows,
                                          cols, _p(y, P))
     return y
+
+
+def q8_dequant(w, scales, biases, sb_dtype=BF16):
+    """deltanet.metal:863-900 closed form. w uint32 [rows, cols/4] (byte c of
+    a row = element c); scales/biases uint16 bits [rows, cols/64]."""
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    rows, c4 = w.shape
+    cols = c4 * 4
+    s = np.ascontiguousarray(scales)
+    b = np.ascontiguousarray(biases)
+    out = np.empty((rows, cols), np.float32)
+    lib().qffo_q8_dequant(w.ctypes.data, s.ctypes.data, b.ctypes.data, sb_dtype, rows, cols, _p(out, _fp))
+    return out
+
+
+def router_logits(w, scales, biases, x, sb_dtype=BF16):
+    """deltanet.metal:2229-2259 factored order. x [cols] f32 -> [rows] f32."""
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    rows, c4 = w.shape
+    s = np.ascontiguousarray(scales)
+    b = np.ascontiguousarray(biases)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(rows, np.float32)
+    lib().qffo_router_logits(w.ctypes.data, s.ctypes.data, b.ctypes.data, sb_dtype, _p(x, _fp), rows, c4 * 4,
+                             _p(out, _fp))
+    return out
+
+
+def router_top8(logits):
+    """deltanet.metal:2283-2329: (indices int32 [8], scores f32 [8])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    idx = np.empty(8, np.int32)
+    sc = np.empty(8, np.float32)
+    lib().qffo_router_top8(_p(lg, _fp), lg.size, idx.ctypes.data, _p(sc, _fp))
+    return idx, sc

@@ -163,6 +163,93 @@ void qffo_q4_dequant(const uint32_t* w, const void* scales, const void* biases,
 }
 
 /* ------------------------------------------------------------------ */
+/* MLX affine Q8, group 64 (deltanet.metal:863-900, 2229-2259): element  */
+/* c of row r is byte c of the row (byte c % 4 of little-endian word     */
+/* c / 4); value = byte * scale + bias. byte (8 bits) x scale (<= 11     */
+/* significant bits) is exact in fp32, so the value is one rounding.     */
+void qffo_q8_dequant(const uint32_t* w, const void* scales, const void* biases,
+                     int sb_dtype, int rows, int cols, float* out) {
+    int groups = cols / 64;
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            uint32_t word = w[(size_t)r * (cols / 4) + c / 4];
+            float q = (float)((word >> (8 * (c % 4))) & 0xFFu);
+            float s = load_elem(scales, sb_dtype, (size_t)r * groups + c / 64);
+            float b = load_elem(biases, sb_dtype, (size_t)r * groups + c / 64);
+            out[(size_t)r * cols + c] = q * s + b;
+        }
+}
+
+/* Router logits, the factored order of qwen_q8_row_simd_f32            */
+/* (deltanet.metal:2229-2259) without its cross-lane split: per group    */
+/* dot = sum q x, sum = sum x, acc = fma(scale, dot, acc) then           */
+/* acc = fma(bias, sum, acc). x [cols] f32 -> logits [rows].            */
+void qffo_router_logits(const uint32_t* w, const void* scales, const void* biases, int sb_dtype,
+                        const float* x, int rows, int cols, float* logits) {
+    int groups = cols / 64;
+    for (int r = 0; r < rows; ++r) {
+        float acc = 0.0f;
+        for (int g = 0; g < groups; ++g) {
+            float s = load_elem(scales, sb_dtype, (size_t)r * groups + g);
+            float b = load_elem(biases, sb_dtype, (size_t)r * groups + g);
+            float dot = 0.0f, sum = 0.0f;
+            for (int i = 0; i < 64; ++i) {
+                int c = 64 * g + i;
+                uint32_t word = w[(size_t)r * (cols / 4) + c / 4];
+                float xv = x[c];
+                dot = fmaf((float)((word >> (8 * (c % 4))) & 0xFFu), xv, dot);
+                sum += xv;
+            }
+            acc = fmaf(s, dot, acc);
+            acc = fmaf(b, sum, acc);
+        }
+        logits[r] = acc;
+    }
+}
+
+/* Top-8 routing, qwen_router_top8_logits_f32 (deltanet.metal:2283-2329): */
+/* insertion of each logit into a descending list of eight (a later     */
+/* logit enters only if strictly larger than the eighth, and moves up   */
+/* only past strictly smaller ones, so ties keep the lower index first), */
+/* softmax over all `n` logits with the top value as the shift, and the */
+/* eight probabilities renormalised to sum to one.                       */
+void qffo_router_top8(const float* logits, int n, int32_t* idx, float* scores) {
+    int top_idx[8];
+    float top_val[8];
+    for (int k = 0; k < 8; ++k) {
+        top_idx[k] = 0;
+        top_val[k] = -INFINITY;
+    }
+    for (int i = 0; i < n; ++i) {
+        float v = logits[i];
+        if (v > top_val[7]) {
+            top_val[7] = v;
+            top_idx[7] = i;
+            for (int k = 6; k >= 0; --k) {
+                if (top_val[k + 1] <= top_val[k]) break;
+                float tv = top_val[k];
+                top_val[k] = top_val[k + 1];
+                top_val[k + 1] = tv;
+                int ti = top_idx[k];
+                top_idx[k] = top_idx[k + 1];
+                top_idx[k + 1] = ti;
+            }
+        }
+    }
+    float mx = top_val[0], den = 0.0f;
+    for (int i = 0; i < n; ++i) den += expf(logits[i] - mx);
+    float p[8], tot = 0.0f;
+    for (int k = 0; k < 8; ++k) {
+        p[k] = expf(top_val[k] - mx) / den;
+        tot += p[k];
+    }
+    for (int k = 0; k < 8; ++k) {
+        idx[k] = top_idx[k];
+        scores[k] = p[k] / tot;
+    }
+}
+
+/* ------------------------------------------------------------------ */
 /* KV append, token-major: DN:670-689. offset = (pos*nkv + kvh)*hd + d,  */
 /* value rounded to the cache dtype (reference: half; build: bf16).      */
 void qffo_kv_append(const float* k_in, const float* v_in, void* k_cache,

@@ -263,6 +263,28 @@ int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w, const vo
     return QFF_OK;
 }
 
+int qff_q8_dequant(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w, const void* scales,
+                   const void* biases, qff_dtype sb_dtype, float* out, int rows, int cols) {
+    if (!ctx || !w || !scales || !biases || !out) return QFF_ERR_INVALID_ARG;
+    if (sb_dtype != QFF_F16 && sb_dtype != QFF_BF16) return QFF_ERR_INVALID_ARG;
+    if (rows <= 0 || cols <= 0) return QFF_ERR_INVALID_ARG;
+    if (cols % 64 != 0) return QFF_ERR_UNSUPPORTED;
+    QFF_CHECK_HIP(launch_q8_dequant(stream, w, scales, biases, sb_dtype, out, rows, cols));
+    return QFF_OK;
+}
+
+int qff_router_top8(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w, const void* scales,
+                    const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, float* logits,
+                    int32_t* indices, float* scores, int experts, int cols, int batch) {
+    if (!ctx || !w || !scales || !biases || !x || !logits || !indices || !scores) return QFF_ERR_INVALID_ARG;
+    if (sb_dtype != QFF_F16 && sb_dtype != QFF_BF16) return QFF_ERR_INVALID_ARG;
+    if (!dtype_ok(x_dtype) || experts <= 0 || cols <= 0 || batch <= 0) return QFF_ERR_INVALID_ARG;
+    if (experts < 8 || experts > 256 || cols % 64 != 0 || cols > 4096) return QFF_ERR_UNSUPPORTED;
+    QFF_CHECK_HIP(launch_router_top8(ctx, stream, w, scales, biases, sb_dtype, x, x_dtype, logits, indices, scores,
+                                     experts, cols, batch));
+    return QFF_OK;
+}
+
 static int check_q4_parts(const qff_ctx* ctx, const qff_q4_part* parts, int nparts, qff_dtype sb_dtype,
                           const void* x, qff_dtype x_dtype, int cols, int batch) {
     if (!ctx || !parts || !x || nparts < 1 || nparts > QFF_Q4_MAX_PARTS) return QFF_ERR_INVALID_ARG;

@@ -148,6 +148,11 @@ struct Q4Norm {
 hipError_t launch_q4_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                            qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm, int cols,
                            int batch);
+hipError_t launch_q8_dequant(hipStream_t stream, const uint32_t* w, const void* scales, const void* biases,
+                             qff_dtype sb_dtype, float* out, int rows, int cols);
+hipError_t launch_router_top8(qff_ctx* ctx, hipStream_t stream, const uint32_t* w, const void* scales,
+                              const void* biases, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
+                              float* logits, int32_t* indices, float* scores, int experts, int cols, int batch);
 constexpr int kQ4GemmMinBatch = 33;   // batches at least this large take the tiled GEMM
 hipError_t launch_kv_append(hipStream_t stream, const float* k, const float* v, void* k_cache,
                             void* v_cache, qff_dtype cache_dtype, int pos, int max_seq);

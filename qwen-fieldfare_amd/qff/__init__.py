@@ -9,4 +9,5 @@ fallback path.
 """
 from ._lib import (BF16, F16, F32, LIB_PATH, QffError, lib)  # noqa: F401
 from .ops import (Context, deltanet_decode, deltanet_prefill, gqa_decode,  # noqa: F401
-                  gqa_prefill, q4_dequant, q4_matmul, q4_matmul_parts, q4_norm_matmul_parts)
+                  gqa_prefill, q4_dequant, q4_matmul, q4_matmul_parts, q4_norm_matmul_parts,
+                  q8_dequant, router_top8)

@@ -57,6 +57,8 @@ SIGNATURES = {
     "qff_q4_matmul": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i],
     "qff_q4_matmul_parts": [_vp, _vp, ctypes.POINTER(Q4Part), _i, _i, _vp, _i, _i, _i],
     "qff_q4_norm_matmul_parts": [_vp, _vp, ctypes.POINTER(Q4Part), _i, _i, _vp, _i, _vp, _i, _f, _i, _i],
+    "qff_q8_dequant": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i],
+    "qff_router_top8": [_vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _i],
     "qff_deltanet_decode": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp, _vp,
                             _vp, _vp, _i, _i],
     "qff_deltanet_prefill": [_vp, _vp, ctypes.POINTER(DeltaNetParams), _vp, _vp, _i, _vp, _vp,

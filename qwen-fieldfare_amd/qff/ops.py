@@ -137,6 +137,38 @@ def q4_norm_matmul_parts(ctx: Context, parts, x: torch.Tensor, norm_w: torch.Ten
     return res
 
 
+def q8_dequant(ctx: Context, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """w int32/uint32 [rows, cols/4]; scales/biases bf16/f16 [rows, cols/64] -> f32 [rows, cols]."""
+    rows, c4 = w.shape
+    if out is None:
+        out = torch.empty(rows, c4 * 4, dtype=torch.float32, device=w.device)
+    check("qff_q8_dequant", lib().qff_q8_dequant(ctx.handle, _stream(), _ptr(w), _ptr(scales),
+                                                 _ptr(biases), _code(scales), _ptr(out), rows, c4 * 4))
+    return out
+
+
+def router_top8(ctx: Context, w, scales, biases, x: torch.Tensor, logits=None, indices=None, scores=None):
+    """MoE router: Q8 logits of x [batch, cols] over the experts (rows of
+    w), then the top eight per token. Returns (indices int32 [batch, 8],
+    scores f32 [batch, 8], logits f32 [batch, experts])."""
+    experts, c4 = w.shape
+    cols = c4 * 4
+    x2 = x.reshape(-1, cols)
+    batch = x2.shape[0]
+    dev = x.device
+    if logits is None:
+        logits = torch.empty(batch, experts, dtype=torch.float32, device=dev)
+    if indices is None:
+        indices = torch.empty(batch, 8, dtype=torch.int32, device=dev)
+    if scores is None:
+        scores = torch.empty(batch, 8, dtype=torch.float32, device=dev)
+    check("qff_router_top8", lib().qff_router_top8(ctx.handle, _stream(), _ptr(w), _ptr(scales), _ptr(biases),
+                                                   _code(scales), _ptr(x2), _code(x2), _ptr(logits), _ptr(indices),
+                                                   _ptr(scores), experts, cols, batch))
+    return indices, scores, logits
+
+
 def _dn_params(p: dict, eps: float):
     for k in ("a_log", "dt_bias", "conv_w", "norm_w"):
         if p[k].dtype != torch.float32:

@@ -115,3 +115,16 @@ def q4_weight(rows: int, cols: int, seed: int, sb_dtype: str = "f16"):
     if sb_dtype == "f16":
         return w, s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
     return w, _bf16_bits(s), _bf16_bits(b)
+
+
+def q8_weight(rows: int, cols: int, seed: int, sb_dtype: str = "bf16"):
+    """MLX affine Q8, group 64: w uint32 [rows, cols/4] of random bytes,
+    scales ~U(0.001, 0.004) and biases ~N(0, 0.1), as bf16 (or f16) bits
+    [rows, cols/64]."""
+    rng = np.random.default_rng(seed)
+    w = rng.integers(0, 2 ** 32, (rows, cols // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.001, 0.004, (rows, cols // 64)).astype(np.float32)
+    b = _normal(rng, (rows, cols // 64), 0.1)
+    if sb_dtype == "f16":
+        return w, s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    return w, _bf16_bits(s), _bf16_bits(b)

@@ -21,7 +21,7 @@ def test_header_declares_the_expected_surface():
     fns = declared_functions()
     for name in ("qff_ctx_create", "qff_ctx_destroy", "qff_workspace_size", "qff_status_string",
                  "qff_version", "qff_q4_dequant", "qff_q4_matmul", "qff_q4_matmul_parts",
-                 "qff_q4_norm_matmul_parts", "qff_deltanet_decode",
+                 "qff_q4_norm_matmul_parts", "qff_q8_dequant", "qff_router_top8", "qff_deltanet_decode",
                  "qff_deltanet_prefill", "qff_gqa_decode", "qff_gqa_prefill", "qff_kv_append",
                  "qff_attention_gate"):
         assert name in fns
@@ -69,6 +69,8 @@ def test_workspace_size_and_argument_checks_without_gpu():
     parts = (Q4Part * 9)()
     assert L.qff_q4_matmul_parts(N, N, parts, 9, 2, N, 1, 64, 1) == -1   # null ctx and too many parts
     assert L.qff_q4_norm_matmul_parts(N, N, N, 1, 2, N, 1, N, 0, 1e-6, 64, 1) == -1
+    assert L.qff_q8_dequant(N, N, N, N, N, 1, N, 64, 64) == -1
+    assert L.qff_router_top8(N, N, N, N, N, 1, N, 0, N, N, N, 256, 2048, 1) == -1
 
 
 def test_product_has_no_cpu_fallback():
