@@ -182,6 +182,9 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         sreg[k] = elem<SB_DT>::load(scales, gi);
         breg[k] = elem<SB_DT>::load(biases, gi);
     }
+    // the weight and scale loads stay ahead of the x loads below, so the LDS
+    // staging of the weights waits for them alone
+    __builtin_amdgcn_sched_barrier(0);
     // this lane's x (16 values per group and token tile): bf16 activations
     // for all GPW groups of its wave up front; fp32 ones (converted to bf16
     // as they arrive) group by group in the product loop
@@ -224,6 +227,14 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         if (idx < RW * G) sb[idx] = make_float2(sreg[k], breg[k] - 128.0f * sreg[k]);
     }
     __syncthreads();
+    // the preloaded x enters the computation only from here: work on it
+    // placed above the barrier would make the barrier wait for the x loads
+    if (X_DT == 1) {
+#pragma unroll
+        for (int i = 0; i < kXPre; ++i)
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) asm volatile("" : "+v"(xv[i][bt][0]), "+v"(xv[i][bt][1]));
+    }
 
     f32x4_t acc[RT][NBT];
 #pragma unroll
