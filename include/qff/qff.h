@@ -150,7 +150,9 @@ int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* pa
  * the grouped product of qff_q4_matmul_parts on the normalised rows,
  *   xn[m, c] = x[m, c] * rsqrt(mean_c x[m, c]^2 + eps) * norm_w[c],
  *   y_p = xn W_p^T (+ residual_p),
- * in one pass over the weights (no normalised copy of x is written).
+ * without writing a normalised copy of x: in one pass over the weights up
+ * to 16 tokens (two for 17-32, one per 16-token half; many-token batches
+ * fold the norm into the group-sum pass their product already makes).
  * Replaces qwen_rmsnorm_f32 (deltanet.metal:18-53, weight used as is, mean
  * over the row) followed by the in-projections, as dispatched at
  * QwenQ4ActiveExpertStreamingRunner.swift:973-997 (DeltaNet layer) and

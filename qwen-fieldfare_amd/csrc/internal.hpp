@@ -42,8 +42,6 @@ struct qff_ctx {
     // (row G after the groups: the inverse RMS of a normed product).
     float* q4_xs = nullptr;
     int q4_xs_tokens = 0;
-    // Normed decode-batch Q4 products: bf16(x w_norm) [32][4096].
-    uint16_t* q4_xn = nullptr;
     // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
     // chunk intermediates.
     float* pf_o = nullptr;
@@ -72,7 +70,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, q4_xn, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

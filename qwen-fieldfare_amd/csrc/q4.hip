@@ -135,10 +135,9 @@ __host__ __device__ constexpr int q4_gemv_lds_bytes(int cols) {
                : q4_gemv_waves<GPW>(cols) * RT * NBT * 64 * 16;
 }
 
-template <int SB_DT, int X_DT, int NBT, int RT, bool RS, int GPW>
+template <int SB_DT, int X_DT, int NBT, int RT, bool NORM, int GPW>
 __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
-                                                                       int cols, int batch,
-                                                                       const float* __restrict__ rs) {
+                                                                       int cols, int batch, Q4Norm nrm) {
     constexpr int RW = 16 * RT;                     // rows per workgroup
     // per thread at most PPT weight pieces and SBT scale/bias entries:
     // RW * (cols / 32) / (64 nw) <= RW GPW / 32 with nw = ceil(G / GPW)
@@ -187,14 +186,75 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     __builtin_amdgcn_sched_barrier(0);
     // this lane's x (16 values per group and token tile): bf16 activations
     // for all GPW groups of its wave up front; fp32 ones (converted to bf16
-    // as they arrive) group by group in the product loop
+    // as they arrive) group by group in the product loop. With NORM the
+    // lane also sums the squares of its raw x over the row's groups and
+    // takes bf16(x w_norm); the waves together cover the row, so their sums
+    // meet in LDS and the row sums are scaled by each token's inverse RMS.
     const int g0 = wave * GPW, gn = min(GPW, G - g0);
+    float ssq[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) ssq[bt] = 0.0f;
+    // NORM: the norm weights go to LDS once per workgroup (fp32), staged
+    // with the weights
+    __shared__ __attribute__((aligned(16))) float wnl[NORM ? 64 * kQ4MaxGroups : 4];
+    if (NORM) {
+        for (int c8 = t; c8 < cols / 8; c8 += NT) {
+            float w8[8];
+            q4_norm_weights<8>(nrm, 8 * c8, w8);
+            *reinterpret_cast<float4*>(&wnl[8 * c8]) = make_float4(w8[0], w8[1], w8[2], w8[3]);
+            *reinterpret_cast<float4*>(&wnl[8 * c8 + 4]) = make_float4(w8[4], w8[5], w8[6], w8[7]);
+        }
+    }
     auto load_x = [&](int i, u32x4_t (&xo2)[NBT][2]) {
         const int g = min(g0 + i, G - 1);
+        float wn[16];
+        if (NORM) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 f = *reinterpret_cast<const float4*>(&wnl[64 * g + 16 * kb + 4 * q]);
+                wn[4 * q] = f.x;
+                wn[4 * q + 1] = f.y;
+                wn[4 * q + 2] = f.z;
+                wn[4 * q + 3] = f.w;
+            }
+        }
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
             const size_t xo = static_cast<size_t>(min(16 * bt + n, batch - 1)) * cols + 64 * g + 16 * kb;
-            if (X_DT == 1) {
+            if (NORM) {
+                float v[16];
+                if (X_DT == 1) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const u32x4_t u =
+                            *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * q);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            v[8 * q + 2 * e] = __uint_as_float(u[e] << 16);
+                            v[8 * q + 2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo)[q];
+                        v[4 * q] = f.x;
+                        v[4 * q + 1] = f.y;
+                        v[4 * q + 2] = f.z;
+                        v[4 * q + 3] = f.w;
+                    }
+                }
+                float s2 = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s2 = fmaf(v[e], v[e], s2);
+                ssq[bt] += i < gn ? s2 : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    xo2[bt][q] = u32x4_t{pack_bf16x2(v[8 * q] * wn[8 * q], v[8 * q + 1] * wn[8 * q + 1]),
+                                         pack_bf16x2(v[8 * q + 2] * wn[8 * q + 2], v[8 * q + 3] * wn[8 * q + 3]),
+                                         pack_bf16x2(v[8 * q + 4] * wn[8 * q + 4], v[8 * q + 5] * wn[8 * q + 5]),
+                                         pack_bf16x2(v[8 * q + 6] * wn[8 * q + 6], v[8 * q + 7] * wn[8 * q + 7])};
+            } else if (X_DT == 1) {
                 xo2[bt][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
                 xo2[bt][1] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8);
             } else {
@@ -207,9 +267,10 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
             }
         }
     };
-    constexpr int kXPre = X_DT == 1 ? GPW : 1;
+    constexpr bool kPre = X_DT == 1 && !NORM;   // all of the wave's x up front
+    constexpr int kXPre = kPre ? GPW : 1;
     u32x4_t xv[kXPre][NBT][2];
-    if (X_DT == 1) {
+    if (kPre) {
 #pragma unroll
         for (int i = 0; i < kXPre; ++i) load_x(i, xv[i]);
     }
@@ -229,7 +290,7 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     __syncthreads();
     // the preloaded x enters the computation only from here: work on it
     // placed above the barrier would make the barrier wait for the x loads
-    if (X_DT == 1) {
+    if (kPre) {
 #pragma unroll
         for (int i = 0; i < kXPre; ++i)
 #pragma unroll
@@ -250,8 +311,8 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         const float keep = i < gn ? 1.0f : 0.0f;
         float xsum[NBT];
         u32x4_t xi[NBT][2];
-        u32x4_t (&xg)[NBT][2] = xv[X_DT == 1 ? i : 0];
-        if (X_DT != 1) load_x(i, xg);
+        u32x4_t (&xg)[NBT][2] = xv[kPre ? i : 0];
+        if (!kPre) load_x(i, xg);
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
             const u32x4_t x0 = xg[bt][0], x1 = xg[bt][1];
@@ -289,6 +350,17 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
             }
         }
     }
+    // per-wave sums of squares of each token (the lanes of one n share a token)
+    __shared__ float q4ss[NORM ? kQ4GemvMaxWaves * 32 : 1];
+    if (NORM) {
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+            float v = ssq[bt];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (kb == 0) q4ss[wave * 32 + 16 * bt + n] = v;
+        }
+    }
     __syncthreads();   // the staged weights are consumed; their bytes take the partial sums
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -301,7 +373,11 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         for (int ww = 1; ww < nw; ++ww) v += part[(ww * RT * NBT + tile) * 64 + lane];
         const int m = 16 * bt + n;
         if (m < batch) {
-            if (RS) v *= rs[m];
+            if (NORM) {
+                float sq = 0.0f;
+                for (int ww = 0; ww < nw; ++ww) sq += q4ss[ww * 32 + m];
+                v *= rsqrtf(sq / static_cast<float>(cols) + nrm.eps);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = R0 + 16 * rt + 4 * kb + j;
@@ -508,13 +584,11 @@ constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
 
 // X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
 // lane l sums half-groups l, l + 64 (32 columns each), pairs of lanes combine.
-// With NORM the summed values are bf16(x w_norm), row G of xs takes the
-// token's inverse RMS, rsqrt(mean(x^2) + eps), from the same pass, and xn
-// (when not null, [batch, cols]) the bf16(x w_norm) values themselves.
+// With NORM the summed values are bf16(x w_norm) and row G of xs takes the
+// token's inverse RMS, rsqrt(mean(x^2) + eps), from the same pass.
 template <int X_DT, bool NORM>
 __global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x, float* __restrict__ xs, int cols,
-                                                      int batch, int xs_stride, Q4Norm nrm,
-                                                      uint16_t* __restrict__ xn) {
+                                                      int batch, int xs_stride, Q4Norm nrm) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = cols / 64;
     if (m >= batch) return;
@@ -560,13 +634,6 @@ __global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x
             }
 #pragma unroll
             for (int c = 0; c < 32; ++c) acc += v[c];
-            if (NORM && xn) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    *reinterpret_cast<u32x4_t*>(xn + o + 8 * i) =
-                        u32x4_t{pack_bf16x2(v[8 * i], v[8 * i + 1]), pack_bf16x2(v[8 * i + 2], v[8 * i + 3]),
-                                pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7])};
-            }
         }
         acc += __shfl_xor(acc, 1, 64);
         if ((lane & 1) == 0 && hg < 2 * G) xs[static_cast<size_t>(hg >> 1) * xs_stride + m] = acc;
@@ -839,10 +906,10 @@ static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
             ProfScope prof(ctx, stream, "q4_xsum");
             if (x_dtype == QFF_BF16)
                 q4_xsum_kernel<1, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
-                                                                        ctx->q4_xs_tokens, norm, nullptr);
+                                                                        ctx->q4_xs_tokens, norm);
             else
                 q4_xsum_kernel<0, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
-                                                                        ctx->q4_xs_tokens, norm, nullptr);
+                                                                        ctx->q4_xs_tokens, norm);
         }
         for (int i = 0; i < nparts; ++i) {
             const qff_q4_part& q = parts[i];
@@ -890,23 +957,19 @@ static hipError_t q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
 #undef QFF_Q4S
         return hipGetLastError();
     }
-    // 2..32 tokens with the norm: one pass writes bf16(x w_norm) and the
-    // inverse RMS of each token to workspace, the product reads those and
-    // scales its row sums
-    const float* rs = nullptr;
-    if (NORM) {
-        {
-            ProfScope prof(ctx, stream, "q4_xsum");
-            if (x_dtype == QFF_BF16)
-                q4_xsum_kernel<1, true><<<(batch + 3) / 4, 256, 0, stream>>>(x, ctx->q4_xs, cols, batch,
-                                                                           ctx->q4_xs_tokens, norm, ctx->q4_xn);
-            else
-                q4_xsum_kernel<0, true><<<(batch + 3) / 4, 256, 0, stream>>>(x, ctx->q4_xs, cols, batch,
-                                                                           ctx->q4_xs_tokens, norm, ctx->q4_xn);
+    if (NORM && batch > 16) {
+        // the normed product keeps one 16-token tile per launch (two tiles
+        // of normed x do not fit the registers): tokens 0-15, then the rest
+        qff_q4_part hi[QFF_Q4_MAX_PARTS];
+        for (int i = 0; i < nparts; ++i) {
+            const size_t off = static_cast<size_t>(16) * parts[i].rows * (parts[i].y_dtype == QFF_BF16 ? 2 : 4);
+            hi[i] = parts[i];
+            hi[i].y = static_cast<char*>(parts[i].y) + off;
+            if (parts[i].residual) hi[i].residual = static_cast<const char*>(parts[i].residual) + off;
         }
-        x = ctx->q4_xn;
-        x_dtype = QFF_BF16;
-        rs = ctx->q4_xs + static_cast<size_t>(cols / 64) * ctx->q4_xs_tokens;
+        QFF_CHECK_HIP_RET((q4_gemv_parts<true>(ctx, stream, parts, nparts, sb_dtype, x, x_dtype, norm, cols, 16)));
+        const void* xh = static_cast<const char*>(x) + static_cast<size_t>(16) * cols * (x_dtype == QFF_BF16 ? 2 : 4);
+        return q4_gemv_parts<true>(ctx, stream, hi, nparts, sb_dtype, xh, x_dtype, norm, cols, batch - 16);
     }
     // four row tiles per workgroup when x is read for several tokens over
     // enough rows to keep one workgroup per CU busy; one otherwise
@@ -922,24 +985,22 @@ static hipError_t q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
         const int bytes = q4_gemv_lds_bytes<RTT, NB, GP>(cols);                                            \
         QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemv_kernel<S, X, NB, RTT, NORM, GP>>(bytes)));                  \
         q4_gemv_kernel<S, X, NB, RTT, NORM, GP><<<blocks, 64 * q4_gemv_waves<GP>(cols), bytes, stream>>>(   \
-            P, x, cols, batch, rs);                                                                        \
+            P, x, cols, batch, norm);                                                                      \
     }
 #define QFF_Q4V(S, X, NB)                                        \
     if (rt4) {                                                   \
-        if (g4) QFF_Q4V1(S, X, NB, 4, 4) else QFF_Q4V1(S, X, NB, 4, 2) \
+        QFF_Q4V1(S, X, NB, 4, 2)                                 \
     } else {                                                     \
         if (g4) QFF_Q4V1(S, X, NB, 1, 4) else QFF_Q4V1(S, X, NB, 1, 2) \
     }
-#define QFF_Q4V_B(S, X) \
-    if (nbt == 1) { QFF_Q4V(S, X, 1); } else { QFF_Q4V(S, X, 2); }
-#define QFF_Q4V_X(S)                   \
-    if constexpr (NORM) {              \
-        QFF_Q4V_B(S, 1);               \
-    } else if (x_dtype == QFF_BF16) {  \
-        QFF_Q4V_B(S, 1);               \
-    } else {                           \
-        QFF_Q4V_B(S, 0);               \
+#define QFF_Q4V_B(S, X)                          \
+    if constexpr (NORM) {                        \
+        QFF_Q4V(S, X, 1);                        \
+    } else {                                     \
+        if (nbt == 1) { QFF_Q4V(S, X, 1); } else { QFF_Q4V(S, X, 2); } \
     }
+#define QFF_Q4V_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4V_B(S, 1); } else { QFF_Q4V_B(S, 0); }
     if (sb_dtype == QFF_BF16) { QFF_Q4V_X(1); } else { QFF_Q4V_X(2); }
 #undef QFF_Q4V_X
 #undef QFF_Q4V_B
