@@ -9,20 +9,21 @@
 //
 // Here the eight q heads that share a kv head run in the same wave, so every
 // K/V byte is read from HBM once, and both products run on the matrix cores:
-//   partial  grid (chunk group, kv head, sequence), four waves, one chunk
-//            each. The workgroup normalises and rotates the 8 q heads into
-//            LDS once (bf16, softmax scale and log2 e folded in); the wave
-//            whose chunk holds the new token also normalises/rotates k,
-//            appends k and v to the cache and keeps both in LDS for its own
-//            use. Each wave then walks 16-position tiles with the next tile's
-//            K and V rows already in flight (two register stages): S^T = K Q^T
-//            with 8 MFMA 16x16x32 (K rows straight from HBM, 16 B per lane),
-//            base-2 online softmax per head whose running max is raised only
-//            past 2^8 (so O is rarely rescaled), the V tile copied row-major
-//            into LDS and read back as MFMA B operands with the gfx950
-//            transpose read (ds_read_b64_tr_b16), O += P V with 16 MFMA
-//            16x16x16, and one (m, d, o[8][256]) partial per chunk (m in
-//            base-2 units).
+//   partial  one wave per (sequence, kv head, chunk) unit: a static grid of
+//            single-wave workgroups for short chunks, a persistent grid that
+//            hands units out through an atomic queue for long ones. The wave
+//            normalises and rotates the 8 q heads into LDS (bf16, softmax
+//            scale and log2 e folded in); the one whose chunk holds the new
+//            token also normalises/rotates k, appends k and v to the cache
+//            and keeps both in LDS for its own use. It then walks 16-position
+//            tiles (long chunks: the next tile's K and V rows already in
+//            flight, two register stages): S^T = K Q^T with 8 MFMA 16x16x32
+//            (K rows straight from HBM, 16 B per lane), base-2 online softmax
+//            per head whose running max is raised only past 2^8 (so O is
+//            rarely rescaled), the V tile copied row-major into LDS and read
+//            back as MFMA B operands with the gfx950 transpose read
+//            (ds_read_b64_tr_b16), O += P V with 16 MFMA 16x16x16, and one
+//            (m, d, o[8][256]) partial per chunk (m in base-2 units).
 //   combine  grid (q head, sequence): merges the chunk partials and applies
 //            out = attn * sigmoid(gate).
 // Lengths come from the device `positions` array, so no host sync is needed;
@@ -41,82 +42,128 @@ struct DecTile {
     u32x4_t k[8], v[8];
 };
 
-// grid (2 kv heads x ceil(chunks / NW), 1, batch), 64 NW threads: the kv
-// head is the fastest-varying block index, so the two heads' workgroups of a
-// chunk group are dispatched together and stream the interleaved halves of
-// the same cache records at the same time; wave w takes chunk NW * group + w. NW = 4 (long chunks) shares one q preparation
-// between four chunks and keeps the next tile's loads in flight (two register
-// stages, two waves per SIMD); NW = 1 (short chunks, small batches) loads
-// each tile as it goes and keeps three or more single-wave workgroups per
-// SIMD resident instead.
-template <int IN_DT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 2 : 3)))
-void gqa_decode_partial_kernel(
-    const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
-    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
-    float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
-    float* __restrict__ pd, float* __restrict__ po) {
-    const int kvh = blockIdx.x & 1, grp = blockIdx.x >> 1, seq = blockIdx.z;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int c = NW * grp + wave;
-    const int pos = positions[seq];
-    // a position outside the cache is the caller's error: skip the sequence
-    // (the combine writes NaN for it) rather than touch memory past the cache
-    if (pos < 0 || pos >= max_ctx) return;
-    const int L = pos + 1;
-    if (NW * grp * chunk_len >= L) return;   // the whole group is past the end
+// Wave-local LDS of one partial unit.
+struct DecLds {
+    uint16_t qs[8][256];                      // normed, rotated, scaled q (bf16)
+    uint16_t vs[kDecTile * kVRowStride];      // the current V tile, row-major
+    uint16_t knew[256], vnew[256];            // the new token's k, v
+    float2 rcs[32];                           // (cos, sin) of pos * f[i]
+};
+
+// Orders one wave's LDS stores before its later LDS loads by other lanes:
+// a wave's LDS accesses complete in issue order, so only the compiler has to
+// be kept from moving them (no s_barrier: waves of one workgroup run
+// different units).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// One partial unit: chunk c (positions c * chunk_len ..) of sequence seq and
+// kv head kvh, run by one wave on its own LDS. The wave normalises and
+// rotates the 8 q heads; if the chunk holds the new token it also
+// normalises / rotates k, appends k and v to the cache and keeps both in
+// LDS for its own use. It then walks 16-position tiles: S^T = K Q^T with 8
+// MFMA 16x16x32 (K rows straight from HBM, 16 B per lane), base-2 online
+// softmax per head whose running max is raised only past 2^8 (so O is
+// rarely rescaled), the V tile copied row-major into LDS and read back as
+// MFMA B operands with the gfx950 transpose read (ds_read_b64_tr_b16),
+// O += P V with 16 MFMA 16x16x16, and writes one (m, d, o[8][256]) partial
+// (m in base-2 units). PIPE keeps the next tile's loads in flight (two
+// register stages, for long chunks).
+template <int IN_DT, bool PIPE>
+__device__ __forceinline__ void gqa_partial_unit(
+    DecLds& L, int seq, int kvh, int c, int pos, int lane, const void* __restrict__ q_gate,
+    const void* __restrict__ k_new, const void* __restrict__ v_new, const float* __restrict__ q_norm_w,
+    const float* __restrict__ k_norm_w, const float* freqs, float scale, float eps,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int max_ctx, int chunk_len, int cstride,
+    float* __restrict__ pm, float* __restrict__ pd, float* __restrict__ po) {
     const int p_start = c * chunk_len;
-    const int p_end = min(L, p_start + chunk_len);
+    const int p_end = min(pos + 1, p_start + chunk_len);
+    const bool has_new = pos >= p_start && pos < p_end;   // then p_end - 1 == pos
+    const size_t seq_base = static_cast<size_t>(seq) * max_ctx * 512 + kvh * 256;
+    const int n = lane & 15, kb = lane >> 4;
+    const uint16_t* Kb = k_cache + seq_base;
+    const uint16_t* Vb = v_cache + seq_base;
 
-    __shared__ __attribute__((aligned(16))) uint16_t qs[8][256];                           // 4 KB
-    __shared__ __attribute__((aligned(16))) uint16_t vs[NW][kDecTile * kVRowStride];  // NW x 8.25 KB
-    __shared__ __attribute__((aligned(16))) uint16_t knew[256], vnew[256];
-    __shared__ float2 rcs[32];   // (cos, sin) of pos * f[i]
-
-    if (t < 32) {
-        const float ang = static_cast<float>(pos) * rf.f[t];
-        rcs[t] = make_float2(cosf(ang), sinf(ang));
-    }
-    __syncthreads();
-
-    // ---- q: head RMSNorm + partial RoPE + scale, bf16 into LDS ---------------
-    // (deltanet.metal:599-651; RoPE angles as QwenQ4ActiveExpertStreamingRunner
-    // .swift:1090-1099 with host-computed inverse frequencies). Thread -> head
-    // u/32, dims 8*(u%32) .. +7 for u = t, t + 64 NW, ...; the RoPE pair
-    // (d, d^32) of dims < 64 sits in threads 4 apart.
-    for (int u = t; u < 256; u += 64 * NW) {
-        const int hl = u >> 5, j = u & 31;
-        const size_t qbase = (static_cast<size_t>(seq) * 16 + kvh * 8 + hl) * 512 + 8 * j;
-        float x[8], ss = 0.0f;
+    // K rows p0 + n (A of 16x16x32) and V rows p0 + 2i + lane/32 (dims
+    // 8*(lane%32) .. +7). Rows past the chunk end re-read its last row: their
+    // scores are masked to -inf, so they enter P V with probability 0 times
+    // finite data (the cache past the sequence may hold any bit pattern, NaN
+    // included, and is never read). Every row that lands on the new token's
+    // position takes the LDS copy instead, so tiles may be loaded before the
+    // append. The loads are unconditional so the compiler's vmcnt bookkeeping
+    // stays exact across the two stages.
+    // (the row addresses are rebuilt from an opaque copy of the lane index
+    // each tile: kept live across the tile loop they would spill)
+    auto load = [&](DecTile& tl, int p0) {
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        const uint16_t* krow = Kb + static_cast<size_t>(min(p0 + (l & 15), p_end - 1)) * 512;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) tl.k[jj] = *reinterpret_cast<const u32x4_t*>(krow + 32 * jj + 8 * (l >> 4));
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            x[i] = elem<IN_DT>::load(q_gate, qbase + i);
-            ss += x[i] * x[i];
+            const int vp = min(p0 + 2 * i + (l >> 5), p_end - 1);
+            tl.v[i] = *reinterpret_cast<const u32x4_t*>(Vb + static_cast<size_t>(vp) * 512 + 8 * (l & 31));
         }
+    };
+    // ---- q: head RMSNorm + partial RoPE + scale, bf16 into LDS ---------------
+    // (deltanet.metal:599-651; RoPE angles as QwenQ4ActiveExpertStreamingRunner
+    // .swift:1090-1099 with host-computed inverse frequencies). Lane -> head
+    // u/32, dims 8*(u%32) .. +7 for u = lane + 64 it; the RoPE pair (d, d^32)
+    // of dims < 64 sits in lanes 4 apart. The q rows and norm weights are
+    // requested first and, for long chunks, the first tile's K/V rows right
+    // behind them, so the q work waits for its own loads only.
+    float xq[4][8], qw[8];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int u = 64 * it + lane;
+        const size_t qbase = (static_cast<size_t>(seq) * 16 + kvh * 8 + (u >> 5)) * 512 + 8 * (u & 31);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xq[it][i] = elem<IN_DT>::load(q_gate, qbase + i);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qw[i] = q_norm_w[8 * (lane & 31) + i];
+    __builtin_amdgcn_sched_barrier(0);
+    DecTile ta, tb;
+    if (PIPE) load(ta, p_start);
+    __builtin_amdgcn_sched_barrier(0);
+    if (lane < 32) {
+        const float ang = static_cast<float>(pos) * freqs[lane];
+        L.rcs[lane] = make_float2(cosf(ang), sinf(ang));
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int u = 64 * it + lane;
+        const int hl = u >> 5, j = u & 31;
+        float* x = xq[it];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
         ss = group_sum<32>(ss);
         const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = x[i] * inv * q_norm_w[8 * j + i];
+        for (int i = 0; i < 8; ++i) x[i] = x[i] * inv * qw[i];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int d = 8 * j + i;
             const float partner = __shfl_xor(x[i], 4, 64);   // d +- 32 (used when d < 64)
             if (d < 64) {
-                const float2 r = rcs[d & 31];
+                const float2 r = L.rcs[d & 31];
                 x[i] = (d < 32) ? x[i] * r.x + (-partner) * r.y : x[i] * r.x + partner * r.y;
             }
         }
         const float qscale = scale * 1.44269504088896341f;
 #pragma unroll
         for (int i = 0; i < 8; i += 2)
-            *reinterpret_cast<uint32_t*>(&qs[hl][8 * j + i]) = pack_bf16x2(x[i] * qscale, x[i + 1] * qscale);
+            *reinterpret_cast<uint32_t*>(&L.qs[hl][8 * j + i]) = pack_bf16x2(x[i] * qscale, x[i + 1] * qscale);
     }
-    // ---- the new token (only the wave whose chunk holds it): k norm + RoPE,
+    // ---- the new token (only the unit whose chunk holds it): k norm + RoPE,
     // append k and v to the cache (deltanet.metal:670-689), keep both in LDS
     // so the wave never reads back its own global stores.
-    const bool has_new = pos >= p_start && pos < p_end;
-    const size_t seq_base = static_cast<size_t>(seq) * max_ctx * 512 + kvh * 256;
     if (has_new) {
         const size_t kb0 = (static_cast<size_t>(seq) * 2 + kvh) * 256 + 4 * lane;
         float kx[4], vx[4], ss = 0.0f;
@@ -136,55 +183,41 @@ void gqa_decode_partial_kernel(
             const float up = __shfl_down(kx[i], 8, 64), dn = __shfl_up(kx[i], 8, 64);
             const int d = 4 * lane + i;
             if (d < 64) {
-                const float2 r = rcs[d & 31];
+                const float2 r = L.rcs[d & 31];
                 kx[i] = (d < 32) ? kx[i] * r.x + (-up) * r.y : kx[i] * r.x + dn * r.y;
             }
         }
         const uint32_t k01 = pack_bf16x2(kx[0], kx[1]), k23 = pack_bf16x2(kx[2], kx[3]);
         const uint32_t v01 = pack_bf16x2(vx[0], vx[1]), v23 = pack_bf16x2(vx[2], vx[3]);
-        *reinterpret_cast<u32x2_t*>(&knew[4 * lane]) = u32x2_t{k01, k23};
-        *reinterpret_cast<u32x2_t*>(&vnew[4 * lane]) = u32x2_t{v01, v23};
+        *reinterpret_cast<u32x2_t*>(&L.knew[4 * lane]) = u32x2_t{k01, k23};
+        *reinterpret_cast<u32x2_t*>(&L.vnew[4 * lane]) = u32x2_t{v01, v23};
         const size_t off = seq_base + static_cast<size_t>(pos) * 512 + 4 * lane;
         *reinterpret_cast<u32x2_t*>(k_cache + off) = u32x2_t{k01, k23};
         *reinterpret_cast<u32x2_t*>(v_cache + off) = u32x2_t{v01, v23};
     }
-    __syncthreads();
-    if (p_start >= L) return;
+    wave_lds_sync();
 
-    const int n = lane & 15, kb = lane >> 4;
     // q^T (B of 16x16x32): col = head n (< 8 real), k = dims 32jj + 8kb .. +7,
     // read from LDS per tile (registers are kept for the two tile stages)
-    const uint16_t* qrow = &qs[n & 7][8 * kb];
-    uint16_t* vsw = vs[wave];
+    const uint16_t* qrow = &L.qs[n & 7][8 * kb];
+    uint16_t* vsw = L.vs;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
 
     float m_run = -INFINITY, d_run = 0.0f;
     f32x4_t oacc[16];
 #pragma unroll
     for (int jd = 0; jd < 16; ++jd) oacc[jd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* Kb = k_cache + seq_base;
-    const uint16_t* Vb = v_cache + seq_base;
 
-    // K rows p0 + n (A of 16x16x32) and V rows p0 + 2i + lane/32 (dims
-    // 8*(lane%32) .. +7). Rows past the chunk end re-read its last row: their
-    // scores are masked to -inf, so they enter P V with probability 0 times
-    // finite data (the cache past the sequence may hold any bit pattern, NaN
-    // included, and is never read). The loads are unconditional so the
-    // compiler's vmcnt bookkeeping stays exact across the two stages.
-    auto load = [&](DecTile& tl, int p0) {
-        const uint16_t* krow = Kb + static_cast<size_t>(min(p0 + n, p_end - 1)) * 512;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) tl.k[jj] = *reinterpret_cast<const u32x4_t*>(krow + 32 * jj + 8 * kb);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int vp = min(p0 + 2 * i + (lane >> 5), p_end - 1);
-            tl.v[i] = *reinterpret_cast<const u32x4_t*>(Vb + static_cast<size_t>(vp) * 512 + 8 * (lane & 31));
-        }
-    };
     auto compute = [&](DecTile& tl, int p0) {
-        if (has_new && min(p0 + n, p_end - 1) == pos) {
+        // (the opaque copy keeps the compiler from folding the LDS read into
+        // the tile load as one flat load through a selected pointer)
+        if (has_new && p0 + n >= pos) {
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) tl.k[jj] = *reinterpret_cast<const u32x4_t*>(&knew[32 * jj + 8 * kb]);
+            for (int jj = 0; jj < 8; ++jj) {
+                u32x4_t kv = *reinterpret_cast<const u32x4_t*>(&L.knew[32 * jj + 8 * kb]);
+                asm volatile("" : "+v"(kv));
+                tl.k[jj] = kv;
+            }
         }
         // S^T = K Q^T
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -198,7 +231,10 @@ void gqa_decode_partial_kernel(
         for (int i = 0; i < 8; ++i) {
             const int r = 2 * i + (lane >> 5);
             u32x4_t v = tl.v[i];
-            if (has_new && p0 + r == pos) v = *reinterpret_cast<const u32x4_t*>(&vnew[8 * (lane & 31)]);
+            if (has_new && p0 + r >= pos) {   // rows clamped to the new token's position
+                v = *reinterpret_cast<const u32x4_t*>(&L.vnew[8 * (lane & 31)]);
+                asm volatile("" : "+v"(v));
+            }
             *reinterpret_cast<u32x4_t*>(&vsw[r * kVRowStride + 8 * (lane & 31)]) = v;
         }
         // online softmax (base 2); lane holds head n, positions p0 + 4kb + i
@@ -234,15 +270,13 @@ void gqa_decode_partial_kernel(
         // B = V^T block straight from the row-major tile with a transpose read:
         // source lane (group kb, s = n) points at row 4kb + n/4, dims
         // 16jd + 4(n%4) .. +3, and receives V[4kb + k][16jd + n], k = 0..3.
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_sync();
         const uint16_t* vsrc = &vsw[(4 * kb + (n >> 2)) * kVRowStride + 4 * (n & 3)];
 #pragma unroll
         for (int jd = 0; jd < 16; ++jd) oacc[jd] = mfma_16x16x16_bf16(pa, lds_read_tr16(vsrc + 16 * jd), oacc[jd]);
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_sync();
     };
-    if (NW == 4) {
-        DecTile ta, tb;
-        load(ta, p_start);
+    if (PIPE) {
         int p0 = p_start;
         for (; p0 + kDecTile < p_end; p0 += 2 * kDecTile) {
             load(tb, p0 + kDecTile);
@@ -253,7 +287,6 @@ void gqa_decode_partial_kernel(
         if (p0 < p_end) compute(ta, p0);
     } else {
         for (int p0 = p_start; p0 < p_end; p0 += kDecTile) {
-            DecTile ta;
             load(ta, p0);
             compute(ta, p0);
         }
@@ -273,6 +306,63 @@ void gqa_decode_partial_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) orow[(4 * kb + i) * 256 + 16 * jd + n] = oacc[jd][i];
     }
+}
+
+// Static grid for short chunks: grid (2 kv heads x chunks, 1, batch), one
+// wave each; the kv head is the fastest-varying block index, so the two
+// heads' workgroups of a chunk are dispatched together and stream the
+// interleaved halves of the same cache records at the same time. Three or
+// more single-wave workgroups per SIMD stay resident. Lengths come from the
+// device `positions` array; waves past a sequence's last chunk exit at once.
+template <int IN_DT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+void gqa_decode_partial_kernel(
+    const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
+    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
+    float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
+    float* __restrict__ pd, float* __restrict__ po) {
+    const int kvh = blockIdx.x & 1, c = blockIdx.x >> 1, seq = blockIdx.z;
+    const int pos = positions[seq];
+    // a position outside the cache is the caller's error: skip the sequence
+    // (the combine writes NaN for it) rather than touch memory past the cache
+    if (pos < 0 || pos >= max_ctx || c * chunk_len > pos) return;
+    __shared__ __attribute__((aligned(16))) DecLds lds;
+    __shared__ float freqs[32];
+    const int lane = threadIdx.x & 63;
+    if (lane < 32) freqs[lane] = rf.f[lane];
+    wave_lds_sync();
+    gqa_partial_unit<IN_DT, false>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
+                                   scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
+}
+
+// Long chunks: grid (2 kv heads x ceil(chunks / 4), 1, batch), four waves
+// per workgroup, wave w taking chunk 4 * group + w of the workgroup's kv
+// head (kv head fastest, so the two heads' workgroups of a chunk group are
+// dispatched together and stream the interleaved halves of the same cache
+// records), each keeping the next tile's loads in flight (two register
+// stages, two waves per SIMD).
+template <int IN_DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void gqa_decode_group_kernel(
+    const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
+    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
+    float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
+    float* __restrict__ pd, float* __restrict__ po) {
+    __shared__ __attribute__((aligned(16))) DecLds lds[4];
+    __shared__ float freqs[32];   // RoPE inverse frequencies
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kvh = blockIdx.x & 1, c = 4 * (blockIdx.x >> 1) + wave, seq = blockIdx.z;
+    const int pos = positions[seq];
+    if (threadIdx.x < 32) freqs[threadIdx.x] = rf.f[threadIdx.x];
+    __syncthreads();
+    // a position outside the cache is the caller's error: skip the sequence
+    // (the combine writes NaN for it) rather than touch memory past the cache
+    if (pos < 0 || pos >= max_ctx || c * chunk_len > pos) return;
+    gqa_partial_unit<IN_DT, true>(lds[wave], seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w,
+                                  freqs, scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
 // grid (16 q heads, batch), 512 threads: attention.metal:342-377 merge, then
@@ -376,17 +466,21 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     {
         ProfScope prof(ctx, stream, "gqa_decode_partial");
-        const bool grouped = ch >= 256;
-#define QFF_PART(I, W)                                                                                     \
-    gqa_decode_partial_kernel<I, W><<<dim3(2 * ((nc + W - 1) / W), 1, batch), 64 * W, 0, stream>>>(              \
+        if (ch >= 256) {
+#define QFF_PART(I)                                                                                             \
+    gqa_decode_group_kernel<I><<<dim3(2 * ((nc + 3) / 4), 1, batch), 256, 0, stream>>>(                         \
         q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
         ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
-        if (in_dtype == QFF_BF16) {
-            if (grouped) QFF_PART(1, 4); else QFF_PART(1, 1);
-        } else {
-            if (grouped) QFF_PART(0, 4); else QFF_PART(0, 1);
-        }
+            if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
 #undef QFF_PART
+        } else {
+#define QFF_PART(I)                                                                                            \
+    gqa_decode_partial_kernel<I><<<dim3(2 * nc, 1, batch), 64, 0, stream>>>(                                   \
+        q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
+        ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
+            if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
+#undef QFF_PART
+        }
     }
     const dim3 cgrid(16, batch);
     ProfScope prof(ctx, stream, "gqa_decode_combine");
