@@ -89,6 +89,28 @@ def timed(fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
+def timed_graph(fn, unroll, steps, warmup):
+    """Per-step time of `unroll` consecutive steps (fn(0) .. fn(unroll - 1),
+    each on its own rotating input set) captured in one HIP graph and
+    replayed: the GPU time of back-to-back steps, as a serving loop that
+    replays graphs sees it, without Python's per-call launch cost."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(unroll):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(unroll):
+            fn(i)
+    reps = max(3, steps // unroll)
+    ms = timed(lambda i: graph.replay(), reps, max(1, warmup // unroll), torch.cuda.current_stream())
+    return ms / unroll
+
+
 def kernel_times(ctx, fn, steps):
     """Per-kernel average durations (ms) over `steps` calls, from the
     library's own hipEvent brackets on the launch stream."""
@@ -158,10 +180,12 @@ def bench_c0(ctx, steps, warmup, sets=128):
         qff.deltanet_decode(ctx, p, qkv[j], z[j], a[j], b[j], conv[j], ssm[j], out=out[j])
 
     stream = torch.cuda.current_stream()
-    ms = timed(step, steps, warmup, stream)
+    ms_eager = timed(step, steps, warmup, stream)
+    ms = timed_graph(step, sets, steps, warmup)
     kt, _ = kernel_times(ctx, step, min(steps, 256))
     k = kt["deltanet_decode"]
-    return {"ms_per_step": ms, "tokens_per_s": 1.0 / (ms * 1e-3),
+    return {"ms_per_step": ms, "ms_per_step_eager": ms_eager, "tokens_per_s": 1.0 / (ms * 1e-3),
+            "step_GBps": C0_BYTES / (ms * 1e-3) / 1e9,
             "kernel_us": k * 1e3, "kernel_GBps": C0_BYTES / (k * 1e-3) / 1e9,
             "hbm_frac": C0_BYTES / (k * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
@@ -186,10 +210,12 @@ def bench_dn_decode_batch(ctx, B, steps, warmup):
         j = i % sets
         qff.deltanet_decode(ctx, p, qkv[j], z[j], a[j], b[j], conv[j], ssm[j], out=out[j])
 
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms_eager = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms = timed_graph(step, sets, steps, warmup)
     kt, _ = kernel_times(ctx, step, min(steps, 64))
     k = kt["deltanet_decode"]
-    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "kernel_us": k * 1e3,
+    return {"ms_per_step": ms, "ms_per_step_eager": ms_eager, "tokens_per_s": B / (ms * 1e-3),
+            "step_GBps": B * C0_BYTES / (ms * 1e-3) / 1e9, "kernel_us": k * 1e3,
             "kernel_GBps": B * C0_BYTES / (k * 1e-3) / 1e9,
             "hbm_frac": B * C0_BYTES / (k * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
@@ -217,12 +243,14 @@ def bench_c2(ctx, B, steps, warmup, max_ctx=8192):
         j = i % pools
         qff.gqa_decode(ctx, p, qg, kn, vn, kc[j], vc[j], pos, out=out)
 
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms_eager = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms = timed_graph(step, pools, steps, warmup)
     kt, _ = kernel_times(ctx, step, min(steps, 64))
     nbytes = int(np.sum(2048 * lengths.astype(np.int64) + 29_696))
     flops = int(np.sum(16_384 * lengths.astype(np.int64)))
     part = kt["gqa_decode_partial"] + kt.get("gqa_decode_combine", 0.0)
-    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "mean_len": float(lengths.mean()),
+    return {"ms_per_step": ms, "ms_per_step_eager": ms_eager, "tokens_per_s": B / (ms * 1e-3),
+            "mean_len": float(lengths.mean()),
             "kernels_us": {k: v * 1e3 for k, v in kt.items()},
             "GBps": nbytes / (part * 1e-3) / 1e9, "hbm_frac": nbytes / (part * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "TFLOPs": flops / (part * 1e-3) / 1e12}
@@ -384,11 +412,13 @@ def bench_router(ctx, B, steps, warmup, sets=64):
         w, sc, bi, _ = ws[i % sets]
         qff.router_top8(ctx, w, sc, bi, x, logits=lg, indices=idx, scores=scr)
 
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms_eager = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms = timed_graph(step, sets, steps, warmup)
     kt, _ = kernel_times(ctx, step, min(steps, 64))
     nbytes = 256 * 2048 + 2 * 256 * 32 * 2 + B * 2048 * 4
     k = kt["router_logits"] + kt["router_top8"]
-    return {"ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "kernels_us": {k_: v * 1e3 for k_, v in kt.items()},
+    return {"ms_per_step": ms, "ms_per_step_eager": ms_eager, "tokens_per_s": B / (ms * 1e-3),
+            "kernels_us": {k_: v * 1e3 for k_, v in kt.items()},
             "GBps": nbytes / (k * 1e-3) / 1e9}
 
 
