@@ -5,9 +5,9 @@
 // path at its position (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561,
 // 1076-1150), so token t attends to positions 0 .. start+t. This file
 // computes all T rows at once:
-//   prep   grid (token, 18 heads): head RMSNorm + partial RoPE of the 16 q
-//          heads (bf16, softmax scale folded in, to workspace) and of the 2 k
-//          heads (appended to the bf16 cache together with v).
+//   prep   one wave per token: head RMSNorm + partial RoPE of the
+//          16 q heads (bf16, softmax scale folded in, to workspace) and of
+//          the 2 k heads (appended to the bf16 cache together with v).
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; eight waves of 16 rows = 2 tokens x 8
 //          heads, so accumulators and q stay in VGPRs and two waves share
@@ -34,39 +34,94 @@ constexpr int kPfQB = 16;       // query tokens per workgroup
 constexpr int kPfKT = 64;       // K/V positions per tile
 constexpr int kKStride = 264;   // bf16 per K row in LDS: 256 + 8 pad (528 B)
 
-// grid (T, 18): y < 16 -> q head y, else kv head y - 16. 256 threads (dims).
+// One wave per token, 8 per workgroup: the token's 32 RoPE angles are
+// evaluated once (lane i < 32: cos, sin of pos * f[i]) and shuffled to the
+// lanes that rotate, then the 18 head slots (0-15 the q heads, 16-17 the kv
+// heads) go in three rounds of six with each round's loads issued together.
+// Lane l holds dims 4l .. 4l+3: the RMS is one wave reduction, and the RoPE
+// partner of dim d < 32 (d + 32) sits 8 lanes up.
+constexpr int kPrepWaves = 8;
+constexpr int kPrepRound = 6;
+
 template <int IN_DT>
-__global__ __launch_bounds__(256) void gqa_prefill_prep_kernel(
+__global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
-    float eps, int start, uint16_t* __restrict__ qb, uint16_t* __restrict__ k_cache,
+    float eps, int start, int T, uint16_t* __restrict__ qb, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache) {
-    __shared__ float xs[256], red[4];
-    const int tok = blockIdx.x, hs = blockIdx.y, t = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int tok = blockIdx.x * kPrepWaves + (threadIdx.x >> 6);
+    if (tok >= T) return;
     const int pos = start + tok;
-    const bool is_q = hs < 16;
-    const float x = is_q ? elem<IN_DT>::load(q_gate, (static_cast<size_t>(tok) * 16 + hs) * 512 + t)
-                         : elem<IN_DT>::load(k, (static_cast<size_t>(tok) * 2 + (hs - 16)) * 256 + t);
-    const float ss = group_sum<64>(x * x);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / 256.0f + eps);
-    xs[t] = x * inv * (is_q ? q_norm_w[t] : k_norm_w[t]);
-    __syncthreads();
-    float r = xs[t];
-    if (t < 64) {
-        const int i = t & 31;
-        const float ang = static_cast<float>(pos) * rf.f[i];
-        const float c = cosf(ang), s = sinf(ang);
-        r = (t < 32) ? r * c + (-xs[t + 32]) * s : r * c + xs[t - 32] * s;
+    float cs, sn;
+    {
+        const float ang = static_cast<float>(pos) * rf.f[lane & 31];
+        cs = cosf(ang);
+        sn = sinf(ang);
     }
-    if (is_q) {
-        qb[(static_cast<size_t>(tok) * 16 + hs) * 256 + t] = f32_to_bf16(r * (scale * 1.44269504088896341f));
-    } else {
-        const int kvh = hs - 16;
-        const size_t off = (static_cast<size_t>(pos) * 2 + kvh) * 256 + t;
-        k_cache[off] = f32_to_bf16(r);
-        v_cache[off] = f32_to_bf16(elem<IN_DT>::load(v, (static_cast<size_t>(tok) * 2 + kvh) * 256 + t));
+    // (cos, sin) of this lane's four dims (d & 31 = (4 lane + i) & 31)
+    float ci[4], si[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ci[i] = __shfl(cs, (4 * lane + i) & 31, 64);
+        si[i] = __shfl(sn, (4 * lane + i) & 31, 64);
+    }
+    float qw[4], kw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qw[i] = q_norm_w[4 * lane + i];
+        kw[i] = k_norm_w[4 * lane + i];
+    }
+    const float qs = scale * 1.44269504088896341f;
+#pragma unroll
+    for (int r0 = 0; r0 < 18; r0 += kPrepRound) {
+        float x[kPrepRound][4];
+#pragma unroll
+        for (int j = 0; j < kPrepRound; ++j) {
+            const int hs = r0 + j;
+            const size_t src = hs < 16 ? (static_cast<size_t>(tok) * 16 + hs) * 512 + 4 * lane
+                                       : (static_cast<size_t>(tok) * 2 + (hs - 16)) * 256 + 4 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[j][i] = elem<IN_DT>::load(hs < 16 ? q_gate : k, src + i);
+        }
+        float vv[2][4];
+        if (r0 + kPrepRound > 16) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    vv[j][i] = elem<IN_DT>::load(v, (static_cast<size_t>(tok) * 2 + j) * 256 + 4 * lane + i);
+        }
+#pragma unroll
+        for (int j = 0; j < kPrepRound; ++j) {
+            const int hs = r0 + j;
+            const bool is_q = hs < 16;
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss += x[j][i] * x[j][i];
+            ss = group_sum<64>(ss);
+            const float inv = 1.0f / sqrtf(ss / 256.0f + eps);
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[i] = x[j][i] * inv * (is_q ? qw[i] : kw[i]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float up = __shfl_down(y[i], 8, 64), dn = __shfl_up(y[i], 8, 64);
+                const int d = 4 * lane + i;
+                if (d < 64) y[i] = (d < 32) ? y[i] * ci[i] + (-up) * si[i] : y[i] * ci[i] + dn * si[i];
+            }
+            if (is_q) {
+                *reinterpret_cast<u32x2_t*>(qb + (static_cast<size_t>(tok) * 16 + hs) * 256 + 4 * lane) =
+                    u32x2_t{pack_bf16x2(y[0] * qs, y[1] * qs), pack_bf16x2(y[2] * qs, y[3] * qs)};
+            } else {
+                const int kvh = hs - 16;
+                const size_t off = (static_cast<size_t>(pos) * 2 + kvh) * 256 + 4 * lane;
+                *reinterpret_cast<u32x2_t*>(k_cache + off) =
+                    u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                *reinterpret_cast<u32x2_t*>(v_cache + off) =
+                    u32x2_t{pack_bf16x2(vv[kvh][0], vv[kvh][1]), pack_bf16x2(vv[kvh][2], vv[kvh][3])};
+            }
+        }
     }
 }
 
@@ -271,12 +326,13 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     {
         ProfScope prof(ctx, stream, "gqa_prefill_prep");
+        const int pgrid = (T + kPrepWaves - 1) / kPrepWaves;
         if (in_dtype == QFF_BF16)
-            gqa_prefill_prep_kernel<1><<<dim3(T, 18), 256, 0, stream>>>(q_gate, k, v, p->q_norm_w, p->k_norm_w, rf,
-                                                                        p->scale, p->eps, start_pos, qb, kc, vc);
+            gqa_prefill_prep_kernel<1><<<pgrid, 64 * kPrepWaves, 0, stream>>>(
+                q_gate, k, v, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, start_pos, T, qb, kc, vc);
         else
-            gqa_prefill_prep_kernel<0><<<dim3(T, 18), 256, 0, stream>>>(q_gate, k, v, p->q_norm_w, p->k_norm_w, rf,
-                                                                        p->scale, p->eps, start_pos, qb, kc, vc);
+            gqa_prefill_prep_kernel<0><<<pgrid, 64 * kPrepWaves, 0, stream>>>(
+                q_gate, k, v, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, start_pos, T, qb, kc, vc);
     }
     const dim3 grid((T + kPfQB - 1) / kPfQB, 2);
     ProfScope prof(ctx, stream, "gqa_prefill_attn");
