@@ -645,19 +645,25 @@ __global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x
     }
 }
 
-template <int SB_DT, int X_DT, int Y_DT, bool NORM>
-__global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict__ w,
-                                                      const uint16_t* __restrict__ scales,
-                                                      const uint16_t* __restrict__ biases,
-                                                      const void* __restrict__ x, const float* __restrict__ xs,
-                                                      int xs_stride, void* __restrict__ y,
-                                                      const void* __restrict__ res, int rows, int cols,
+template <int SB_DT, int X_DT, bool NORM>
+__global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Parts parts, const void* __restrict__ x,
+                                                      const float* __restrict__ xs, int xs_stride, int cols,
                                                       int batch, Q4Norm nrm) {
+    // the part of this workgroup's row tile (parts' tiles are consecutive in x)
+    int pp = 0;
+    while (pp + 1 < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[pp + 1]) ++pp;
+    const uint32_t* __restrict__ w = parts.w[pp];
+    const uint16_t* __restrict__ scales = parts.s[pp];
+    const uint16_t* __restrict__ biases = parts.b[pp];
+    void* __restrict__ y = parts.y[pp];
+    const void* __restrict__ res = parts.res[pp];
+    const int rows = parts.rows[pp];
+    const bool ybf = parts.ybf16[pp];
     const int G = cols / 64;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
     const int wr = wave & 1, wm = wave >> 1;
-    const int R0 = blockIdx.x * 128, M0 = blockIdx.y * 128;
+    const int R0 = (blockIdx.x - parts.blk0[pp]) * 128, M0 = blockIdx.y * 128;
 
     __shared__ __attribute__((aligned(16))) uint16_t Wl[128 * kQ4LD];
     __shared__ __attribute__((aligned(16))) uint16_t Xl[128 * kQ4LD];
@@ -826,18 +832,22 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const uint32_t* __restrict
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (NORM) acc[rt][mt][i] *= rs;
-                if (res && r + i < rows) acc[rt][mt][i] += elem<Y_DT>::load(res, o + i);
+                if (res && r + i < rows)
+                    acc[rt][mt][i] += ybf ? elem<1>::load(res, o + i) : elem<0>::load(res, o + i);
             }
             if (r + 3 < rows && (rows & 3) == 0) {
-                if (Y_DT == 1)
+                if (ybf)
                     *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
                         u32x2_t{pack_bf16x2(acc[rt][mt][0], acc[rt][mt][1]), pack_bf16x2(acc[rt][mt][2], acc[rt][mt][3])};
                 else
                     *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = acc[rt][mt];
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (r + i < rows) elem<Y_DT>::store(y, o + i, acc[rt][mt][i]);
+                for (int i = 0; i < 4; ++i) {
+                    if (r + i >= rows) continue;
+                    if (ybf) elem<1>::store(y, o + i, acc[rt][mt][i]);
+                    else elem<0>::store(y, o + i, acc[rt][mt][i]);
+                }
             }
         }
     }
@@ -894,7 +904,8 @@ static Q4Parts q4_pack_parts(const qff_q4_part* parts, int nparts, int rpb, int&
 }
 
 // Many tokens: group sums (and inverse RMS) once per token slice, then one
-// tiled launch per part.
+// tiled launch over all parts (the small parts' tiles fill the chip beside the
+// large one's).
 template <bool NORM>
 static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                                 qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm,
@@ -911,27 +922,25 @@ static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
                 q4_xsum_kernel<0, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
                                                                         ctx->q4_xs_tokens, norm);
         }
+        // one launch over every part's row tiles, outputs offset to this slice
+        qff_q4_part sl[QFF_Q4_MAX_PARTS];
         for (int i = 0; i < nparts; ++i) {
-            const qff_q4_part& q = parts[i];
-            const size_t yoff = static_cast<size_t>(m0) * q.rows * (q.y_dtype == QFF_BF16 ? 2 : 4);
-            void* ym = static_cast<char*>(q.y) + yoff;
-            const void* rm = q.residual ? static_cast<const char*>(q.residual) + yoff : nullptr;
-            const uint16_t* s = static_cast<const uint16_t*>(q.scales);
-            const uint16_t* b = static_cast<const uint16_t*>(q.biases);
-            const dim3 grid((q.rows + 127) / 128, (mb + 127) / 128);
-            ProfScope prof(ctx, stream, "q4_gemm");
-#define QFF_Q4G(S, X, Y)                                                                                 \
-    q4_gemm_kernel<S, X, Y, NORM><<<grid, 256, 0, stream>>>(q.w, s, b, xm, ctx->q4_xs, ctx->q4_xs_tokens, \
-                                                            ym, rm, q.rows, cols, mb, norm)
-#define QFF_Q4G_Y(S, X) \
-    if (q.y_dtype == QFF_BF16) QFF_Q4G(S, X, 1); else QFF_Q4G(S, X, 0)
-#define QFF_Q4G_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4G_Y(S, 1); } else { QFF_Q4G_Y(S, 0); }
-            if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
-#undef QFF_Q4G_X
-#undef QFF_Q4G_Y
-#undef QFF_Q4G
+            sl[i] = parts[i];
+            const size_t yoff = static_cast<size_t>(m0) * parts[i].rows * (parts[i].y_dtype == QFF_BF16 ? 2 : 4);
+            sl[i].y = static_cast<char*>(parts[i].y) + yoff;
+            if (parts[i].residual) sl[i].residual = static_cast<const char*>(parts[i].residual) + yoff;
         }
+        int tiles = 0;
+        const Q4Parts P = q4_pack_parts(sl, nparts, 128, tiles);
+        const dim3 grid(tiles, (mb + 127) / 128);
+        ProfScope prof(ctx, stream, "q4_gemm");
+#define QFF_Q4G(S, X) \
+    q4_gemm_kernel<S, X, NORM><<<grid, 256, 0, stream>>>(P, xm, ctx->q4_xs, ctx->q4_xs_tokens, cols, mb, norm)
+#define QFF_Q4G_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4G(S, 1); } else { QFF_Q4G(S, 0); }
+        if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
+#undef QFF_Q4G_X
+#undef QFF_Q4G
     }
     return hipGetLastError();
 }
