@@ -7,8 +7,9 @@
 //   chunked    conv1d + SiLU, L2 norms, gates and the chunked WY form of the
 //              gated delta rule (deltanet_chunked.hip), pre-norm outputs to
 //              workspace;
-//   norm       gated RMSNorm of every (token, value head) output row;
-//   conv state the conv state after the last token.
+//   norm       gated RMSNorm of every (token, value head) output row, and
+//              (32 extra workgroups of the same launch) the conv state after
+//              the last token.
 #include "common.hpp"
 #include "internal.hpp"
 #include "mfma.hpp"
@@ -57,8 +58,23 @@ template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __restrict__ po,
                                                               const void* __restrict__ z,
                                                               const float* __restrict__ norm_w, float eps,
-                                                              void* __restrict__ out) {
-    const int tok = blockIdx.x, t = threadIdx.x;
+                                                              void* __restrict__ out, int T,
+                                                              const void* __restrict__ qkv,
+                                                              float* __restrict__ conv_state) {
+    const int t = threadIdx.x;
+    if (blockIdx.x >= static_cast<unsigned>(T)) {
+        // the 32 workgroups past the tokens: conv state after the last token,
+        // slots = e[T .. T+3] of channel c (the chunk-local pass has read the
+        // old slots before this launch)
+        const int c = (blockIdx.x - T) * 256 + t;
+        const float e0 = conv_ext<IN_DT>(conv_state, qkv, c, T);
+        const float e1 = conv_ext<IN_DT>(conv_state, qkv, c, T + 1);
+        const float e2 = conv_ext<IN_DT>(conv_state, qkv, c, T + 2);
+        const float e3 = conv_ext<IN_DT>(conv_state, qkv, c, T + 3);
+        reinterpret_cast<float4*>(conv_state)[c] = make_float4(e0, e1, e2, e3);
+        return;
+    }
+    const int tok = blockIdx.x;
     const int r0 = 16 * (t & 7);
     const size_t base = static_cast<size_t>(tok) * 4096 + (t >> 3) * 128 + r0;
     float o[2][8], zz[2][8], ss = 0.0f;
@@ -81,18 +97,6 @@ __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __res
     }
 }
 
-// conv state after the last token: slots = e[T .. T+3]. grid 32 x 256.
-template <int IN_DT>
-__global__ __launch_bounds__(256) void dn_prefill_conv_state_kernel(int T, const void* __restrict__ qkv,
-                                                                    float* __restrict__ conv_state) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    const float e0 = conv_ext<IN_DT>(conv_state, qkv, c, T);
-    const float e1 = conv_ext<IN_DT>(conv_state, qkv, c, T + 1);
-    const float e2 = conv_ext<IN_DT>(conv_state, qkv, c, T + 2);
-    const float e3 = conv_ext<IN_DT>(conv_state, qkv, c, T + 3);
-    reinterpret_cast<float4*>(conv_state)[c] = make_float4(e0, e1, e2, e3);
-}
-
 hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
                                    const void* qkv, const void* z, qff_dtype in_dtype,
                                    const float* a, const float* b, float* conv_state,
@@ -102,20 +106,17 @@ hipError_t launch_deltanet_prefill(qff_ctx* ctx, hipStream_t stream, const qff_d
         hipError_t e = launch_deltanet_chunked(ctx, stream, p, qkv, in_dtype, a, b, conv_state, ssm_state, T);
         if (e != hipSuccess) return e;
     }
-    const dim3 ng(T);
-    {
+    const dim3 ng(T + 32);
     ProfScope prof(ctx, stream, "dn_prefill_norm");
-#define QFF_NORM(I, O) dn_prefill_norm_kernel<I, O><<<ng, 256, 0, stream>>>(ctx->pf_o, z, p->norm_w, p->eps, out)
+#define QFF_NORM(I, O)                                                                                   \
+    dn_prefill_norm_kernel<I, O><<<ng, 256, 0, stream>>>(ctx->pf_o, z, p->norm_w, p->eps, out, T, qkv, \
+                                                         conv_state)
     if (bf) {
         if (out_dtype == QFF_BF16) QFF_NORM(1, 1); else QFF_NORM(1, 0);
     } else {
         if (out_dtype == QFF_BF16) QFF_NORM(0, 1); else QFF_NORM(0, 0);
     }
 #undef QFF_NORM
-    }
-    ProfScope prof(ctx, stream, "dn_prefill_conv_state");
-    if (bf) dn_prefill_conv_state_kernel<1><<<32, 256, 0, stream>>>(T, qkv, conv_state);
-    else dn_prefill_conv_state_kernel<0><<<32, 256, 0, stream>>>(T, qkv, conv_state);
     return hipGetLastError();
 }
 
