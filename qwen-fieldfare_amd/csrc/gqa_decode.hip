@@ -16,8 +16,8 @@
 //            scale and log2 e folded in); the one whose chunk holds the new
 //            token also normalises/rotates k, appends k and v to the cache
 //            and keeps both in LDS for its own use. It then walks 16-position
-//            tiles (long chunks: the next tile's K and V rows already in
-//            flight, two register stages): S^T = K Q^T with 8 MFMA 16x16x32
+//            tiles with the next tile's K and V rows already in flight (two
+//            register stages): S^T = K Q^T with 8 MFMA 16x16x32
 //            (K rows straight from HBM, 16 B per lane), base-2 online softmax
 //            per head whose running max is raised only past 2^8 (so O is
 //            rarely rescaled), the V tile copied row-major into LDS and read
@@ -70,9 +70,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // rarely rescaled), the V tile copied row-major into LDS and read back as
 // MFMA B operands with the gfx950 transpose read (ds_read_b64_tr_b16),
 // O += P V with 16 MFMA 16x16x16, and writes one (m, d, o[8][256]) partial
-// (m in base-2 units). PIPE keeps the next tile's loads in flight (two
-// register stages, for long chunks).
-template <int IN_DT, bool PIPE>
+// (m in base-2 units). The next tile's loads are in flight while a tile
+// computes (two register stages).
+template <int IN_DT>
 __device__ __forceinline__ void gqa_partial_unit(
     DecLds& L, int seq, int kvh, int c, int pos, int lane, const void* __restrict__ q_gate,
     const void* __restrict__ k_new, const void* __restrict__ v_new, const float* __restrict__ q_norm_w,
@@ -114,8 +114,8 @@ __device__ __forceinline__ void gqa_partial_unit(
     // .swift:1090-1099 with host-computed inverse frequencies). Lane -> head
     // u/32, dims 8*(u%32) .. +7 for u = lane + 64 it; the RoPE pair (d, d^32)
     // of dims < 64 sits in lanes 4 apart. The q rows and norm weights are
-    // requested first and, for long chunks, the first tile's K/V rows right
-    // behind them, so the q work waits for its own loads only.
+    // requested first and the first tile's K/V rows right behind them, so
+    // the q work waits for its own loads only.
     float xq[4][8], qw[8];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -128,7 +128,7 @@ __device__ __forceinline__ void gqa_partial_unit(
     for (int i = 0; i < 8; ++i) qw[i] = q_norm_w[8 * (lane & 31) + i];
     __builtin_amdgcn_sched_barrier(0);
     DecTile ta, tb;
-    if (PIPE) load(ta, p_start);
+    load(ta, p_start);
     __builtin_amdgcn_sched_barrier(0);
     if (lane < 32) {
         const float ang = static_cast<float>(pos) * freqs[lane];
@@ -276,21 +276,14 @@ __device__ __forceinline__ void gqa_partial_unit(
         for (int jd = 0; jd < 16; ++jd) oacc[jd] = mfma_16x16x16_bf16(pa, lds_read_tr16(vsrc + 16 * jd), oacc[jd]);
         wave_lds_sync();
     };
-    if (PIPE) {
-        int p0 = p_start;
-        for (; p0 + kDecTile < p_end; p0 += 2 * kDecTile) {
-            load(tb, p0 + kDecTile);
-            compute(ta, p0);
-            load(ta, p0 + 2 * kDecTile);
-            compute(tb, p0 + kDecTile);
-        }
-        if (p0 < p_end) compute(ta, p0);
-    } else {
-        for (int p0 = p_start; p0 < p_end; p0 += kDecTile) {
-            load(ta, p0);
-            compute(ta, p0);
-        }
+    int p0 = p_start;
+    for (; p0 + kDecTile < p_end; p0 += 2 * kDecTile) {
+        load(tb, p0 + kDecTile);
+        compute(ta, p0);
+        load(ta, p0 + 2 * kDecTile);
+        compute(tb, p0 + kDecTile);
     }
+    if (p0 < p_end) compute(ta, p0);
     // ---- partial (m, d, o) of this chunk; oacc[jd][i] = O[head 4kb+i][dim 16jd+n]
     d_run += __shfl_xor(d_run, 16, 64);
     d_run += __shfl_xor(d_run, 32, 64);
@@ -311,11 +304,12 @@ __device__ __forceinline__ void gqa_partial_unit(
 // Static grid for short chunks: grid (2 kv heads x chunks, 1, batch), one
 // wave each; the kv head is the fastest-varying block index, so the two
 // heads' workgroups of a chunk are dispatched together and stream the
-// interleaved halves of the same cache records at the same time. Three or
-// more single-wave workgroups per SIMD stay resident. Lengths come from the
+// interleaved halves of the same cache records at the same time. Two
+// single-wave workgroups per SIMD stay resident, each with its next tile in
+// flight. Lengths come from the
 // device `positions` array; waves past a sequence's last chunk exit at once.
 template <int IN_DT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
@@ -332,7 +326,7 @@ void gqa_decode_partial_kernel(
     const int lane = threadIdx.x & 63;
     if (lane < 32) freqs[lane] = rf.f[lane];
     wave_lds_sync();
-    gqa_partial_unit<IN_DT, false>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
+    gqa_partial_unit<IN_DT>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
                                    scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
@@ -361,7 +355,7 @@ void gqa_decode_group_kernel(
     // a position outside the cache is the caller's error: skip the sequence
     // (the combine writes NaN for it) rather than touch memory past the cache
     if (pos < 0 || pos >= max_ctx || c * chunk_len > pos) return;
-    gqa_partial_unit<IN_DT, true>(lds[wave], seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w,
+    gqa_partial_unit<IN_DT>(lds[wave], seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w,
                                   freqs, scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
