@@ -359,25 +359,29 @@ void gqa_decode_group_kernel(
                                   freqs, scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
-// grid (16 q heads, batch), 512 threads: attention.metal:342-377 merge, then
-// the gate of deltanet.metal:700-708. Chunk weights are formed one thread per
-// chunk; then wave w sums chunks w, w+8, ... for all 256 dims (a float4 per
-// lane) so each lane has few dependent loads in flight, and the 8 wave sums
-// are added in LDS in a fixed order.
-template <int IN_DT, int OUT_DT>
+// grid (16 q heads x DS dim blocks, batch), 512 threads: attention.metal
+// :342-377 merge, then the gate of deltanet.metal:700-708, for 256 / DS dims
+// per workgroup (DS = 4 at small batches, so more than 16 workgroups share
+// the partial reads). Chunk weights are formed one thread per chunk; then
+// the 8 DS chunk streams (stream s sums chunks s, s + 8 DS, ...; 64 / DS
+// lanes per stream, a float4 of dims per lane) keep few dependent loads in
+// flight per lane, and their sums are added in LDS in a fixed order.
+template <int IN_DT, int OUT_DT, int DS>
 __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int max_ctx, int chunk_len,
     int cstride, const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
+    constexpr int kDims = 256 / DS, kLanes = 64 / DS, kStreams = 8 * DS;
     __shared__ float es[kGqaMaxChunks], red[16];
-    __shared__ __attribute__((aligned(16))) float osum[8][256];
-    const int h = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float osum[kStreams][kDims];
+    const int h = blockIdx.x / DS, dblk = blockIdx.x % DS, seq = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int kvh = h >> 3, hl = h & 7;
+    const int d0 = dblk * kDims;
     const size_t qi = (static_cast<size_t>(seq) * 16 + h);
     const int pos = positions[seq];
     if (pos < 0 || pos >= max_ctx) {
-        if (t < 256) elem<OUT_DT>::store(out, qi * 256 + t, __builtin_nanf(""));
+        if (t < kDims) elem<OUT_DT>::store(out, qi * 256 + d0 + t, __builtin_nanf(""));
         return;
     }
     const int L = pos + 1;
@@ -396,35 +400,36 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const float wd = group_sum<64>(d * e);
     if (lane == 0) red[8 + wave] = wd;
     __syncthreads();
-    const float4* pr = reinterpret_cast<const float4*>(po + (base * 8 + hl) * 256) + lane;  // chunk c at pr[c*512]
+    const int sid = wave * DS + lane / kLanes, f = lane % kLanes;
+    // chunk c of this head at pr[c * 512]
+    const float4* pr = reinterpret_cast<const float4*>(po + (base * 8 + hl) * 256 + d0) + f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int c = wave;
-    for (; c + 24 < nc; c += 32) {
+    int c = sid;
+    for (; c + 3 * kStreams < nc; c += 4 * kStreams) {
         float4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = pr[static_cast<size_t>(c + 8 * u) * 512];
+        for (int u = 0; u < 4; ++u) v[u] = pr[static_cast<size_t>(c + kStreams * u) * 512];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float w = es[c + 8 * u];
+            const float w = es[c + kStreams * u];
             acc.x += v[u].x * w; acc.y += v[u].y * w; acc.z += v[u].z * w; acc.w += v[u].w * w;
         }
     }
-    for (; c < nc; c += 8) {
+    for (; c < nc; c += kStreams) {
         const float4 v = pr[static_cast<size_t>(c) * 512];
         const float w = es[c];
         acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
     }
-    reinterpret_cast<float4*>(osum[wave])[lane] = acc;
+    reinterpret_cast<float4*>(osum[sid])[f] = acc;
     __syncthreads();
-    if (t < 256) {
+    if (t < kDims) {
         float D = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            D += red[8 + w];
-            O += osum[w][t];
-        }
-        const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + t);
-        elem<OUT_DT>::store(out, qi * 256 + t, (O / D) * sigmoid(gate));
+        for (int w = 0; w < 8; ++w) D += red[8 + w];
+#pragma unroll
+        for (int s2 = 0; s2 < kStreams; ++s2) O += osum[s2][t];
+        const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + d0 + t);
+        elem<OUT_DT>::store(out, qi * 256 + d0 + t, (O / D) * sigmoid(gate));
     }
 }
 
@@ -476,14 +481,21 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
 #undef QFF_PART
         }
     }
-    const dim3 cgrid(16, batch);
+    // small batches split each head's 256 dims over 4 workgroups
+    const int ds = batch <= 8 ? 4 : 1;
+    const dim3 cgrid(16 * ds, batch);
     ProfScope prof(ctx, stream, "gqa_decode_combine");
-#define QFF_COMB(I, O) \
-    gqa_decode_combine_kernel<I, O><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap, ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
+#define QFF_COMB(I, O)                                                                                      \
+    if (ds == 4)                                                                                            \
+        gqa_decode_combine_kernel<I, O, 4><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
+                                                                      ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out); \
+    else                                                                                                    \
+        gqa_decode_combine_kernel<I, O, 1><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
+                                                                      ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
     if (in_dtype == QFF_BF16) {
-        if (out_dtype == QFF_BF16) QFF_COMB(1, 1); else QFF_COMB(1, 0);
+        if (out_dtype == QFF_BF16) { QFF_COMB(1, 1); } else { QFF_COMB(1, 0); }
     } else {
-        if (out_dtype == QFF_BF16) QFF_COMB(0, 1); else QFF_COMB(0, 0);
+        if (out_dtype == QFF_BF16) { QFF_COMB(0, 1); } else { QFF_COMB(0, 0); }
     }
 #undef QFF_COMB
     return hipGetLastError();
