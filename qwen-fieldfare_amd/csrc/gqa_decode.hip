@@ -9,9 +9,9 @@
 //
 // Here the eight q heads that share a kv head run in the same wave, so every
 // K/V byte is read from HBM once, and both products run on the matrix cores:
-//   partial  one wave per (sequence, kv head, chunk) unit: a static grid of
-//            single-wave workgroups for short chunks, a persistent grid that
-//            hands units out through an atomic queue for long ones. The wave
+//   partial  one single-wave workgroup per (sequence, kv head, chunk) unit
+//            (four-wave workgroups of four chunks and a persistent grid on an
+//            atomic queue were measured no faster and slower). The wave
 //            normalises and rotates the 8 q heads into LDS (bf16, softmax
 //            scale and log2 e folded in); the one whose chunk holds the new
 //            token also normalises/rotates k, appends k and v to the cache
@@ -301,8 +301,7 @@ __device__ __forceinline__ void gqa_partial_unit(
     }
 }
 
-// Static grid for short chunks: grid (2 kv heads x chunks, 1, batch), one
-// wave each; the kv head is the fastest-varying block index, so the two
+// grid (2 kv heads x chunks, 1, batch), one wave each; the kv head is the fastest-varying block index, so the two
 // heads' workgroups of a chunk are dispatched together and stream the
 // interleaved halves of the same cache records at the same time. Two
 // single-wave workgroups per SIMD stay resident, each with its next tile in
@@ -328,35 +327,6 @@ void gqa_decode_partial_kernel(
     wave_lds_sync();
     gqa_partial_unit<IN_DT>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
                                    scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
-}
-
-// Long chunks: grid (2 kv heads x ceil(chunks / 4), 1, batch), four waves
-// per workgroup, wave w taking chunk 4 * group + w of the workgroup's kv
-// head (kv head fastest, so the two heads' workgroups of a chunk group are
-// dispatched together and stream the interleaved halves of the same cache
-// records), each keeping the next tile's loads in flight (two register
-// stages, two waves per SIMD).
-template <int IN_DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void gqa_decode_group_kernel(
-    const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
-    const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
-    float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
-    float* __restrict__ pd, float* __restrict__ po) {
-    __shared__ __attribute__((aligned(16))) DecLds lds[4];
-    __shared__ float freqs[32];   // RoPE inverse frequencies
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kvh = blockIdx.x & 1, c = 4 * (blockIdx.x >> 1) + wave, seq = blockIdx.z;
-    const int pos = positions[seq];
-    if (threadIdx.x < 32) freqs[threadIdx.x] = rf.f[threadIdx.x];
-    __syncthreads();
-    // a position outside the cache is the caller's error: skip the sequence
-    // (the combine writes NaN for it) rather than touch memory past the cache
-    if (pos < 0 || pos >= max_ctx || c * chunk_len > pos) return;
-    gqa_partial_unit<IN_DT>(lds[wave], seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w,
-                                  freqs, scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
 // grid (16 q heads x DS dim blocks, batch), 512 threads: attention.metal
@@ -465,21 +435,12 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     {
         ProfScope prof(ctx, stream, "gqa_decode_partial");
-        if (ch >= 256) {
-#define QFF_PART(I)                                                                                             \
-    gqa_decode_group_kernel<I><<<dim3(2 * ((nc + 3) / 4), 1, batch), 256, 0, stream>>>(                         \
-        q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
-        ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
-            if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
-#undef QFF_PART
-        } else {
 #define QFF_PART(I)                                                                                            \
     gqa_decode_partial_kernel<I><<<dim3(2 * nc, 1, batch), 64, 0, stream>>>(                                   \
         q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
         ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
-            if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
+        if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
 #undef QFF_PART
-        }
     }
     // small batches split each head's 256 dims over 4 workgroups
     const int ds = batch <= 8 ? 4 : 1;
