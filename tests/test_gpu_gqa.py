@@ -77,6 +77,14 @@ def test_gqa_decode_long_context(hip):
     _run_case(hip, [65536, 40000], 65536)
 
 
+def test_gqa_decode_config4_shape(hip):
+    # config 4's batch-16 decode at 32K context: 256-position chunks, 128 per
+    # sequence and kv head, the full-dims combine
+    rng = np.random.default_rng(16)
+    lengths = list(rng.integers(1, 32769, 14)) + [32768, 257]
+    _run_case(hip, lengths, 32768, out_dtype=torch.bfloat16, seed=16)
+
+
 @pytest.mark.parametrize("L", [65536, 50001])
 def test_gqa_decode_batch1_long_context(hip, L):
     # config 4's single-sequence decode: batch 1 spreads the split over 512
