@@ -142,7 +142,8 @@ struct Q4Norm {
     float eps = 0.0f;
 };
 // Product over up to QFF_Q4_MAX_PARTS parts sharing x: one launch for decode
-// batches, one group-sum pass plus one tiled launch per part for many tokens.
+// batches, one group-sum pass plus one tiled launch over all parts for many
+// tokens.
 hipError_t launch_q4_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                            qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm, int cols,
                            int batch);
