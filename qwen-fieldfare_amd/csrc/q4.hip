@@ -646,7 +646,7 @@ __global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x
 }
 
 template <int SB_DT, int X_DT, bool NORM>
-__global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Parts parts, const void* __restrict__ x,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q4_gemm_kernel(Q4Parts parts, const void* __restrict__ x,
                                                       const float* __restrict__ xs, int xs_stride, int cols,
                                                       int batch, Q4Norm nrm) {
     // the part of this workgroup's row tile (parts' tiles are consecutive in x)
@@ -682,11 +682,17 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Parts parts, const void*
     const uint32_t* wsrc = w + static_cast<size_t>(min(R0 + srow, rows - 1)) * (cols / 8) + 4 * shalf;
     const int xm = min(M0 + srow, batch - 1);
     const int xsm = min(M0 + (t & 127), batch - 1);
-    u32x4_t wreg, xreg[4];
-    float xsreg;
-    auto fetch = [&](int g) {
+    // one group's staging registers; two stages (raw x) keep groups g+1 and
+    // g+2 in flight while group g computes
+    struct Stage {
+        u32x4_t w, x[4];
+        float xs;
+    };
+    auto fetch = [&](Stage& st, int g) {
+        u32x4_t& wreg = st.w;
+        u32x4_t (&xreg)[4] = st.x;
         wreg = *reinterpret_cast<const u32x4_t*>(wsrc + 8 * g);
-        xsreg = xs[static_cast<size_t>(g) * xs_stride + xsm];
+        st.xs = xs[static_cast<size_t>(g) * xs_stride + xsm];
         const size_t xo = static_cast<size_t>(xm) * cols + 64 * g + 32 * shalf;
         if (NORM) {
             // bf16(x w_norm); the token's inverse RMS scales the result
@@ -734,16 +740,20 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Parts parts, const void*
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    fetch(0);
-    for (int g = 0; g < G; ++g) {
+    // group g from stage st, then st refilled with group gn (clamped, so the
+    // loads are unconditional and the compiler's vmcnt bookkeeping exact)
+    auto step = [&](Stage& st, int g, int gn) {
+        // (the two stages' steps are kept apart: interleaved by the scheduler
+        // they would not fit the registers)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<u32x4_t*>(&Wl[srow * kQ4LD + 32 * shalf + 8 * i]) = q4_to_bf16_interleaved(wreg[i]);
-            *reinterpret_cast<u32x4_t*>(&Xl[srow * kQ4LD + 32 * shalf + 8 * i]) = interleave8(xreg[i]);
+            *reinterpret_cast<u32x4_t*>(&Wl[srow * kQ4LD + 32 * shalf + 8 * i]) = q4_to_bf16_interleaved(st.w[i]);
+            *reinterpret_cast<u32x4_t*>(&Xl[srow * kQ4LD + 32 * shalf + 8 * i]) = interleave8(st.x[i]);
         }
-        if (t < 128) xsl[t] = -128.0f * xsreg;
+        if (t < 128) xsl[t] = -128.0f * st.xs;
         __syncthreads();
-        if (g + 1 < G) fetch(g + 1);
+        fetch(st, gn);
         f32x4_t P[4][4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -774,6 +784,22 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Parts parts, const void*
                 for (int i = 0; i < 4; ++i) acc[rt][mt][i] = fmaf(sv[i], P[rt][mt][i], acc[rt][mt][i]);
         }
         __syncthreads();
+    };
+    Stage s0;
+    fetch(s0, 0);
+    if constexpr (NORM) {
+        // the normed x is formed as it is fetched, so its loads complete in
+        // the fetch: one stage (a second would not fit the registers)
+        for (int g = 0; g < G; ++g) step(s0, g, min(g + 1, G - 1));
+    } else {
+        Stage s1;
+        fetch(s1, min(1, G - 1));
+        int g = 0;
+        for (; g + 1 < G; g += 2) {
+            step(s0, g, min(g + 2, G - 1));
+            step(s1, g + 1, min(g + 3, G - 1));
+        }
+        if (g < G) step(s0, g, g);
     }
     // bias sums: acc += B X^T over the groups (k = g), bf16x3. A lane holds
     // B[row][8kb .. 8kb+7] and X[token][8kb .. 8kb+7] of a 32-group step;
