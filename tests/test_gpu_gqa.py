@@ -85,6 +85,43 @@ def test_gqa_decode_config4_shape(hip):
     _run_case(hip, lengths, 32768, out_dtype=torch.bfloat16, seed=16)
 
 
+@pytest.mark.parametrize("B", [3, 10])
+def test_gqa_decode_position_outside_cache(hip, B):
+    """A sequence whose position lies outside the cache (negative or >=
+    max_ctx) gets NaN outputs and leaves its cache rows untouched; the other
+    sequences of the batch are unaffected (both combine shapes: B <= 8 and
+    B > 8)."""
+    import qff
+    max_ctx = 512
+    print(f"gqa_decode invalid positions B={B}", flush=True)
+    p = synth.gqa_params()
+    inp = synth.gqa_decode_inputs(B, max_ctx, seed=70 + B, lengths=[200 + 30 * i for i in range(B)])
+    bad = {1: -1, B - 1: max_ctx}
+    positions = inp["positions"].copy()
+    for s_, v in bad.items():
+        positions[s_] = v
+    ctx = qff.Context(max_batch=B, max_ctx=max_ctx, max_prefill_tokens=1)
+    kc, vc = bf16_tensor(inp["k_cache"]), bf16_tensor(inp["v_cache"])
+    out = qff.gqa_decode(ctx, {k: f32_tensor(v) for k, v in p.items()}, bf16_tensor(inp["q_gate"]),
+                         bf16_tensor(inp["k_new"]), bf16_tensor(inp["v_new"]), kc, vc,
+                         torch.from_numpy(positions).to(DEV), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    kc_g = kc.cpu().view(torch.int16).numpy().view(np.uint16)
+    vc_g = vc.cpu().view(torch.int16).numpy().view(np.uint16)
+    for s_ in range(B):
+        if s_ in bad:
+            assert np.isnan(got[s_]).all()
+            assert np.array_equal(kc_g[s_], inp["k_cache"][s_]) and np.array_equal(vc_g[s_], inp["v_cache"][s_])
+            continue
+        pos = int(positions[s_])
+        kref, vref = inp["k_cache"][s_].copy(), inp["v_cache"][s_].copy()
+        O.gqa_append_kv_seq(O.bf16_to_f32(inp["k_new"][s_])[None], O.bf16_to_f32(inp["v_new"][s_])[None],
+                            p["k_norm_w"], kref, vref, O.BF16, start_pos=pos)
+        ref = O.gqa_attend(O.bf16_to_f32(inp["q_gate"][s_]), p["q_norm_w"], kref, vref, O.BF16, pos)
+        assert_f32_output_close(got[s_], ref)
+
+
 @pytest.mark.parametrize("L", [65536, 50001])
 def test_gqa_decode_batch1_long_context(hip, L):
     # config 4's single-sequence decode: batch 1 spreads the split over 512
