@@ -277,7 +277,9 @@ int qff_gqa_decode(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
  * values appended to the cache. The reference runs prompts token by token
  * through the decode path (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561).
  *   q_gate [T, 16, 512], k, v [T, 2, 256] (in_dtype);
- *   k_cache, v_cache [max_ctx, 2, 256] bf16; out [T, 16, 256] (out_dtype). */
+ *   k_cache, v_cache [max_ctx, 2, 256] bf16; out [T, 16, 256] (out_dtype).
+ * QFF_ERR_INVALID_ARG when start_pos + T > max_ctx; QFF_ERR_WORKSPACE when T
+ * exceeds the context's max_prefill_tokens. */
 int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
                     const void* q_gate, const void* k, const void* v,
                     qff_dtype in_dtype, void* k_cache, void* v_cache,

@@ -381,6 +381,7 @@ int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p, 
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return QFF_ERR_INVALID_ARG;
     if (T <= 0 || start_pos < 0 || max_ctx <= 0) return QFF_ERR_INVALID_ARG;
     if (static_cast<long long>(start_pos) + T > max_ctx) return QFF_ERR_INVALID_ARG;
+    if (T > ctx->cfg.max_prefill_tokens) return QFF_ERR_WORKSPACE;   // the staged q rows hold that many tokens
     QFF_CHECK_HIP(launch_gqa_prefill(ctx, stream, p, q_gate, k, v, in_dtype, k_cache, v_cache, start_pos,
                                      out, out_dtype, T, max_ctx));
     return QFF_OK;

@@ -220,3 +220,32 @@ def test_gqa_prefill_config3_full_length_sampled_rows(hip):
     rows = sorted({0, 1, 15, 16, 31, 32, 33, 1000, 4095, 4096, 8190, 8191} |
                   set(np.random.default_rng(3).integers(0, 8192, 6).tolist()))
     _prefill_case(hip, 8192, 0, max_ctx=8192, rows=rows)
+
+
+def test_gqa_rejects_bad_calls(hip):
+    """Host-side checks: nothing is launched for these."""
+    import qff
+    max_ctx = 64
+    ctx = qff.Context(max_batch=2, max_ctx=max_ctx, max_prefill_tokens=8)
+    pg = {k: f32_tensor(v) for k, v in synth.gqa_params().items()}
+    kc = torch.zeros(max_ctx, 2, 256, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+
+    def prefill(T, start):
+        qg = torch.zeros(T, 16, 512, dtype=torch.bfloat16, device=DEV)
+        kv = torch.zeros(T, 2, 256, dtype=torch.bfloat16, device=DEV)
+        return qff.gqa_prefill(ctx, pg, qg, kv, kv, kc, vc, start)
+
+    with pytest.raises(qff.QffError) as e:       # T above max_prefill_tokens
+        prefill(16, 0)
+    assert e.value.status == -4
+    with pytest.raises(qff.QffError) as e:       # past the end of the cache
+        prefill(8, 60)
+    assert e.value.status == -1
+    qg = torch.zeros(3, 16, 512, dtype=torch.bfloat16, device=DEV)
+    kn = torch.zeros(3, 2, 256, dtype=torch.bfloat16, device=DEV)
+    kc3 = torch.zeros(3, max_ctx, 2, 256, dtype=torch.bfloat16, device=DEV)
+    pos = torch.zeros(3, dtype=torch.int32, device=DEV)
+    with pytest.raises(qff.QffError) as e:       # batch above max_batch
+        qff.gqa_decode(ctx, pg, qg, kn, kn, kc3, kc3.clone(), pos)
+    assert e.value.status == -4
