@@ -22,12 +22,12 @@
 //            with 32-lane butterfly sums;
 //   phase 3  gated RMSNorm of both heads from LDS.
 // Batch <= 4: 16 workgroups per sequence would leave the chip idle, so the
-// step is split over 128 workgroups per sequence in two launches; every
+// step is split over 256 workgroups per sequence in two launches; every
 // workgroup of the first reads the old conv state, the second writes it:
-//   dn_decode_state_kernel  grid (32 value heads x 4 row parts, batch), 256
+//   dn_decode_state_kernel  grid (32 value heads x 8 row parts, batch), 256
 //       threads: conv + SiLU of the key head's q and k channels and the
-//       part's v channels (conv state read only), L2 norms, then the 32
-//       state rows of the part as above (4 float4 per lane); pre-norm output
+//       part's v channels (conv state read only), L2 norms, then the 16
+//       state rows of the part as above (2 float4 per lane); pre-norm output
 //       rows to the context workspace;
 //   dn_decode_norm_kernel  grid (32 heads, batch): gated RMSNorm of each
 //       head's output, and the conv-state shift of 256 channels per
@@ -267,7 +267,7 @@ hipError_t launch_deltanet_decode(qff_ctx* ctx, hipStream_t stream, const qff_de
 #undef QFF_DN_LAUNCH
         return hipGetLastError();
     }
-    constexpr int R = 4;
+    constexpr int R = 8;   // row parts per head (4 and 16 measured slower at batch 1)
     const dim3 sgrid(32 * R, batch), ngrid(32, batch);
     if (bf_in)
         dn_decode_state_kernel<1, R><<<sgrid, 256, 0, stream>>>(qkv, a, b, p->a_log, p->dt_bias, p->conv_w,
