@@ -411,15 +411,15 @@ int gqa_chunk_cap(const qff_ctx_cfg& cfg, int batch) {
 }
 
 // Chunk length: aim for ~4096 one-wave partial workgroups over the batch
-// (16 per CU), at most `cap` chunks per sequence, multiples of 64 positions
-// (4 MFMA tiles).
+// (16 per CU), at most `cap` chunks per sequence, multiples of 32 positions
+// (2 MFMA tiles; 64 measured 3-5 % slower at batch 1 and 8).
 int gqa_chunk_len(int max_ctx, int batch, int cap) {
     int target = 4096 / (2 * batch);
     if (target < 1) target = 1;
     if (target > cap) target = cap;
     const int per = (max_ctx + target - 1) / target;
-    const int ch = ((per + 63) / 64) * 64;
-    return ch < 64 ? 64 : ch;
+    const int ch = ((per + 31) / 32) * 32;
+    return ch < 32 ? 32 : ch;
 }
 
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
