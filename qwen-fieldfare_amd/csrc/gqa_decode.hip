@@ -410,16 +410,25 @@ int gqa_chunk_cap(const qff_ctx_cfg& cfg, int batch) {
     return cap < kGqaMaxChunks ? cap : kGqaMaxChunks;
 }
 
-// Chunk length: aim for ~4096 one-wave partial workgroups over the batch
-// (16 per CU), at most `cap` chunks per sequence, multiples of 32 positions
-// (2 MFMA tiles; 64 measured 3-5 % slower at batch 1 and 8).
-int gqa_chunk_len(int max_ctx, int batch, int cap) {
-    int target = 4096 / (2 * batch);
+// Chunk length for `waves` one-wave partial workgroups over the batch, at
+// most `cap` chunks per sequence, multiples of 32 positions (2 MFMA tiles).
+static int gqa_chunk_len_for(int max_ctx, int batch, int cap, int waves) {
+    int target = waves / (2 * batch);
     if (target < 1) target = 1;
     if (target > cap) target = cap;
     const int per = (max_ctx + target - 1) / target;
     const int ch = ((per + 31) / 32) * 32;
     return ch < 32 ? 32 : ch;
+}
+
+// One round of resident waves (two per SIMD) when that still gives chunks of
+// 512 positions or more, else two rounds: long contexts lose less to a
+// second round's tail than short ones gain from more waves (measured: config
+// 4 at 32K 2.7 % faster with one round, config 2 at 8K 6 % slower).
+int gqa_chunk_len(int max_ctx, int batch, int cap, int num_cu) {
+    const int resident = 8 * num_cu;
+    const int one = gqa_chunk_len_for(max_ctx, batch, cap, resident);
+    return one >= 512 ? one : gqa_chunk_len_for(max_ctx, batch, cap, 2 * resident);
 }
 
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
@@ -428,7 +437,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                              int max_ctx) {
     const int cap = gqa_chunk_cap(ctx->cfg, batch);
-    const int ch = gqa_chunk_len(max_ctx, batch, cap);
+    const int ch = gqa_chunk_len(max_ctx, batch, cap, ctx->num_cu);
     const int nc = (max_ctx + ch - 1) / ch;
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
