@@ -1,0 +1,78 @@
+"""numpy front-end to oracle/cpu_baseline.c: the reference's CPU algorithms
+with OpenMP drivers, timed as bench.py's CPU baseline.
+
+TEST INFRASTRUCTURE ONLY: loaded by bench.py's cpu_baseline leg and by
+tests/ (which check it against the oracle bit for bit), never by the
+product.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PORTABLE = os.path.join(HERE, "build", "libqff_cpu_baseline.so")
+NATIVE_FLAGS = ["-O3", "-march=native", "-fopenmp", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-std=c11"]
+
+_fp = ctypes.POINTER(ctypes.c_float)
+
+
+def build_native(outdir: str) -> str | None:
+    """Compile cpu_baseline.c for the host this runs on (gcc -O3
+    -march=native -fopenmp) into outdir; None when no compiler works."""
+    os.makedirs(outdir, exist_ok=True)
+    out = os.path.join(outdir, "libqff_cpu_baseline_native.so")
+    cmd = ["gcc", *NATIVE_FLAGS, "-shared", "-o", out, os.path.join(HERE, "cpu_baseline.c"), "-lm"]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return out if r.returncode == 0 else None
+
+
+def load(path: str | None = None):
+    L = ctypes.CDLL(path or PORTABLE)
+    L.qffb_openmp.restype = ctypes.c_int
+    L.qffb_deltanet_prefill.argtypes = [ctypes.c_int] + [_fp] * 8 + [ctypes.c_float] + [_fp] * 4 + [ctypes.c_int]
+    L.qffb_attention_decode.argtypes = [ctypes.c_int, _fp, _fp, _fp, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_float, _fp, ctypes.c_int]
+    return L
+
+
+def _f(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    return a.ctypes.data_as(_fp)
+
+
+def deltanet_prefill(L, qkv, z, a, b, prm, conv_state, ssm_state, threads=1, eps=1e-6):
+    """T tokens through the DeltaNet layer core (QwenDeltaNetKernel.swift
+    :39-151 token by token). Returns (out [T,4096], conv_state, ssm_state)."""
+    qkv = _f(qkv).reshape(-1, 8192)
+    T = qkv.shape[0]
+    z, a, b = _f(z).reshape(T, 4096), _f(a).reshape(T, 32), _f(b).reshape(T, 32)
+    pr = [_f(prm[k]) for k in ("a_log", "dt_bias", "conv_w", "norm_w")]
+    cs = _f(conv_state).reshape(8192, 4).copy()
+    ss = _f(ssm_state).reshape(32, 128, 128).copy()
+    out = np.empty((T, 4096), np.float32)
+    work = np.empty((T, 8192), np.float32)
+    L.qffb_deltanet_prefill(T, _p(qkv), _p(z), _p(a), _p(b), *[_p(x) for x in pr], eps, _p(cs), _p(ss),
+                            _p(out), _p(work), threads)
+    return out, cs, ss
+
+
+def attention_decode(L, q, K, V, lengths, scale=1.0 / 16, threads=1):
+    """Split-KV decode attention (attention.metal:134-224, 342-377) of B
+    sequences: q [B,16,256], K, V [B,max_ctx,2,256] fp32, lengths [B] ->
+    out [B,16,256]."""
+    q, K, V = _f(q), _f(K), _f(V)
+    B, max_ctx = K.shape[0], K.shape[1]
+    lens = np.ascontiguousarray(lengths, dtype=np.int32)
+    out = np.empty((B, 16, 256), np.float32)
+    L.qffb_attention_decode(B, _p(q), _p(K), _p(V), lens.ctypes.data, max_ctx, scale, _p(out), threads)
+    return out

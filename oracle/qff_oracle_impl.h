@@ -76,29 +76,33 @@ void SFX(qffo_l2norm)(const R* v, int d, R eps, R* out) {
  *      expanded to v-heads), state is [32][128 rows = v][128 cols = k].
  *      Per head: decay the whole state, then per row kv = S_r.k,
  *      delta = (v_r - kv) * beta, S_r += k * delta; then o_r = S_r.q. ---- */
+/* One value head of that step (LA:86-120 for one h): qh, kh, vh [128],
+ * a, b the head's gate inputs, S [128][128], out [128]. */
+void SFX(qffo_deltanet_head_step)(const R* qh, const R* kh, const R* vh, R a, R b,
+                                  R a_log, R dt_bias, R* S, R* out) {
+    R beta = SFX(sigmoid_)(b);
+    R g = EXP(-EXP(a_log) * SFX(softplus_)(a + dt_bias));
+    for (int i = 0; i < 128 * 128; ++i) S[i] *= g;
+    for (int r = 0; r < 128; ++r) {
+        R kv = 0;
+        for (int c = 0; c < 128; ++c) kv += S[r * 128 + c] * kh[c];
+        R delta = (vh[r] - kv) * beta;
+        for (int c = 0; c < 128; ++c) S[r * 128 + c] += kh[c] * delta;
+    }
+    for (int r = 0; r < 128; ++r) {
+        R o = 0;
+        for (int c = 0; c < 128; ++c) o += S[r * 128 + c] * qh[c];
+        out[r] = o;
+    }
+}
+
 void SFX(qffo_deltanet_recurrent_step)(const R* q, const R* k, const R* v,
                                        const R* a, const R* b, const R* a_log,
                                        const R* dt_bias, R* state, R* out) {
-    for (int h = 0; h < 32; ++h) {
-        R beta = SFX(sigmoid_)(b[h]);
-        R g = EXP(-EXP(a_log[h]) * SFX(softplus_)(a[h] + dt_bias[h]));
-        const R* qh = q + h * 128;
-        const R* kh = k + h * 128;
-        const R* vh = v + h * 128;
-        R* S = state + (size_t)h * 128 * 128;
-        for (int i = 0; i < 128 * 128; ++i) S[i] *= g;
-        for (int r = 0; r < 128; ++r) {
-            R kv = 0;
-            for (int c = 0; c < 128; ++c) kv += S[r * 128 + c] * kh[c];
-            R delta = (vh[r] - kv) * beta;
-            for (int c = 0; c < 128; ++c) S[r * 128 + c] += kh[c] * delta;
-        }
-        for (int r = 0; r < 128; ++r) {
-            R o = 0;
-            for (int c = 0; c < 128; ++c) o += S[r * 128 + c] * qh[c];
-            out[h * 128 + r] = o;
-        }
-    }
+    for (int h = 0; h < 32; ++h)
+        SFX(qffo_deltanet_head_step)(q + h * 128, k + h * 128, v + h * 128, a[h], b[h],
+                                     a_log[h], dt_bias[h], state + (size_t)h * 128 * 128,
+                                     out + h * 128);
 }
 
 /* ---- gated RMSNorm: LA:127-151. out = o * inv * w_r * silu(z) ---- */
@@ -200,18 +204,17 @@ void SFX(qffo_rope_partial)(R* x, const R* cos_t, const R* sin_t, int nheads,
  *      as real values (already rounded to the cache dtype) -> out [nq][hd]
  *      before the reference's final half() cast. num_chunks <= 0 selects
  *      the reference geometry; 1 gives the single-pass recurrence. ---- */
-void SFX(qffo_attention_decode)(const R* q, const R* K, const R* V, int L,
-                                int nq, int nkv, int hd, R scale, int num_chunks,
-                                R* out) {
+/* One q head of it (kv head kvh): qh [hd] -> out_h [hd]. */
+void SFX(qffo_attention_decode_head)(const R* qh, const R* K, const R* V, int L,
+                                     int nkv, int kvh, int hd, R scale, int num_chunks,
+                                     R* out_h) {
     int NC = num_chunks > 0 ? num_chunks : (L < 16 ? (L < 1 ? 1 : L) : 16);
     int chunk_len = ((L < 1 ? 1 : L) + NC - 1) / NC;
     R* m_p = (R*)malloc(sizeof(R) * NC);
     R* d_p = (R*)malloc(sizeof(R) * NC);
     R* o_p = (R*)malloc(sizeof(R) * NC * hd);
     R* o_l = (R*)malloc(sizeof(R) * hd);
-    for (int h = 0; h < nq; ++h) {
-        int kvh = h / (nq / nkv);
-        const R* qh = q + (size_t)h * hd;
+    {
         for (int c = 0; c < NC; ++c) {
             int p0 = c * chunk_len, p1 = p0 + chunk_len;
             if (p1 > L) p1 = L;
@@ -245,10 +248,18 @@ void SFX(qffo_attention_decode)(const R* q, const R* K, const R* V, int L,
         for (int i = 0; i < hd; ++i) {
             R acc = 0;
             for (int c = 0; c < NC; ++c) acc += o_p[(size_t)c * hd + i] * EXP(m_p[c] - mg);
-            out[(size_t)h * hd + i] = acc * inv_d;
+            out_h[i] = acc * inv_d;
         }
     }
     free(m_p); free(d_p); free(o_p); free(o_l);
+}
+
+void SFX(qffo_attention_decode)(const R* q, const R* K, const R* V, int L,
+                                int nq, int nkv, int hd, R scale, int num_chunks,
+                                R* out) {
+    for (int h = 0; h < nq; ++h)
+        SFX(qffo_attention_decode_head)(q + (size_t)h * hd, K, V, L, nkv, h / (nq / nkv), hd,
+                                        scale, num_chunks, out + (size_t)h * hd);
 }
 
 /* ---- Q4 affine matvec, factored order of the generic kernel DN:816-861:

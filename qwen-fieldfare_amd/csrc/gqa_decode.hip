@@ -17,12 +17,15 @@
 //            token also normalises/rotates k, appends k and v to the cache
 //            and keeps both in LDS for its own use. It then walks 16-position
 //            tiles with the next tile's K and V rows already in flight (two
-//            register stages): S^T = K Q^T with 8 MFMA 16x16x32
-//            (K rows straight from HBM, 16 B per lane), base-2 online softmax
+//            register stages): S^T = K Q^T with 16 MFMA 16x16x32
+//            (K rows straight from HBM, 16 B per lane; q as bf16 hi + lo,
+//            so the scores see ~16 bits of q, more than the reference's
+//            fp16 q), base-2 online softmax
 //            per head whose running max is raised only past 2^8 (so O is
 //            rarely rescaled), the V tile copied row-major into LDS and read
 //            back as MFMA B operands with the gfx950 transpose read
-//            (ds_read_b64_tr_b16), O += P V with 16 MFMA 16x16x16, and one
+//            (ds_read_b64_tr_b16), O += P V with 32 MFMA 16x16x16 (P as
+//            bf16 hi + lo), and one
 //            (m, d, o[8][256]) partial per chunk (m in base-2 units).
 //   combine  grid (q head, sequence): merges the chunk partials and applies
 //            out = attn * sigmoid(gate).
@@ -44,7 +47,8 @@ struct DecTile {
 
 // Wave-local LDS of one partial unit.
 struct DecLds {
-    uint16_t qs[8][256];                      // normed, rotated, scaled q (bf16)
+    uint16_t qs[8][256];                      // normed, rotated, scaled q: bf16 hi part
+    uint16_t ql[8][256];                      // ... and lo part (q = hi + lo to ~2^-16)
     uint16_t vs[kDecTile * kVRowStride];      // the current V tile, row-major
     uint16_t knew[256], vnew[256];            // the new token's k, v
     float2 rcs[32];                           // (cos, sin) of pos * f[i]
@@ -64,14 +68,14 @@ __device__ __forceinline__ void wave_lds_sync() {
 // kv head kvh, run by one wave on its own LDS. The wave normalises and
 // rotates the 8 q heads; if the chunk holds the new token it also
 // normalises / rotates k, appends k and v to the cache and keeps both in
-// LDS for its own use. It then walks 16-position tiles: S^T = K Q^T with 8
-// MFMA 16x16x32 (K rows straight from HBM, 16 B per lane), base-2 online
-// softmax per head whose running max is raised only past 2^8 (so O is
-// rarely rescaled), the V tile copied row-major into LDS and read back as
-// MFMA B operands with the gfx950 transpose read (ds_read_b64_tr_b16),
-// O += P V with 16 MFMA 16x16x16, and writes one (m, d, o[8][256]) partial
-// (m in base-2 units). The next tile's loads are in flight while a tile
-// computes (two register stages).
+// LDS for its own use. It then walks 16-position tiles: S^T = K Q^T with 16
+// MFMA 16x16x32 (K rows straight from HBM, 16 B per lane; q as bf16 hi +
+// lo), base-2 online softmax per head whose running max is raised only past
+// 2^8 (so O is rarely rescaled), the V tile copied row-major into LDS and
+// read back as MFMA B operands with the gfx950 transpose read
+// (ds_read_b64_tr_b16), O += P V with 32 MFMA 16x16x16 (P as bf16 hi + lo),
+// and writes one (m, d, o[8][256]) partial (m in base-2 units). The next
+// tile's loads are in flight while a tile computes (two register stages).
 template <int IN_DT>
 __device__ __forceinline__ void gqa_partial_unit(
     DecLds& L, int seq, int kvh, int c, int pos, int lane, const void* __restrict__ q_gate,
@@ -158,8 +162,12 @@ __device__ __forceinline__ void gqa_partial_unit(
         }
         const float qscale = scale * 1.44269504088896341f;
 #pragma unroll
-        for (int i = 0; i < 8; i += 2)
-            *reinterpret_cast<uint32_t*>(&L.qs[hl][8 * j + i]) = pack_bf16x2(x[i] * qscale, x[i + 1] * qscale);
+        for (int i = 0; i < 8; i += 2) {
+            uint32_t hi, lo;
+            split_bf16x2(x[i] * qscale, x[i + 1] * qscale, hi, lo);
+            *reinterpret_cast<uint32_t*>(&L.qs[hl][8 * j + i]) = hi;
+            *reinterpret_cast<uint32_t*>(&L.ql[hl][8 * j + i]) = lo;
+        }
     }
     // ---- the new token (only the unit whose chunk holds it): k norm + RoPE,
     // append k and v to the cache (deltanet.metal:670-689), keep both in LDS
@@ -200,6 +208,7 @@ __device__ __forceinline__ void gqa_partial_unit(
     // q^T (B of 16x16x32): col = head n (< 8 real), k = dims 32jj + 8kb .. +7,
     // read from LDS per tile (registers are kept for the two tile stages)
     const uint16_t* qrow = &L.qs[n & 7][8 * kb];
+    const uint16_t* qrow_lo = &L.ql[n & 7][8 * kb];
     uint16_t* vsw = L.vs;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
 
@@ -219,13 +228,17 @@ __device__ __forceinline__ void gqa_partial_unit(
                 tl.k[jj] = kv;
             }
         }
-        // S^T = K Q^T
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // S^T = K Q^T, q as hi + lo (K is exact in bf16): the scores carry
+        // ~16 significant bits of q, finer than the reference's fp16 q
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f}, s_lo = s;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
             const u32x4_t qv = n < 8 ? *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj) : u32x4_t{0u, 0u, 0u, 0u};
+            const u32x4_t qvl = n < 8 ? *reinterpret_cast<const u32x4_t*>(qrow_lo + 32 * jj) : u32x4_t{0u, 0u, 0u, 0u};
             s = mfma_16x16x32_bf16(tl.k[jj], qv, s);
+            s_lo = mfma_16x16x32_bf16(tl.k[jj], qvl, s_lo);
         }
+        s += s_lo;
         // V tile row-major into LDS (the new token's row from LDS as well)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -265,15 +278,23 @@ __device__ __forceinline__ void gqa_partial_unit(
             pe[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
             d_run += pe[i];
         }
-        // A of O += P V (16x16x16): row = head n, k = positions 4kb .. +3
-        const u32x2_t pa = u32x2_t{pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])};
+        // A of O += P V (16x16x16): row = head n, k = positions 4kb .. +3,
+        // P as bf16 hi + lo (V is exact in bf16)
+        uint32_t ph0, pl0, ph1, pl1;
+        split_bf16x2(pe[0], pe[1], ph0, pl0);
+        split_bf16x2(pe[2], pe[3], ph1, pl1);
+        const u32x2_t pa = u32x2_t{ph0, ph1}, pl = u32x2_t{pl0, pl1};
         // B = V^T block straight from the row-major tile with a transpose read:
         // source lane (group kb, s = n) points at row 4kb + n/4, dims
         // 16jd + 4(n%4) .. +3, and receives V[4kb + k][16jd + n], k = 0..3.
         wave_lds_sync();
         const uint16_t* vsrc = &vsw[(4 * kb + (n >> 2)) * kVRowStride + 4 * (n & 3)];
 #pragma unroll
-        for (int jd = 0; jd < 16; ++jd) oacc[jd] = mfma_16x16x16_bf16(pa, lds_read_tr16(vsrc + 16 * jd), oacc[jd]);
+        for (int jd = 0; jd < 16; ++jd) {
+            const u32x2_t vb = lds_read_tr16(vsrc + 16 * jd);
+            oacc[jd] = mfma_16x16x16_bf16(pa, vb, oacc[jd]);
+            oacc[jd] = mfma_16x16x16_bf16(pl, vb, oacc[jd]);
+        }
         wave_lds_sync();
     };
     int p0 = p_start;
@@ -436,8 +457,18 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              qff_dtype in_dtype, void* k_cache, void* v_cache,
                              const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                              int max_ctx) {
-    const int cap = gqa_chunk_cap(ctx->cfg, batch);
-    const int ch = gqa_chunk_len(max_ctx, batch, cap, ctx->num_cu);
+    const GqaPartials ws{ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, gqa_chunk_cap(ctx->cfg, batch), ctx->num_cu};
+    return launch_gqa_decode_into(ctx, ws, stream, p, q_gate, k_new, v_new, in_dtype, k_cache, v_cache, positions,
+                                  out, out_dtype, batch, max_ctx);
+}
+
+hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream_t stream,
+                                  const qff_gqa_params* p, const void* q_gate, const void* k_new,
+                                  const void* v_new, qff_dtype in_dtype, void* k_cache, void* v_cache,
+                                  const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
+                                  int max_ctx) {
+    const int cap = ws.cap;
+    const int ch = gqa_chunk_len(max_ctx, batch, cap, ws.num_cu);
     const int nc = (max_ctx + ch - 1) / ch;
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
@@ -447,7 +478,7 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
 #define QFF_PART(I)                                                                                            \
     gqa_decode_partial_kernel<I><<<dim3(2 * nc, 1, batch), 64, 0, stream>>>(                                   \
         q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
-        ctx->gqa_m, ctx->gqa_d, ctx->gqa_o)
+        ws.m, ws.d, ws.o)
         if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
 #undef QFF_PART
     }
@@ -458,10 +489,10 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
 #define QFF_COMB(I, O)                                                                                      \
     if (ds == 4)                                                                                            \
         gqa_decode_combine_kernel<I, O, 4><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
-                                                                      ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out); \
+                                                                      ws.m, ws.d, ws.o, out);               \
     else                                                                                                    \
         gqa_decode_combine_kernel<I, O, 1><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
-                                                                      ctx->gqa_m, ctx->gqa_d, ctx->gqa_o, out)
+                                                                      ws.m, ws.d, ws.o, out)
     if (in_dtype == QFF_BF16) {
         if (out_dtype == QFF_BF16) { QFF_COMB(1, 1); } else { QFF_COMB(1, 0); }
     } else {

@@ -6,19 +6,25 @@
 // 1076-1150), so token t attends to positions 0 .. start+t. This file
 // computes all T rows at once:
 //   prep   one wave per token: head RMSNorm + partial RoPE of the
-//          16 q heads (bf16, softmax scale folded in, to workspace) and of
-//          the 2 k heads (appended to the bf16 cache together with v).
+//          16 q heads (fp16, softmax scale folded in, to workspace: the
+//          reference also rounds q to half, Runner:1119-1126) and of the 2 k
+//          heads (appended to the bf16 cache together with v).
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; eight waves of 16 rows = 2 tokens x 8
 //          heads, so accumulators and q stay in VGPRs and two waves share
 //          each SIMD) and walks 64-position K/V tiles staged in LDS
 //          row-major (double-buffered; the next tile's global loads are in
-//          flight while the current one computes). S^T = K Q^T on 16x16x32
-//          bf16 MFMAs; softmax in
+//          flight while the current one computes), converted from the bf16
+//          cache to fp16 as they are staged (exact for the cache's values),
+//          so both products run on fp16 operands: S^T = K Q^T on 16x16x32
+//          fp16 MFMAs (q keeps the 11-bit significand the reference gives
+//          it, where bf16 q puts rare outputs beyond the output tolerance
+//          once logits reach ~15); softmax in
 //          base 2 (q carries scale * log2 e), with the running max raised
 //          only when a tile exceeds it by more than 2^8, so the O rescale is
 //          rare; causal masking only on the tiles that reach past the
-//          block's first token. O += P V with 16x16x32 MFMAs whose 32-deep k
+//          block's first token. O += P V with 16x16x32 fp16 MFMAs (P in
+//          fp16, 8x finer than bf16) whose 32-deep k
 //          runs over the tile's positions in the order the S^T registers
 //          hold them; the V operand comes from the row-major tile through the
 //          LDS transpose read. Query blocks are issued last-first so the
@@ -32,7 +38,7 @@ namespace qff {
 
 constexpr int kPfQB = 16;       // query tokens per workgroup
 constexpr int kPfKT = 64;       // K/V positions per tile
-constexpr int kKStride = 264;   // bf16 per K row in LDS: 256 + 8 pad (528 B)
+constexpr int kKStride = 264;   // fp16 per K row in LDS: 256 + 8 pad (528 B)
 
 // One wave per token, 8 per workgroup: the token's 32 RoPE angles are
 // evaluated once (lane i < 32: cos, sin of pos * f[i]) and shuffled to the
@@ -112,7 +118,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
             }
             if (is_q) {
                 *reinterpret_cast<u32x2_t*>(qb + (static_cast<size_t>(tok) * 16 + hs) * 256 + 4 * lane) =
-                    u32x2_t{pack_bf16x2(y[0] * qs, y[1] * qs), pack_bf16x2(y[2] * qs, y[3] * qs)};
+                    u32x2_t{pack_f16x2(y[0] * qs, y[1] * qs), pack_f16x2(y[2] * qs, y[3] * qs)};
             } else {
                 const int kvh = hs - 16;
                 const size_t off = (static_cast<size_t>(pos) * 2 + kvh) * 256 + 4 * lane;
@@ -150,14 +156,15 @@ __device__ __forceinline__ void tile_load(TileRegs& r, const uint16_t* __restric
     }
 }
 
+// ... and stores them to LDS as fp16.
 __device__ __forceinline__ void tile_store(const TileRegs& r, uint16_t* __restrict__ ks, uint16_t* __restrict__ vs,
                                            int t) {
 #pragma unroll
     for (int i = 0; i < kPfPieces; ++i) {
         const int q = t + kPfThreads * i;
         const int o = (q >> 5) * kKStride + 8 * (q & 31);
-        *reinterpret_cast<u32x4_t*>(ks + o) = r.k[i];
-        *reinterpret_cast<u32x4_t*>(vs + o) = r.v[i];
+        *reinterpret_cast<u32x4_t*>(ks + o) = bf16x8_to_f16x8(r.k[i]);
+        *reinterpret_cast<u32x4_t*>(vs + o) = bf16x8_to_f16x8(r.v[i]);
     }
 }
 
@@ -229,7 +236,7 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                         &Ks[cur][(16 * pt + n) * kKStride + 32 * (jj + 1) + 8 * kb]);
             }
 #pragma unroll
-            for (int pt = 0; pt < NPT; ++pt) s[pt] = mfma_16x16x32_bf16(ka[jj & 1][pt], qreg[jj], s[pt]);
+            for (int pt = 0; pt < NPT; ++pt) s[pt] = mfma_16x16x32_f16(ka[jj & 1][pt], qreg[jj], s[pt]);
         }
         // softmax (base 2); lane holds q row n, positions p0 + 16pt + 4kb + i
         float tmax = -INFINITY;
@@ -269,8 +276,8 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                     pe[h][i] = __builtin_amdgcn_exp2f(s[2 * c + h][i] - m_run);
                     d_run += pe[h][i];
                 }
-            pa[c] = u32x4_t{pack_bf16x2(pe[0][0], pe[0][1]), pack_bf16x2(pe[0][2], pe[0][3]),
-                            pack_bf16x2(pe[1][0], pe[1][1]), pack_bf16x2(pe[1][2], pe[1][3])};
+            pa[c] = u32x4_t{pack_f16x2(pe[0][0], pe[0][1]), pack_f16x2(pe[0][2], pe[0][3]),
+                            pack_f16x2(pe[1][0], pe[1][1]), pack_f16x2(pe[1][2], pe[1][3])};
         }
         // O += P V; B operand through the LDS transpose read: lane s of group
         // kb points at position 32c + 16h + 4kb + s/4, dims 16jd + 4(s%4)
@@ -288,7 +295,7 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
 #pragma unroll
                 for (int jd = 0; jd < 8; ++jd)
                     oacc[j0 + jd] =
-                        mfma_16x16x32_bf16(pa[c], u32x4_t{v0[jd][0], v0[jd][1], v1[jd][0], v1[jd][1]}, oacc[j0 + jd]);
+                        mfma_16x16x32_f16(pa[c], u32x4_t{v0[jd][0], v0[jd][1], v1[jd][0], v1[jd][1]}, oacc[j0 + jd]);
             }
         if (more) tile_store(regs, Ks[cur ^ 1], Vs[cur ^ 1], t);
         __syncthreads();
@@ -319,7 +326,7 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
                               const void* q_gate, const void* k, const void* v, qff_dtype in_dtype,
                               void* k_cache, void* v_cache, int start_pos, void* out,
                               qff_dtype out_dtype, int T, int) {
-    // the bf16 q rows [T][16][256] reuse the DeltaNet prefill staging buffer
+    // the fp16 q rows [T][16][256] (workspace)
     uint16_t* qb = ctx->gqa_qb;
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
     uint16_t* vc = static_cast<uint16_t*>(v_cache);

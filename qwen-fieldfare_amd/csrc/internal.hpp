@@ -125,6 +125,22 @@ hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_par
                              qff_dtype in_dtype, void* k_cache, void* v_cache,
                              const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                              int max_ctx);
+// Split-KV partial slots (m, d [slots][8], o [slots][8][256] fp32) and the
+// chunk cap per (sequence, kv head) they allow for a call's batch.
+struct GqaPartials {
+    float* m;
+    float* d;
+    float* o;
+    int cap;
+    int num_cu;
+};
+// The decode kernels on caller-chosen partial slots; ctx only for profiling
+// (may be null).
+hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream_t stream,
+                                  const qff_gqa_params* p, const void* q_gate, const void* k_new,
+                                  const void* v_new, qff_dtype in_dtype, void* k_cache, void* v_cache,
+                                  const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
+                                  int max_ctx);
 hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
                               const void* q_gate, const void* k, const void* v, qff_dtype in_dtype,
                               void* k_cache, void* v_cache, int start_pos, void* out,

@@ -1,8 +1,8 @@
-// mfma.hpp -- CDNA4 matrix-core operand types and the two bf16 MFMA shapes
-// the attention kernels use.
+// mfma.hpp -- CDNA4 matrix-core operand types, the bf16 and fp16 MFMA
+// shapes the kernels use and the operand conversions around them.
 //
 // Register layouts (wave64, lane l):
-//   16x16x32 bf16: A[16 x 32]: lane l holds row l%16, k = 8*(l/16) .. +7
+//   16x16x32 bf16 / f16: A[16 x 32]: lane l holds row l%16, k = 8*(l/16) .. +7
 //                  B[32 x 16]: lane l holds col l%16, k = 8*(l/16) .. +7
 //   16x16x16 bf16: A[16 x 16]: lane l holds row l%16, k = 4*(l/16) .. +3
 //                  B[16 x 16]: lane l holds col l%16, k = 4*(l/16) .. +3
@@ -28,6 +28,33 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32_bf16(u32x4_t a, u32x4_t b, f32x
 __device__ __forceinline__ f32x4_t mfma_16x16x16_bf16(u32x2_t a, u32x2_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
                                                      __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4_t mfma_16x16x32_f16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Two floats -> packed fp16 pair, round to nearest even; the low half holds lo.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two packed bf16 -> two packed fp16. Exact for every bf16 value inside the
+// fp16 normal range (8 significant bits fit in 11); values below 2^-14 lose
+// low bits to fp16's subnormals and values of magnitude >= 65520 become
+// +-65504 (the reference keeps its KV cache in fp16 with the same limits).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ u32x4_t bf16x8_to_f16x8(u32x4_t v) {
+    return u32x4_t{bf16x2_to_f16x2(v[0]), bf16x2_to_f16x2(v[1]), bf16x2_to_f16x2(v[2]), bf16x2_to_f16x2(v[3])};
 }
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each group of 16

@@ -139,6 +139,7 @@ template <int SB_DT, int X_DT, int NBT, int RT, bool NORM, int GPW>
 __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts parts, const void* __restrict__ x,
                                                                        int cols, int batch, Q4Norm nrm) {
     constexpr int RW = 16 * RT;                     // rows per workgroup
+    constexpr bool HILO = X_DT == 0 || NORM;        // x is not exactly bf16: hi + lo operands
     // per thread at most PPT weight pieces and SBT scale/bias entries:
     // RW * (cols / 32) / (64 nw) <= RW GPW / 32 with nw = ceil(G / GPW)
     constexpr int PPT = RW * GPW / 32, SBT = (RW * GPW + 63) / 64;
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
             *reinterpret_cast<float4*>(&wnl[8 * c8 + 4]) = make_float4(w8[4], w8[5], w8[6], w8[7]);
         }
     }
-    auto load_x = [&](int i, u32x4_t (&xo2)[NBT][2]) {
+    auto load_x = [&](int i, u32x4_t (&xo2)[NBT][2], u32x4_t (&xl2)[NBT][2]) {
         const int g = min(g0 + i, G - 1);
         float wn[16];
         if (NORM) {
@@ -250,20 +251,29 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
                 ssq[bt] += i < gn ? s2 : 0.0f;
 #pragma unroll
                 for (int q = 0; q < 2; ++q)
-                    xo2[bt][q] = u32x4_t{pack_bf16x2(v[8 * q] * wn[8 * q], v[8 * q + 1] * wn[8 * q + 1]),
-                                         pack_bf16x2(v[8 * q + 2] * wn[8 * q + 2], v[8 * q + 3] * wn[8 * q + 3]),
-                                         pack_bf16x2(v[8 * q + 4] * wn[8 * q + 4], v[8 * q + 5] * wn[8 * q + 5]),
-                                         pack_bf16x2(v[8 * q + 6] * wn[8 * q + 6], v[8 * q + 7] * wn[8 * q + 7])};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        uint32_t hh, ll;
+                        split_bf16x2(v[8 * q + 2 * e] * wn[8 * q + 2 * e], v[8 * q + 2 * e + 1] * wn[8 * q + 2 * e + 1],
+                                     hh, ll);
+                        xo2[bt][q][e] = hh;
+                        xl2[bt][q][e] = ll;
+                    }
             } else if (X_DT == 1) {
                 xo2[bt][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
                 xo2[bt][1] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8);
             } else {
                 const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo);
                 const float4 e0 = q[0], e1 = q[1], e2 = q[2], e3 = q[3];
-                xo2[bt][0] = u32x4_t{pack_bf16x2(e0.x, e0.y), pack_bf16x2(e0.z, e0.w),
-                                     pack_bf16x2(e1.x, e1.y), pack_bf16x2(e1.z, e1.w)};
-                xo2[bt][1] = u32x4_t{pack_bf16x2(e2.x, e2.y), pack_bf16x2(e2.z, e2.w),
-                                     pack_bf16x2(e3.x, e3.y), pack_bf16x2(e3.z, e3.w)};
+                const float f[16] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w,
+                                     e2.x, e2.y, e2.z, e2.w, e3.x, e3.y, e3.z, e3.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    uint32_t hh, ll;
+                    split_bf16x2(f[2 * e], f[2 * e + 1], hh, ll);
+                    xo2[bt][e >> 2][e & 3] = hh;
+                    xl2[bt][e >> 2][e & 3] = ll;
+                }
             }
         }
     };
@@ -271,8 +281,9 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     constexpr int kXPre = kPre ? GPW : 1;
     u32x4_t xv[kXPre][NBT][2];
     if (kPre) {
+        u32x4_t unused[NBT][2];
 #pragma unroll
-        for (int i = 0; i < kXPre; ++i) load_x(i, xv[i]);
+        for (int i = 0; i < kXPre; ++i) load_x(i, xv[i], unused);
     }
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
@@ -310,9 +321,10 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
         const int g = min(g0 + i, G - 1);
         const float keep = i < gn ? 1.0f : 0.0f;
         float xsum[NBT];
-        u32x4_t xi[NBT][2];
+        u32x4_t xi[NBT][2], xil[NBT][2];
         u32x4_t (&xg)[NBT][2] = xv[kPre ? i : 0];
-        if (!kPre) load_x(i, xg);
+        u32x4_t xgl[NBT][2];
+        if (!kPre) load_x(i, xg, xgl);
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
             const u32x4_t x0 = xg[bt][0], x1 = xg[bt][1];
@@ -321,6 +333,15 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
             for (int j = 0; j < 4; ++j)
                 sx += (__uint_as_float(x0[j] << 16) + __uint_as_float(x0[j] & 0xffff0000u)) +
                       (__uint_as_float(x1[j] << 16) + __uint_as_float(x1[j] & 0xffff0000u));
+            if (HILO) {
+                const u32x4_t l0 = xgl[bt][0], l1 = xgl[bt][1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    sx += (__uint_as_float(l0[j] << 16) + __uint_as_float(l0[j] & 0xffff0000u)) +
+                          (__uint_as_float(l1[j] << 16) + __uint_as_float(l1[j] & 0xffff0000u));
+                xil[bt][0] = interleave8(l0);
+                xil[bt][1] = interleave8(l1);
+            }
             sx += __shfl_xor(sx, 16, 64);
             sx += __shfl_xor(sx, 32, 64);
             xsum[bt] = sx;
@@ -344,6 +365,10 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
                 f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
                 P = mfma_16x16x32_bf16(a0, xi[bt][0], P);
                 P = mfma_16x16x32_bf16(a1, xi[bt][1], P);
+                if (HILO) {
+                    P = mfma_16x16x32_bf16(a0, xil[bt][0], P);
+                    P = mfma_16x16x32_bf16(a1, xil[bt][1], P);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[rt][bt][j] = fmaf(svb[j].x, P[j], fmaf(svb[j].y, xsum[bt], acc[rt][bt][j]));
@@ -394,9 +419,14 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
 // one 16-B load per lane per 2048 columns (lane l takes the 32-column piece
 // l of each 2048), all rows' loads in flight from the first instruction.
 // Meanwhile the workgroup prepares x once for its four waves: each thread
-// converts 8 columns to bf16 (with NORM: bf16(x w_norm), plus its share of
-// sum x^2), stores them in LDS in the pair order of the nibble conversion
-// below, and the 32-column piece sums; one barrier. Products run on the
+// converts 8 columns to bf16 (with NORM: x w_norm, plus its share of sum
+// x^2), stores them in LDS in the pair order of the nibble conversion
+// below, and the 32-column piece sums; one barrier. Values that are not
+// exactly bf16 (fp32 x, and every normed x) go in as a bf16 hi + lo pair
+// with x = hi + lo to ~2^-16, each taken by its own dot2 pass over the same
+// nibbles, and the piece sums add hi + lo, so the product keeps fp32-class
+// activations as the reference's fp32 row kernels do (deltanet.metal
+// :1838-1895). Products run on the
 // vector units: the nibbles of a word become four bf16 pairs 128 + q with
 // one shift and one and-or each (pair h = columns h and h + 4 of the word),
 // and v_dot2_f32_bf16 takes a pair of them against the matching pair of x,
@@ -418,6 +448,7 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 template <int SB_DT, int X_DT, int KW, bool NORM>
 __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts parts, const void* __restrict__ x,
                                                                     int cols, Q4Norm nrm) {
+    constexpr bool HILO = X_DT == 0 || NORM;   // x is not exactly bf16: hi + lo
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     int p = 0;
 #pragma unroll
@@ -471,6 +502,7 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
     // x once per workgroup: slice i -> xl[i] as the four bf16 pairs
     // (x0 x4, x1 x5, x2 x6, x3 x7); xsl[i / 4] = its 32-column piece's sum
     __shared__ u32x4_t xl[64 * KW * 4];
+    __shared__ u32x4_t xll[HILO ? 64 * KW * 4 : 1];
     __shared__ float xsl[64 * KW];
     __shared__ float ssl[kQ4VecWaves];
     float ss = 0.0f;
@@ -487,16 +519,29 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
                 v[k][e] *= wn[k][e];
             }
         }
-        u32x4_t xb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xb[e] = pack_bf16x2(v[k][e], v[k][e + 4]);   // exact for bf16 x, no norm
+        u32x4_t xb, xlb;
         float sum = 0.0f;
+        if (HILO) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum += __uint_as_float(xb[e] << 16) + __uint_as_float(xb[e] & 0xffff0000u);
+            for (int e = 0; e < 4; ++e) {
+                uint32_t hh, ll;
+                split_bf16x2(v[k][e], v[k][e + 4], hh, ll);
+                xb[e] = hh;
+                xlb[e] = ll;
+                sum += (__uint_as_float(hh << 16) + __uint_as_float(ll << 16)) +
+                       (__uint_as_float(hh & 0xffff0000u) + __uint_as_float(ll & 0xffff0000u));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xb[e] = pack_bf16x2(v[k][e], v[k][e + 4]);   // exact: bf16 x, no norm
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum += __uint_as_float(xb[e] << 16) + __uint_as_float(xb[e] & 0xffff0000u);
+        }
         sum += __shfl_xor(sum, 1, 64);
         sum += __shfl_xor(sum, 2, 64);
         if (live) {
             xl[i] = xb;
+            if (HILO) xll[i] = xlb;
             if ((i & 3) == 0) xsl[i >> 2] = sum;
         }
     }
@@ -515,19 +560,27 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
         const int pc = lane + 64 * k;
         const bool live = pc < npc;
         const int pcc = min(pc, npc - 1);
-        u32x4_t xv[4];
+        u32x4_t xv[4], xw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[j] = xl[4 * pcc + j];
+        for (int j = 0; j < 4; ++j) {
+            xv[j] = xl[4 * pcc + j];
+            if (HILO) xw[j] = xll[4 * pcc + j];
+        }
         const float xs = live ? xsl[pcc] : 0.0f;
 #pragma unroll
         for (int r = 0; r < kQ4VecRows; ++r) {
-            float dq = 0.0f;
+            float dq = 0.0f, dl = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t wd = wq[r][k][j];
 #pragma unroll
-                for (int h = 0; h < 4; ++h) dq = dot2_bf16(((wd >> (4 * h)) & 0x000F000Fu) | 0x43004300u, xv[j][h], dq);
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t wp = ((wd >> (4 * h)) & 0x000F000Fu) | 0x43004300u;
+                    dq = dot2_bf16(wp, xv[j][h], dq);
+                    if (HILO) dl = dot2_bf16(wp, xw[j][h], dl);
+                }
             }
+            if (HILO) dq += dl;
             // pieces past the row end (cols < 2048) hold a copy: weight zero
             const float sk = live ? sv[r][k] : 0.0f, bk = live ? bv[r][k] : 0.0f;
             part[r] = fmaf(sk, dq, fmaf(fmaf(-128.0f, sk, bk), xs, part[r]));

@@ -176,14 +176,27 @@ def _dn_params(p: dict, eps: float):
     return DeltaNetParams(_ptr(p["a_log"]), _ptr(p["dt_bias"]), _ptr(p["conv_w"]), _ptr(p["norm_w"]), eps)
 
 
+def _check_dn_inputs(qkv, z, a, b, conv_state, ssm_state, n, seqs):
+    """n tokens of `seqs` sequences: the shapes and element types the
+    library assumes, checked before any pointer reaches it."""
+    if z.dtype != qkv.dtype:
+        raise TypeError("qkv and z must share a dtype")
+    for name, t in (("a", a), ("b", b), ("conv_state", conv_state), ("ssm_state", ssm_state)):
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32")
+    if qkv.numel() != n * 8192 or z.numel() != n * 4096 or a.numel() != n * 32 or b.numel() != n * 32:
+        raise ValueError("qkv, z, a, b must be [n, 8192], [n, 4096], [n, 32], [n, 32]")
+    if conv_state.numel() != seqs * 8192 * 4 or ssm_state.numel() != seqs * 32 * 128 * 128:
+        raise ValueError("conv_state / ssm_state must hold [8192, 4] / [32, 128, 128] per sequence")
+
+
 def deltanet_decode(ctx: Context, params: dict, qkv, z, a, b, conv_state, ssm_state, out=None,
                     out_dtype=torch.bfloat16, eps: float = 1e-6) -> torch.Tensor:
     """One decode step for batch B. qkv [B,8192], z [B,4096] (same dtype), a, b
     [B,32] f32, conv_state [B,8192,4] f32, ssm_state [B,32,128,128] f32 (both
     updated in place) -> out [B,4096]."""
     B = qkv.shape[0]
-    if z.dtype != qkv.dtype:
-        raise TypeError("qkv and z must share a dtype")
+    _check_dn_inputs(qkv, z, a, b, conv_state, ssm_state, B, B)
     if out is None:
         out = torch.empty(B, 4096, dtype=out_dtype, device=qkv.device)
     prm = _dn_params(params, eps)
@@ -198,6 +211,7 @@ def deltanet_prefill(ctx: Context, params: dict, qkv, z, a, b, conv_state, ssm_s
     """T tokens of one sequence. qkv [T,8192], z [T,4096], a, b [T,32];
     conv_state [8192,4], ssm_state [32,128,128] updated in place -> out [T,4096]."""
     T = qkv.shape[0]
+    _check_dn_inputs(qkv, z, a, b, conv_state, ssm_state, T, 1)
     if out is None:
         out = torch.empty(T, 4096, dtype=out_dtype, device=qkv.device)
     prm = _dn_params(params, eps)
@@ -205,6 +219,17 @@ def deltanet_prefill(ctx: Context, params: dict, qkv, z, a, b, conv_state, ssm_s
         ctx.handle, _stream(), ctypes.byref(prm), _ptr(qkv), _ptr(z), _code(qkv), _ptr(a), _ptr(b),
         _ptr(conv_state), _ptr(ssm_state), _ptr(out), _code(out), T, chunk))
     return out
+
+
+def _check_gqa_inputs(q_gate, k, v, k_cache, v_cache, n):
+    """The library reads q_gate, k and v with one element type and the
+    caches as bf16: reject anything else before it reaches the device."""
+    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("KV caches must be bfloat16")
+    if k.dtype != q_gate.dtype or v.dtype != q_gate.dtype:
+        raise TypeError("k and v must share q_gate's dtype")
+    if q_gate.numel() != n * 16 * 512 or k.numel() != n * 512 or v.numel() != n * 512:
+        raise ValueError("q_gate must be [n, 16, 512] and k, v [n, 2, 256]")
 
 
 def _gqa_params(p: dict, theta, scale, eps):
@@ -217,10 +242,11 @@ def gqa_decode(ctx: Context, params: dict, q_gate, k_new, v_new, k_cache, v_cach
     positions int32 [B] (device) -> out [B,16,256]."""
     B = q_gate.shape[0]
     max_ctx = k_cache.shape[1]
-    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise TypeError("KV caches must be bfloat16")
-    if positions.dtype != torch.int32:
-        raise TypeError("positions must be int32")
+    _check_gqa_inputs(q_gate, k_new, v_new, k_cache, v_cache, B)
+    if tuple(k_cache.shape) != (B, max_ctx, 2, 256) or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError("KV caches must be [B, max_ctx, 2, 256]")
+    if positions.dtype != torch.int32 or positions.numel() != B:
+        raise TypeError("positions must be int32 [B]")
     if out is None:
         out = torch.empty(B, 16, 256, dtype=out_dtype, device=q_gate.device)
     prm = _gqa_params(params, theta, scale, eps)
@@ -236,6 +262,9 @@ def gqa_prefill(ctx: Context, params: dict, q_gate, k, v, k_cache, v_cache, star
     """q_gate [T,16,512], k/v [T,2,256]; caches [max_ctx,2,256] bf16 -> out [T,16,256]."""
     T = q_gate.shape[0]
     max_ctx = k_cache.shape[0]
+    _check_gqa_inputs(q_gate, k, v, k_cache, v_cache, T)
+    if tuple(k_cache.shape) != (max_ctx, 2, 256) or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError("KV caches must be [max_ctx, 2, 256]")
     if out is None:
         out = torch.empty(T, 16, 256, dtype=out_dtype, device=q_gate.device)
     prm = _gqa_params(params, theta, scale, eps)

@@ -155,3 +155,75 @@ def test_deltanet_rejects_bad_arguments(hip):
                              torch.zeros(17, 32, device=DEV), torch.zeros(17, 32, device=DEV),
                              conv[0], ssm[0])
     assert e.value.status == -4
+
+
+@pytest.mark.parametrize("B,T", [(1, 4096), (6, 1024)])
+def test_deltanet_decode_consecutive_steps(hip, B, T):
+    """qff_deltanet_decode, the reference's per-token path
+    (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561 -> deltanet.metal
+    :250-356), T steps in a row on the config-1 inputs from zero state (batch
+    1: 4096 steps, the two-launch small-batch kernels; batch 6: 1024 steps
+    of six independent sequences, the one-launch kernel), against the
+    sequential fp32 oracle: every step's output within the bf16 bar and the
+    state rel <= 1e-4 at the end."""
+    import qff
+    print(f"deltanet_decode {T} consecutive steps B={B} (oracle running)", flush=True)
+    p = synth.deltanet_params()
+    seqs = [synth.deltanet_prefill_inputs(T, seed=900 + s) for s in range(B)]
+    refs = [O.deltanet_sequence(O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"]), inp["a"], inp["b"],
+                                p["a_log"], p["dt_bias"], p["conv_w"], p["norm_w"], inp["conv_state"],
+                                inp["ssm_state"]) for inp in seqs]
+    # token-major across the batch: step t feeds row t of every sequence
+    qkv = bf16_tensor(np.stack([s["qkv"] for s in seqs], 1))       # [T, B, 8192]
+    z = bf16_tensor(np.stack([s["z"] for s in seqs], 1))
+    a = f32_tensor(np.stack([s["a"] for s in seqs], 1))
+    b = f32_tensor(np.stack([s["b"] for s in seqs], 1))
+    ctx = qff.Context(max_batch=8, max_prefill_tokens=1)
+    conv = torch.zeros(B, 8192, 4, device=DEV)
+    ssm = torch.zeros(B, 32, 128, 128, device=DEV)
+    out = torch.empty(T, B, 4096, dtype=torch.bfloat16, device=DEV)
+    pg = _params_gpu(p)
+    print("  GPU steps", flush=True)
+    for t in range(T):
+        qff.deltanet_decode(ctx, pg, qkv[t], z[t], a[t], b[t], conv, ssm, out=out[t])
+    torch.cuda.synchronize()
+    got = to_np(out)
+    for s in range(B):
+        ref_o, ref_c, ref_s = refs[s]
+        assert_bf16_output_close(got[:, s], ref_o)
+        assert np.array_equal(to_np(conv)[s], ref_c)
+        rel = state_rel_err(to_np(ssm)[s], ref_s)
+        print(f"  seq {s}: state rel {rel:.3g}", flush=True)
+        assert rel <= 1e-4
+
+
+@pytest.mark.parametrize("T", [70, 200])
+def test_deltanet_prefill_f32_inputs(hip, T):
+    """fp32 qkv / z (in_dtype F32) through the chunked prefill from a
+    non-zero state, fp32 and bf16 outputs, against the oracle fed the same
+    fp32 values."""
+    import qff
+    print(f"deltanet_prefill f32 inputs T={T}", flush=True)
+    p = synth.deltanet_params()
+    rng = np.random.default_rng(600 + T)
+    qkv = rng.standard_normal((T, 8192)).astype(np.float32)
+    z = rng.standard_normal((T, 4096)).astype(np.float32)
+    a = rng.standard_normal((T, 32)).astype(np.float32)
+    b = rng.standard_normal((T, 32)).astype(np.float32)
+    conv0 = np.zeros((8192, 4), np.float32)
+    conv0[:, 1:] = rng.standard_normal((8192, 3)).astype(np.float32)
+    ssm0 = (rng.standard_normal((32, 128, 128)) * 0.02).astype(np.float32)
+    ref_o, ref_c, ref_s = O.deltanet_sequence(qkv, z, a, b, p["a_log"], p["dt_bias"], p["conv_w"], p["norm_w"],
+                                              conv0, ssm0)
+    ctx = qff.Context(max_batch=1, max_prefill_tokens=256)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        conv, ssm = f32_tensor(conv0), f32_tensor(ssm0)
+        out = qff.deltanet_prefill(ctx, _params_gpu(p), f32_tensor(qkv), f32_tensor(z), f32_tensor(a),
+                                   f32_tensor(b), conv, ssm, out_dtype=out_dtype)
+        torch.cuda.synchronize()
+        if out_dtype == torch.float32:
+            assert_f32_output_close(to_np(out), ref_o)
+        else:
+            assert_bf16_output_close(to_np(out), ref_o)
+        assert np.array_equal(to_np(conv), ref_c)
+        assert state_rel_err(to_np(ssm), ref_s) <= 1e-4

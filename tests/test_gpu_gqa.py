@@ -249,3 +249,154 @@ def test_gqa_rejects_bad_calls(hip):
     with pytest.raises(qff.QffError) as e:       # batch above max_batch
         qff.gqa_decode(ctx, pg, qg, kn, kn, kc3, kc3.clone(), pos)
     assert e.value.status == -4
+
+
+def test_gqa_decode_f32_inputs(hip):
+    """fp32 q_gate / k_new / v_new (in_dtype F32) at random lengths, against
+    the oracle fed the same fp32 values."""
+    import qff
+    B, max_ctx = 5, 4096
+    print(f"gqa_decode f32 inputs B={B}", flush=True)
+    rng = np.random.default_rng(55)
+    p = synth.gqa_params()
+    inp = synth.gqa_decode_inputs(B, max_ctx, seed=55, lengths=[1, 700, 4096, 33, 2500])
+    qg = rng.standard_normal((B, 16, 512)).astype(np.float32)
+    kn = rng.standard_normal((B, 2, 256)).astype(np.float32)
+    vn = rng.standard_normal((B, 2, 256)).astype(np.float32)
+    ctx = qff.Context(max_batch=B, max_ctx=max_ctx, max_prefill_tokens=1)
+    kc, vc = bf16_tensor(inp["k_cache"]), bf16_tensor(inp["v_cache"])
+    out = qff.gqa_decode(ctx, {k: f32_tensor(v) for k, v in p.items()}, f32_tensor(qg), f32_tensor(kn),
+                         f32_tensor(vn), kc, vc, torch.from_numpy(inp["positions"]).to(DEV),
+                         out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    kc_g = kc.cpu().view(torch.int16).numpy().view(np.uint16)
+    for s in range(B):
+        pos = int(inp["positions"][s])
+        kref, vref = inp["k_cache"][s].copy(), inp["v_cache"][s].copy()
+        O.gqa_append_kv_seq(kn[s][None], vn[s][None], p["k_norm_w"], kref, vref, O.BF16, start_pos=pos)
+        ref = O.gqa_attend(qg[s], p["q_norm_w"], kref, vref, O.BF16, pos)
+        assert_f32_output_close(got[s], ref)
+        kr = O.bf16_to_f32(kref[pos])
+        assert np.all(np.abs(O.bf16_to_f32(kc_g[s][pos]) - kr) <= np.maximum(bf16_ulp(kr), 2.0 ** -16))
+
+
+@pytest.mark.parametrize("T,start", [(100, 37), (300, 0)])
+def test_gqa_prefill_f32_inputs(hip, T, start):
+    """fp32 q_gate / k / v through the causal prefill, every row against the
+    token-by-token oracle fed the same fp32 values."""
+    import qff
+    print(f"gqa_prefill f32 inputs T={T} start={start}", flush=True)
+    max_ctx = 1024
+    rng = np.random.default_rng(70 + T)
+    p = synth.gqa_params()
+    qg = rng.standard_normal((T, 16, 512)).astype(np.float32)
+    kk = rng.standard_normal((T, 2, 256)).astype(np.float32)
+    vv = rng.standard_normal((T, 2, 256)).astype(np.float32)
+    kc0 = O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32))
+    vc0 = O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32))
+    ctx = qff.Context(max_batch=1, max_ctx=max_ctx, max_prefill_tokens=T)
+    kc, vc = bf16_tensor(kc0), bf16_tensor(vc0)
+    out = qff.gqa_prefill(ctx, {k: f32_tensor(v) for k, v in p.items()}, f32_tensor(qg), f32_tensor(kk),
+                          f32_tensor(vv), kc, vc, start_pos=start, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    kref, vref = kc0.copy(), vc0.copy()
+    O.gqa_append_kv_seq(kk, vv, p["k_norm_w"], kref, vref, O.BF16, start_pos=start)
+    assert np.array_equal(vc.cpu().view(torch.int16).numpy().view(np.uint16), vref)
+    for t in range(T):
+        ref = O.gqa_attend(qg[t], p["q_norm_w"], kref, vref, O.BF16, start + t)
+        assert_bf16_output_close(got[t], ref)
+
+
+def _attend_all_rows_torch(qg, kref, vref, q_norm_w, T, theta=1e7, scale=1.0 / 16, eps=1e-6):
+    """Every output row of a causal prefill from position 0 in the oracle's
+    arithmetic (gqa_attend: per-head RMSNorm of q, RoPE on dims 0..63 with
+    host fp32 inverse frequencies, q rounded to fp16, fp32 softmax over
+    positions 0..t, output rounded to fp16, times sigmoid(gate)), vectorised
+    on the GPU in fp32. qg [T, 16, 512] f32; kref, vref [T, 2, 256] bf16 bits
+    (the cache after the append). Pinned against the oracle's gqa_attend on
+    sampled rows by the caller."""
+    dev = DEV
+    q = torch.from_numpy(qg[:, :, :256].copy()).to(dev)
+    gate = torch.from_numpy(qg[:, :, 256:].copy()).to(dev)
+    w = torch.from_numpy(q_norm_w.astype(np.float32)).to(dev)
+    q = q * torch.rsqrt((q * q).mean(-1, keepdim=True) + eps) * w
+    inv = torch.from_numpy(np.array([np.float32(1.0) / np.power(np.float32(theta), np.float32(2 * i) / np.float32(64))
+                                     for i in range(32)], np.float32)).to(dev)
+    ang = torch.arange(T, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+    c, s = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+    x0, x1 = q[:, :, :32].clone(), q[:, :, 32:64].clone()
+    q[:, :, :32] = x0 * c - x1 * s
+    q[:, :, 32:64] = x1 * c + x0 * s
+    q = q.half().float()
+    K = torch.from_numpy(O.bf16_to_f32(kref[:T])).to(dev)
+    V = torch.from_numpy(O.bf16_to_f32(vref[:T])).to(dev)
+    out = torch.empty(T, 16, 256, device=dev)
+    mask = torch.triu(torch.ones(T, T, dtype=torch.bool, device=dev), diagonal=1)
+    for h in range(16):
+        kh = K[:, h // 8, :].contiguous()
+        sc = (q[:, h, :].contiguous() @ kh.t().contiguous()) * scale
+        sc.masked_fill_(mask, float("-inf"))
+        pr = torch.softmax(sc, dim=-1)
+        out[:, h, :] = pr @ V[:, h // 8, :].contiguous()
+        del sc, pr
+    return (out.half().float() * torch.sigmoid(gate)).cpu().numpy()
+
+
+def test_gqa_prefill_config3_exact_call(hip):
+    """Config 3 as bench.py times it: the three-part Q4 GEMM (q|gate 8192,
+    k 512, v 512 rows from hidden 2048, fp16 scales) over T = 8192 tokens in
+    one call, then qff_gqa_prefill on its bf16 outputs from position 0.
+    Projections: 64 sampled tokens of every part against the fp64 product of
+    the dequantized weights, each bf16 output within one bf16 ulp. Attention:
+    all 8192 output rows against a vectorised fp32 restatement of the
+    oracle's arithmetic, itself checked against the oracle on 8 rows."""
+    import qff
+    T, H = 8192, 2048
+    print("config 3 exact call: Q4 GEMM T=8192 + gqa_prefill", flush=True)
+    rng = np.random.default_rng(3)
+    xb = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    ws = [synth.q4_weight(rows, H, seed=300 + i) for i, rows in enumerate((8192, 512, 512))]
+    parts = [(torch.from_numpy(w.view(np.int32)).to(DEV), torch.from_numpy(s.view(np.int16)).view(torch.float16).to(DEV),
+              torch.from_numpy(b.view(np.int16)).view(torch.float16).to(DEV)) for w, s, b in ws]
+    ctx = qff.Context(max_batch=1, max_ctx=T, max_prefill_tokens=T)
+    qg = torch.empty(T, 8192, dtype=torch.bfloat16, device=DEV)
+    k = torch.empty(T, 512, dtype=torch.bfloat16, device=DEV)
+    v = torch.empty(T, 512, dtype=torch.bfloat16, device=DEV)
+    qff.q4_matmul_parts(ctx, parts, bf16_tensor(xb), outs=(qg, k, v))
+    p = synth.gqa_params()
+    kc = torch.zeros(T, 2, 256, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    out = qff.gqa_prefill(ctx, {kk: f32_tensor(vv) for kk, vv in p.items()}, qg.view(T, 16, 512),
+                          k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    # projections on sampled tokens: the fp32 accumulation over 2048 columns
+    # is off by ~1e-6 of the terms' magnitudes (absolute, so it dominates
+    # near zero), then rounded once to bf16
+    toks = sorted({0, 1, 127, 128, 4095, 4096, 8191} | set(rng.integers(0, T, 57).tolist()))
+    xs = O.bf16_to_f32(xb[toks]).astype(np.float64)
+    for (w, s, b), y in zip(ws, (qg, k, v)):
+        ref = xs @ O.q4_dequant(w, s, b, O.F16).astype(np.float64).T
+        got = to_np(y)[toks]
+        err = np.abs(got - ref) - bf16_ulp(ref)
+        assert np.all(err <= 1e-4), f"Q4 GEMM output beyond one bf16 ulp + 1e-4: worst excess {err.max():.3g}"
+    print("  projections ok", flush=True)
+    qg_f = to_np(qg).reshape(T, 16, 512)
+    kref = np.zeros((T, 2, 256), np.uint16)
+    vref = np.zeros((T, 2, 256), np.uint16)
+    O.gqa_append_kv_seq(to_np(k).reshape(T, 2, 256), to_np(v).reshape(T, 2, 256), p["k_norm_w"], kref, vref,
+                        O.BF16, start_pos=0)
+    assert np.array_equal(vc.cpu().view(torch.int16).numpy().view(np.uint16), vref)
+    kr = O.bf16_to_f32(kref)
+    assert np.all(np.abs(O.bf16_to_f32(kc.cpu().view(torch.int16).numpy().view(np.uint16)) - kr)
+                  <= np.maximum(bf16_ulp(kr), 2.0 ** -16))
+    ref_all = _attend_all_rows_torch(qg_f, kref, vref, p["q_norm_w"], T)
+    for t in (0, 1, 63, 64, 4095, 5000, 8190, 8191):
+        o = O.gqa_attend(qg_f[t], p["q_norm_w"], kref, vref, O.BF16, t)
+        # both round the attention output to fp16 from fp32 sums taken in a
+        # different order: at most a couple of fp16 ulps (2^-10 |x|) apart
+        assert np.all(np.abs(o - ref_all[t]) <= np.maximum(2e-3, np.abs(o) * 2.0 ** -9)), \
+            f"vectorised restatement off the oracle at row {t}"
+    print("  restatement pinned; checking all rows", flush=True)
+    assert_bf16_output_close(to_np(out), ref_all)
