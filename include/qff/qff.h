@@ -272,6 +272,21 @@ int qff_gqa_decode(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
                    const int32_t* positions, void* out, qff_dtype out_dtype,
                    int batch, int max_ctx);
 
+/* qff_gqa_decode without a context, for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. No counterpart in the reference (its split-KV scratch is
+ * allocated with the Attention object, Kernels/Attention/Attention.swift
+ * :117-126). Same arguments, kernels and results as qff_gqa_decode on the
+ * current device; the split-KV partials live in a fixed device array of the
+ * library (4096 slots, 33.8 MB, one per GPU, held until the process ends),
+ * so batch is limited to 64 (QFF_ERR_WORKSPACE above). The first call on a
+ * device looks up that array's address; no call allocates or frees. Calls
+ * that overlap on one GPU (other streams or threads) race on the array. */
+int qff_gqa_decode_static(qff_stream_t stream, const qff_gqa_params* p, const void* q_gate,
+                          const void* k_new, const void* v_new, qff_dtype in_dtype, void* k_cache,
+                          void* v_cache, const int32_t* positions, void* out, qff_dtype out_dtype,
+                          int batch, int max_ctx);
+
 /* T consecutive tokens of one sequence at positions start_pos .. start_pos+T-1
  * (causal): the same per-token steps as qff_gqa_decode, with all T keys and
  * values appended to the cache. The reference runs prompts token by token

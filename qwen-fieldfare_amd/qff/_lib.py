@@ -65,6 +65,8 @@ SIGNATURES = {
                              _vp, _vp, _vp, _i, _i, _i],
     "qff_gqa_decode": [_vp, _vp, ctypes.POINTER(GqaParams), _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                        _i, _i, _i],
+    "qff_gqa_decode_static": [_vp, ctypes.POINTER(GqaParams), _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i,
+                              _i],
     "qff_gqa_prefill": [_vp, _vp, ctypes.POINTER(GqaParams), _vp, _vp, _vp, _i, _vp, _vp, _i, _vp,
                         _i, _i, _i],
     "qff_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i],
