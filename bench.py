@@ -32,13 +32,17 @@ C0_BYTES = 4_424_448           # DeltaNet decode, one layer-step at B=1
 C0_FLOPS = 3_670_016
 C1_FLOPS = 23_622_320_128      # DeltaNet chunked prefill T=4096
 C1_BYTES = 137_428_992
-# Config 1 per kernel, per launch (64 chunks x 32 heads, C = 64, d = 128):
-# the chunk-local pass owns K K^T, Q K^T, T X and T V (4 * 2C^2 d per chunk
-# and head), the state pass P U~, S W^T, S Qe^T and U^T K~ (2C^2 d + 3 * 2Cd^2).
+# Config 1 per kernel, per launch (64 chunks x 32 heads, C = 64, d = 128),
+# the canonical terms split by the kernel that computes them: the chunk-local
+# pass K K^T, Q K^T, T X and T V (4 * 2C^2 d per chunk and head), the state
+# pass S W^T and K~^T U (2 * 2Cd^2), the output pass P U~ and S Qe^T
+# (2C^2 d + 2Cd^2); the three sum to C1_FLOPS.
 C1_KERNEL_FLOPS = {
     "dn_chunk_local": 2048 * 4 * 2 * 64 * 64 * 128,
-    "dn_chunk_state": 2048 * (2 * 64 * 64 * 128 + 3 * 2 * 64 * 128 * 128),
+    "dn_chunk_state": 2048 * 2 * 2 * 64 * 128 * 128,
+    "dn_chunk_out": 2048 * (2 * 64 * 64 * 128 + 2 * 64 * 128 * 128),
 }
+assert sum(C1_KERNEL_FLOPS.values()) == 23_622_320_128
 C3_ATTN_FLOPS = 549_822_922_752   # GQA causal prefill T=8192: 32 D T (T + 1)
 C3_PROJ_FLOPS = 309_237_645_312   # 2 T 2048 (8192 + 512 + 512)
 COPY_PROBE_BYTES = 256 << 20   # --copy-probe: one D2D copy of this size (counter calibration)

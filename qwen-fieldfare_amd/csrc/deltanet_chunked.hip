@@ -416,8 +416,11 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         unswz<kC>(t, row, k8);
         pkeep[0] = *reinterpret_cast<const u32x4_t*>(Th + row * kLT + 8 * k8);
         pkeep[1] = *reinterpret_cast<const u32x4_t*>(Tl + row * kLT + 8 * k8);
-        *reinterpret_cast<u32x4_t*>(out.ph + ch * kC * kC + 8 * t) = pkeep[0];
-        *reinterpret_cast<u32x4_t*>(out.pl + ch * kC * kC + 8 * t) = pkeep[1];
+        // P and Qe are read only by the output pass, after the state pass:
+        // streamed past the caches so that W, K~ and U~, which the state pass
+        // reads next, stay in the last-level cache (state pass 107 -> 90 us)
+        __builtin_nontemporal_store(pkeep[0], reinterpret_cast<u32x4_t*>(out.ph + ch * kC * kC + 8 * t));
+        __builtin_nontemporal_store(pkeep[1], reinterpret_cast<u32x4_t*>(out.pl + ch * kC * kC + 8 * t));
     }
     // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
     //   diagonal blocks by forward substitution, waves 0-3 one each;
@@ -572,7 +575,11 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         const float4 v1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * k8 + 4);
         const float y[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         const size_t o = ch * kC * 128 + 8 * p;
-        store_split8(out.qeh + o, out.qel + o, y);
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) split_bf16x2(y[2 * k], y[2 * k + 1], hw[k], lw[k]);
+        __builtin_nontemporal_store(u32x4_t{hw[0], hw[1], hw[2], hw[3]}, reinterpret_cast<u32x4_t*>(out.qeh + o));
+        __builtin_nontemporal_store(u32x4_t{lw[0], lw[1], lw[2], lw[3]}, reinterpret_cast<u32x4_t*>(out.qel + o));
     }
     if (t == 0) s_next = 2 * grid + static_cast<int>(grabbed);
     __syncthreads();
@@ -594,162 +601,205 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 // round-robin by linear id, so the id -> (head, row block) map puts all row
 // blocks of a head on one XCD, whose L2 then serves the chunk inputs they
 // share.
-// Waves 0-3 form U^T for tokens 16w .. 16w+15, waves 4-7 O^T for tokens
-// 16(w-4) .. +15; wave w keeps state columns 16w .. 16w+15. Two waves per
-// SIMD, each with short MFMA chains, so one wave's LDS and MFMA latencies
-// overlap the other's work.
-constexpr int kStateThreads = 512;
-constexpr int kLA = 200;   // [S | U~^T] row stride: 128 + 64 + 8
+//
+// The pass carries only the state: per chunk it reads W (U waves) and K~^T
+// (S waves) and the block's U~^T rows, 68 KB per workgroup, and writes the
+// chunk's starting state S_c (bf16 hi / lo, MFMA operand order) for the
+// output pass, which forms O = Qe S_c^T + P U~ in parallel over chunks.
+//   waves 0-3 (U waves): token tile tt = wave: U = U~ - W S^T
+//       (A = W from global memory, B = S rows from LDS);
+//   waves 4-7 (S waves): state columns 32(w-4) .. +31 held as S^T tiles:
+//       S^T = e^{G_C} S^T + K~^T U (A = K~^T from global memory, B = U from
+//       LDS); they publish S_c to LDS;
+//   wave 8 (writer): copies each published S_c from LDS to the snapshot.
+// The snapshot stores have a wave of their own because vmcnt counts stores
+// as well as loads, in issue order: a wave that both stores and waits for
+// its operand loads would wait for every store issued before those loads.
+// With U and S^T as the products' outputs every LDS store is one 8-byte
+// access per lane (four consecutive tokens / state columns of one row) and
+// every operand read one 16-byte access. The two roles run separate loops
+// (same barriers), so each loop's loads and waits are straight-line code,
+// and each role issues its loads in the other role's phase: U waves refill
+// their stage (W, U~^T rows of chunk c+2) after barrier B, while the S
+// waves update the state; S waves refill theirs (K~^T of chunk c+2, a third
+// register stage) after barrier A, while the U waves form U. Issuing loads
+// stalls a wave for as long as the CU's load path is busy, so loads on the
+// chain's critical path set the step time.
+constexpr int kStateThreads = 576;
+constexpr int kSA = 136;   // S hi / lo row stride: 128 + 8
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
-                                                                      float* __restrict__ ssm_state,
-                                                                      float* __restrict__ po) {
+                                                                      float* __restrict__ ssm_state) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
     const int h = xcd * 4 + (slot >> 3), rb = slot & 7;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const bool owave = wave >= 4;          // wave-uniform role
-    const int tt = wave & 3;               // token tile of U^T / O^T
 
-    __shared__ __attribute__((aligned(16))) uint16_t Ah[16 * kLA], Al[16 * kLA];
-    __shared__ __attribute__((aligned(16))) uint16_t Uh[16 * kLT], Ul[16 * kLT];
-
-    float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * rb) * 128;
-    f32x4_t sacc;
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) sacc[ii] = Sg[(4 * kb + ii) * 128 + 16 * wave + n];
+    __shared__ __attribute__((aligned(16))) uint16_t Sh[16 * kSA], Sl[16 * kSA];   // S_c [16 rows][128]
+    __shared__ __attribute__((aligned(16))) uint16_t Uh[16 * kLT], Ul[16 * kLT];   // U^T [16 rows][64 tokens]
+    __shared__ __attribute__((aligned(16))) uint16_t Vh[16 * kLT], Vl[16 * kLT];   // U~^T rows [16][64]
 
     const int nch = (T + kC - 1) / kC;
-    // Operands of one chunk. op[0..7]: W (U waves) or Qe (O waves) token
-    // tile tt, [k step][hi, lo]; op[8..11]: P token tile tt (O waves; the U
-    // waves load W's first steps there again, an L1 hit, so that every wave
-    // runs the same loads). kr: K~^T column tile `wave`. ur: this thread's
-    // piece of the block's U~^T rows (threads < 256). Two stages: each is
-    // refilled with chunk c+2 as soon as its operands are consumed.
-    struct Stage {
-        u32x4_t op[12], kr[2][2], ur;
-        float gam;
-    };
-    const uint16_t* oph = owave ? in.qeh : in.wh;
-    const uint16_t* opl = owave ? in.qel : in.wl;
-    const uint16_t* pph = owave ? in.ph : in.wh;
-    const uint16_t* ppl = owave ? in.pl : in.wl;
-    const int pstride = owave ? kC * kC : kC * 128;   // elements per (chunk, head) block
-    auto fetch_u = [&](Stage& S, int c) {
-        const size_t ch = static_cast<size_t>(c) * 32 + h;
-        const int q = t & 255, arr = q >> 7, rem = q & 127;
-        S.ur = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) + (ch * 128 + 16 * rb + (rem >> 3)) * kC +
-                                                 8 * (rem & 7));
-        S.gam = in.gam[ch];
-    };
-    auto fetch_op = [&](Stage& S, int c) {
-        const size_t ch = static_cast<size_t>(c) * 32 + h;
-        const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
+    if (wave == 8) {
+        // ---- writer: snapshot of S_c, operand blocks (rb, k step) of the
+        // head's [128][128] state, hi and lo (read from LDS before barrier B,
+        // after which the S waves overwrite it)
+        for (int c = 0; c < nch; ++c) {
+            __syncthreads();   // A
+            const size_t so = ((static_cast<size_t>(c) * 32 + h) * 8 + rb) * 4 * 512 + 8 * lane;
+            u32x4_t vh[4], vl[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            S.op[2 * ks] = *reinterpret_cast<const u32x4_t*>(oph + ow + 512 * ks);
-            S.op[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(opl + ow + 512 * ks);
-        }
-        const size_t op = ch * pstride + 8 * (tt * (owave ? 2 : 4) * 64 + lane);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            S.op[8 + 2 * ks] = *reinterpret_cast<const u32x4_t*>(pph + op + 512 * ks);
-            S.op[9 + 2 * ks] = *reinterpret_cast<const u32x4_t*>(ppl + op + 512 * ks);
-        }
-    };
-    auto fetch_k = [&](Stage& S, int c) {
-        const size_t ch = static_cast<size_t>(c) * 32 + h;
-        const size_t ok = ch * 128 * kC + 8 * (wave * 2 * 64 + lane);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            S.kr[ks][0] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 512 * ks);
-            S.kr[ks][1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 512 * ks);
-        }
-    };
-    // One chunk from stage S, refilling S with chunk cn. The refill loads are
-    // unconditional (cn is clamped to the last chunk) and so are the output
-    // stores (the output buffer holds whole chunks): with no branch around a
-    // memory instruction the compiler's vmcnt bookkeeping stays exact and
-    // each wait covers only the loads it needs.
-    auto step = [&](Stage& S, int c, int cn) {
-        // [S | U~^T] -> LDS
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            uint16_t hh, ll;
-            split_bf16(sacc[ii], hh, ll);
-            const int o = (4 * kb + ii) * kLA + 16 * wave + n;
-            Ah[o] = hh;
-            Al[o] = ll;
-        }
-        if (t < 256) {
-            const int arr = t >> 7, rem = t & 127;
-            *reinterpret_cast<u32x4_t*>((arr ? Al : Ah) + (rem >> 3) * kLA + 128 + 8 * (rem & 7)) = S.ur;
-        }
-        const float g = S.gam;
-        __syncthreads();
-        fetch_u(S, cn);
-        // U waves: acc = S W^T (k = d, 4 steps); O waves: acc = S Qe^T +
-        // U~^T P^T (6 steps). Three accumulators (lo*hi, hi*lo, hi*hi) keep
-        // the dependent MFMA chains short.
-        f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
-#pragma unroll
-        for (int ks = 0; ks < 6; ++ks) {
-            if (ks >= 4 && !owave) break;
-            const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(Ah + n * kLA + 32 * ks + 8 * kb);
-            const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(Al + n * kLA + 32 * ks + 8 * kb);
-            a0 = mfma_16x16x32_bf16(a_l, S.op[2 * ks], a0);
-            a1 = mfma_16x16x32_bf16(a_h, S.op[2 * ks + 1], a1);
-            a2 = mfma_16x16x32_bf16(a_h, S.op[2 * ks], a2);
-        }
-        fetch_op(S, cn);
-        const f32x4_t acc = a0 + a1 + a2;
-        const int i = 16 * tt + n;
-        if (owave) {
-            // O^T -> pre-norm output (token-major)
-            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + i) * 4096 + h * 128 + 16 * rb + 4 * kb) = acc;
-        } else {
-            // U^T = U~^T - S W^T -> LDS
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                const int row = 4 * kb + ii;
-                const float ut = bf16_to_f32(Ah[row * kLA + 128 + i]) + bf16_to_f32(Al[row * kLA + 128 + i]) - acc[ii];
-                uint16_t hh, ll;
-                split_bf16(ut, hh, ll);
-                Uh[row * kLT + i] = hh;
-                Ul[row * kLT + i] = ll;
+            for (int ks = 0; ks < 4; ++ks) {
+                vh[ks] = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
+                vl[ks] = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
             }
-        }
-        __syncthreads();
-        // S = e^{G_C} S + U^T K~ (k = token, 2 steps)
-        f32x4_t s1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        sacc *= g;
+            // streamed past the caches: the output pass reads them only after
+            // this pass (measured 120 -> 110 us at T = 4096)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const u32x4_t a_h = *reinterpret_cast<const u32x4_t*>(Uh + n * kLT + 32 * ks + 8 * kb);
-            const u32x4_t a_l = *reinterpret_cast<const u32x4_t*>(Ul + n * kLT + 32 * ks + 8 * kb);
-            s1 = mfma_16x16x32_bf16(a_l, S.kr[ks][0], s1);
-            s1 = mfma_16x16x32_bf16(a_h, S.kr[ks][1], s1);
-            sacc = mfma_16x16x32_bf16(a_h, S.kr[ks][0], sacc);
+            for (int ks = 0; ks < 4; ++ks) {
+                __builtin_nontemporal_store(vh[ks], reinterpret_cast<u32x4_t*>(in.sh + so + 512 * ks));
+                __builtin_nontemporal_store(vl[ks], reinterpret_cast<u32x4_t*>(in.sl + so + 512 * ks));
+            }
+            __syncthreads();   // B
         }
-        sacc += s1;
-        fetch_k(S, cn);
-    };
-    Stage s0, s1;
-    fetch_u(s0, 0);
-    fetch_op(s0, 0);
-    fetch_k(s0, 0);
-    const int c1 = min(1, nch - 1);
-    fetch_u(s1, c1);
-    fetch_op(s1, c1);
-    fetch_k(s1, c1);
-    int c = 0;
-    for (; c + 1 < nch; c += 2) {
-        step(s0, c, min(c + 2, nch - 1));
-        step(s1, c + 1, min(c + 3, nch - 1));
+    } else if (wave < 4) {
+        // ---- U waves ------------------------------------------------------
+        const int tt = wave;
+        struct Stage {
+            u32x4_t w[8];   // W token tile tt: [k step][hi, lo]
+            u32x4_t ur;     // this thread's 16 B of the block's U~^T rows
+        };
+        auto fetch = [&](Stage& S, int c) {
+            const size_t ch = static_cast<size_t>(c) * 32 + h;
+            const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                S.w[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.wh + ow + 512 * ks);
+                S.w[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.wl + ow + 512 * ks);
+            }
+            const int arr = t >> 7, rem = t & 127;
+            S.ur = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) +
+                                                     (ch * 128 + 16 * rb + (rem >> 3)) * kC + 8 * (rem & 7));
+        };
+        auto step = [&](Stage& S, int cn) {
+            {
+                const int arr = t >> 7, rem = t & 127;
+                *reinterpret_cast<u32x4_t*>((arr ? Vl : Vh) + (rem >> 3) * kLT + 8 * (rem & 7)) = S.ur;
+            }
+            __syncthreads();   // A: S_c and U~^T rows in LDS
+            // acc[tok][row] = sum_k W[tok][k] S[row][k] (three accumulators:
+            // lo*hi, hi*lo, hi*hi)
+            f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const u32x4_t b_h = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
+                const u32x4_t b_l = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
+                a0 = mfma_16x16x32_bf16(S.w[2 * ks + 1], b_h, a0);
+                a1 = mfma_16x16x32_bf16(S.w[2 * ks], b_l, a1);
+                a2 = mfma_16x16x32_bf16(S.w[2 * ks], b_h, a2);
+            }
+            const f32x4_t acc = a0 + a1 + a2;
+            // U[tok][row] = U~[tok][row] - acc for row n, tokens 16 tt + 4 kb + ii:
+            // four consecutive tokens of row n in the [row][token] tiles
+            const int o = n * kLT + 16 * tt + 4 * kb;
+            const u32x2_t vh = *reinterpret_cast<const u32x2_t*>(Vh + o);
+            const u32x2_t vl = *reinterpret_cast<const u32x2_t*>(Vl + o);
+            float u[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                u[2 * e] = __uint_as_float(vh[e] << 16) + __uint_as_float(vl[e] << 16) - acc[2 * e];
+                u[2 * e + 1] = __uint_as_float(vh[e] & 0xffff0000u) + __uint_as_float(vl[e] & 0xffff0000u) -
+                               acc[2 * e + 1];
+            }
+            uint32_t h0, l0, h1, l1;
+            split_bf16x2(u[0], u[1], h0, l0);
+            split_bf16x2(u[2], u[3], h1, l1);
+            *reinterpret_cast<u32x2_t*>(Uh + o) = u32x2_t{h0, h1};
+            *reinterpret_cast<u32x2_t*>(Ul + o) = u32x2_t{l0, l1};
+            __syncthreads();   // B: U in LDS
+            fetch(S, cn);
+        };
+        Stage s0, s1;
+        fetch(s0, 0);
+        fetch(s1, min(1, nch - 1));
+        int c = 0;
+        for (; c + 1 < nch; c += 2) {
+            step(s0, min(c + 2, nch - 1));
+            step(s1, min(c + 3, nch - 1));
+        }
+        if (c < nch) step(s0, c);
+    } else {
+        // ---- S waves ------------------------------------------------------
+        // sacc[ct][ii] = S[row n][col 32 sw + 16 ct + 4 kb + ii]: the C tile of
+        // S^T for state columns 32 sw + 16 ct .. +15
+        const int sw = wave - 4;
+        float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * rb + n) * 128 + 32 * sw + 4 * kb;
+        f32x4_t sacc[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) sacc[ct] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * ct);
+        struct Stage {
+            u32x4_t k[2][4];   // K~^T column tiles 2 sw + ct: [k step][hi, lo]
+            float gam;
+        };
+        auto fetch = [&](Stage& S, int c) {
+            const size_t ch = static_cast<size_t>(c) * 32 + h;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const size_t ok = ch * 128 * kC + 8 * ((2 * sw + ct) * 2 * 64 + lane);
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    S.k[ct][2 * ks] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 512 * ks);
+                    S.k[ct][2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 512 * ks);
+                }
+            }
+            S.gam = in.gam[ch];
+        };
+        // step c computes from stage S and refills stage F (last used in step
+        // c - 1) with chunk cn = c + 2
+        auto step = [&](Stage& S, Stage& F, int cn) {
+            // publish S_c: row n, four consecutive columns per tile
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                uint32_t h0, l0, h1, l1;
+                split_bf16x2(sacc[ct][0], sacc[ct][1], h0, l0);
+                split_bf16x2(sacc[ct][2], sacc[ct][3], h1, l1);
+                const int o = n * kSA + 32 * sw + 16 * ct + 4 * kb;
+                *reinterpret_cast<u32x2_t*>(Sh + o) = u32x2_t{h0, h1};
+                *reinterpret_cast<u32x2_t*>(Sl + o) = u32x2_t{l0, l1};
+            }
+            __syncthreads();   // A
+            fetch(F, cn);
+            const float g = S.gam;
+            __syncthreads();   // B
+            // S^T = e^{G_C} S^T + K~^T U (k = token, 2 steps)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const u32x4_t b_h = *reinterpret_cast<const u32x4_t*>(Uh + n * kLT + 32 * ks + 8 * kb);
+                const u32x4_t b_l = *reinterpret_cast<const u32x4_t*>(Ul + n * kLT + 32 * ks + 8 * kb);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    if (ks == 0) sacc[ct] *= g;
+                    f32x4_t s1 = mfma_16x16x32_bf16(S.k[ct][2 * ks + 1], b_h, f32x4_t{0.f, 0.f, 0.f, 0.f});
+                    s1 = mfma_16x16x32_bf16(S.k[ct][2 * ks], b_l, s1);
+                    sacc[ct] = mfma_16x16x32_bf16(S.k[ct][2 * ks], b_h, sacc[ct]);
+                    sacc[ct] += s1;
+                }
+            }
+        };
+        Stage s0, s1, s2;
+        fetch(s0, 0);
+        fetch(s1, min(1, nch - 1));
+        int c = 0;
+        for (; c + 2 < nch; c += 3) {
+            step(s0, s2, min(c + 2, nch - 1));
+            step(s1, s0, min(c + 3, nch - 1));
+            step(s2, s1, min(c + 4, nch - 1));
+        }
+        if (c < nch) step(s0, s2, min(c + 2, nch - 1));
+        if (c + 1 < nch) step(s1, s0, c + 1);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) *reinterpret_cast<f32x4_t*>(Sg + 16 * ct) = sacc[ct];
     }
-    if (c < nch) step(s0, c, c);
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) Sg[(4 * kb + ii) * 128 + 16 * wave + n] = sacc[ii];
 }
 
 hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_deltanet_params* p,
@@ -769,7 +819,7 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
                                                                          p->conv_w, conv_state, ctx->dn, sched);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
-    dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);
+    dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state);
     return hipGetLastError();
 }
 
