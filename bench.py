@@ -35,12 +35,11 @@ C1_BYTES = 137_428_992
 # Config 1 per kernel, per launch (64 chunks x 32 heads, C = 64, d = 128),
 # the canonical terms split by the kernel that computes them: the chunk-local
 # pass K K^T, Q K^T, T X and T V (4 * 2C^2 d per chunk and head), the state
-# pass S W^T and K~^T U (2 * 2Cd^2), the output pass P U~ and S Qe^T
-# (2C^2 d + 2Cd^2); the three sum to C1_FLOPS.
+# pass S W^T, K~^T U, S Qe^T and P U~ (3 * 2Cd^2 + 2C^2 d); the two sum to
+# C1_FLOPS (the norm pass does no matrix work).
 C1_KERNEL_FLOPS = {
     "dn_chunk_local": 2048 * 4 * 2 * 64 * 64 * 128,
-    "dn_chunk_state": 2048 * 2 * 2 * 64 * 128 * 128,
-    "dn_chunk_out": 2048 * (2 * 64 * 64 * 128 + 2 * 64 * 128 * 128),
+    "dn_chunk_state": 2048 * (3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128),
 }
 assert sum(C1_KERNEL_FLOPS.values()) == 23_622_320_128
 C3_ATTN_FLOPS = 549_822_922_752   # GQA causal prefill T=8192: 32 D T (T + 1)

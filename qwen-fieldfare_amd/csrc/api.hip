@@ -39,6 +39,7 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
     L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * (64 + 1) * sizeof(float));   // 64 group sums + inverse RMS
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
+    L.pf_o = take(TC * 4096 * sizeof(float));
     L.dn_o = take(B * 4096 * sizeof(float));
     L.sched = take(2 * kSchedSlots * sizeof(unsigned));
     const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
@@ -48,9 +49,6 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.uth = take(big); L.utl = take(big);
     L.ph = take(small); L.pl = take(small);
     L.gam = take(TC / 64 * 32 * sizeof(float));
-    const size_t snap = TC / 64 * 32 * 128 * 128 * sizeof(uint16_t);
-    L.sh = take(snap);
-    L.sl = take(snap);
     L.total = off;
     return L;
 }
@@ -160,6 +158,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_qb = u16(L.gqa_qb);
     c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
+    c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
     c->dn_o = reinterpret_cast<float*>(base + L.dn_o);
     c->sched = reinterpret_cast<unsigned*>(base + L.sched);
     c->num_cu = prop.multiProcessorCount;
@@ -170,8 +169,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
         return QFF_ERR_HIP;
     }
     c->dn = qff_dn_bufs{u16(L.wh),  u16(L.wl),  u16(L.qeh), u16(L.qel), u16(L.kth), u16(L.ktl),
-                        u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam),
-                        u16(L.sh),  u16(L.sl)};
+                        u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam)};
     (void)hipSetDevice(prev);
     *out = c;
     return QFF_OK;

@@ -596,40 +596,35 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 
 // ---- sequential state pass ---------------------------------------------------
 
-// One workgroup per (16-row block of the state, value head), 512 threads; a
+// One workgroup per (16-row block of the state, value head), 768 threads; a
 // 1-D grid of 256 workgroups. Workgroups are dispatched to the 8 XCDs
 // round-robin by linear id, so the id -> (head, row block) map puts all row
 // blocks of a head on one XCD, whose L2 then serves the chunk inputs they
-// share.
-//
-// The pass carries only the state: per chunk it reads W (U waves) and K~^T
-// (S waves) and the block's U~^T rows, 68 KB per workgroup, and writes the
-// chunk's starting state S_c (bf16 hi / lo, MFMA operand order) for the
-// output pass, which forms O = Qe S_c^T + P U~ in parallel over chunks.
+// share. Twelve waves with fixed roles:
 //   waves 0-3 (U waves): token tile tt = wave: U = U~ - W S^T
 //       (A = W from global memory, B = S rows from LDS);
 //   waves 4-7 (S waves): state columns 32(w-4) .. +31 held as S^T tiles:
 //       S^T = e^{G_C} S^T + K~^T U (A = K~^T from global memory, B = U from
 //       LDS); they publish S_c to LDS;
-//   wave 8 (writer): copies each published S_c from LDS to the snapshot.
-// The snapshot stores have a wave of their own because vmcnt counts stores
-// as well as loads, in issue order: a wave that both stores and waits for
-// its operand loads would wait for every store issued before those loads.
-// With U and S^T as the products' outputs every LDS store is one 8-byte
-// access per lane (four consecutive tokens / state columns of one row) and
-// every operand read one 16-byte access. The two roles run separate loops
-// (same barriers), so each loop's loads and waits are straight-line code,
-// and each role issues its loads in the other role's phase: U waves refill
-// their stage (W, U~^T rows of chunk c+2) after barrier B, while the S
-// waves update the state; S waves refill theirs (K~^T of chunk c+2, a third
-// register stage) after barrier A, while the U waves form U. Issuing loads
-// stalls a wave for as long as the CU's load path is busy, so loads on the
-// chain's critical path set the step time.
-constexpr int kStateThreads = 576;
+//   waves 8-11 (O waves): token tile tt = wave - 8: the block's pre-norm
+//       output rows O^T = S_c Qe^T + U~^T P^T (Qe, P from global memory).
+// Per chunk c:
+//   [S waves publish S_c, U waves publish U~ rows]
+//   A  U waves form U;  O waves copy S_c and U~ rows (their A operands) to
+//      registers;  S waves request K~ of chunk c+2
+//   B  S waves update the state;  O waves form and store O^T, then request
+//      Qe, P of chunk c+1;  U waves request W, U~ of chunk c+2
+// so the chain (U, then the state update) never waits on a global load it
+// issues itself: issuing loads stalls a wave for as long as the CU's load
+// path is busy. With U and S^T as the chain's product outputs every LDS
+// store is one 8-byte access per lane. The roles run separate loops (same
+// barriers), so each loop's loads and waits are straight-line code.
+constexpr int kStateThreads = 768;
 constexpr int kSA = 136;   // S hi / lo row stride: 128 + 8
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
-                                                                      float* __restrict__ ssm_state) {
+                                                                      float* __restrict__ ssm_state,
+                                                                      float* __restrict__ po) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
     const int h = xcd * 4 + (slot >> 3), rb = slot & 7;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -640,27 +635,61 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
     __shared__ __attribute__((aligned(16))) uint16_t Vh[16 * kLT], Vl[16 * kLT];   // U~^T rows [16][64]
 
     const int nch = (T + kC - 1) / kC;
-    if (wave == 8) {
-        // ---- writer: snapshot of S_c, operand blocks (rb, k step) of the
-        // head's [128][128] state, hi and lo (read from LDS before barrier B,
-        // after which the S waves overwrite it)
+    if (wave >= 8) {
+        // ---- O waves ------------------------------------------------------
+        const int tt = wave - 8;
+        struct Stage {
+            u32x4_t qe[8];   // Qe token tile tt: [k step][hi, lo]
+            u32x4_t p[4];    // P token tile tt: [k step][hi, lo]
+        };
+        auto fetch = [&](Stage& S, int c) {
+            const size_t ch = static_cast<size_t>(c) * 32 + h;
+            const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                S.qe[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.qeh + ow + 512 * ks);
+                S.qe[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.qel + ow + 512 * ks);
+            }
+            const size_t op = ch * kC * kC + 8 * (tt * 2 * 64 + lane);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                S.p[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.ph + op + 512 * ks);
+                S.p[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.pl + op + 512 * ks);
+            }
+        };
+        Stage st;
+        fetch(st, 0);
         for (int c = 0; c < nch; ++c) {
-            __syncthreads();   // A
-            const size_t so = ((static_cast<size_t>(c) * 32 + h) * 8 + rb) * 4 * 512 + 8 * lane;
-            u32x4_t vh[4], vl[4];
+            __syncthreads();   // A(c)
+            u32x4_t sa_h[4], sa_l[4], ua_h[2], ua_l[2];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                vh[ks] = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
-                vl[ks] = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
+                sa_h[ks] = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
+                sa_l[ks] = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
             }
-            // streamed past the caches: the output pass reads them only after
-            // this pass (measured 120 -> 110 us at T = 4096)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                ua_h[ks] = *reinterpret_cast<const u32x4_t*>(Vh + n * kLT + 32 * ks + 8 * kb);
+                ua_l[ks] = *reinterpret_cast<const u32x4_t*>(Vl + n * kLT + 32 * ks + 8 * kb);
+            }
+            __syncthreads();   // B(c): (the barrier waits for these LDS reads)
+            f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                __builtin_nontemporal_store(vh[ks], reinterpret_cast<u32x4_t*>(in.sh + so + 512 * ks));
-                __builtin_nontemporal_store(vl[ks], reinterpret_cast<u32x4_t*>(in.sl + so + 512 * ks));
+                a0 = mfma_16x16x32_bf16(sa_l[ks], st.qe[2 * ks], a0);
+                a1 = mfma_16x16x32_bf16(sa_h[ks], st.qe[2 * ks + 1], a1);
+                a2 = mfma_16x16x32_bf16(sa_h[ks], st.qe[2 * ks], a2);
             }
-            __syncthreads();   // B
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                a0 = mfma_16x16x32_bf16(ua_l[ks], st.p[2 * ks], a0);
+                a1 = mfma_16x16x32_bf16(ua_h[ks], st.p[2 * ks + 1], a1);
+                a2 = mfma_16x16x32_bf16(ua_h[ks], st.p[2 * ks], a2);
+            }
+            fetch(st, min(c + 1, nch - 1));
+            // O^T[row 4kb + ii][token 16 tt + n] -> pre-norm output (token-major)
+            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + 16 * tt + n) * 4096 + h * 128 + 16 * rb +
+                                        4 * kb) = a0 + a1 + a2;
         }
     } else if (wave < 4) {
         // ---- U waves ------------------------------------------------------
@@ -754,8 +783,8 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             }
             S.gam = in.gam[ch];
         };
-        // step c computes from stage S and refills stage F (last used in step
-        // c - 1) with chunk cn = c + 2
+        // step computes from stage S and refills stage F (last used in the
+        // previous step) with chunk cn = c + 2
         auto step = [&](Stage& S, Stage& F, int cn) {
             // publish S_c: row n, four consecutive columns per tile
 #pragma unroll
@@ -819,7 +848,7 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
                                                                          p->conv_w, conv_state, ctx->dn, sched);
     }
     ProfScope prof(ctx, stream, "dn_chunk_state");
-    dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state);
+    dn_chunk_state_kernel<<<256, kStateThreads, 0, stream>>>(T, ctx->dn, ssm_state, ctx->pf_o);
     return hipGetLastError();
 }
 

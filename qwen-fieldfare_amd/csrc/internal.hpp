@@ -24,7 +24,6 @@ struct qff_dn_bufs {
     uint16_t *uth, *utl;    // U~^T [128][64]
     uint16_t *ph, *pl;      // P [64][64]
     float* gam;             // e^{G_C}
-    uint16_t *sh, *sl;      // S_c, the state at the chunk's start [128][128] (written by the state pass)
 };
 
 struct qff_ctx {
@@ -43,7 +42,9 @@ struct qff_ctx {
     // (row G after the groups: the inverse RMS of a normed product).
     float* q4_xs = nullptr;
     int q4_xs_tokens = 0;
-    // DeltaNet prefill: chunk intermediates and per-chunk state snapshots.
+    // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
+    // chunk intermediates.
+    float* pf_o = nullptr;
     qff_dn_bufs dn{};
     // DeltaNet decode: pre-norm outputs [max_batch][32][128] fp32.
     float* dn_o = nullptr;
@@ -69,7 +70,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam, sh, sl;
+    size_t gqa_qb, q4_xs, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
