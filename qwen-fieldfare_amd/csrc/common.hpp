@@ -107,6 +107,43 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Integer sum / maximum over the whole wave (every lane gets the result) and
+// the inclusive prefix sum over lanes 0 .. l, on the same DPP paths. The
+// scan is the row-shift ladder within each row of 16 lanes, then
+// row_bcast:15 (row r's last lane added to row r + 1) and row_bcast:31
+// (lane 31 added to rows 2 and 3); lanes without a source add 0.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ int dpp_int(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, BANK_MASK, true);
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+    v += dpp_int<0xB1>(v);
+    v += dpp_int<0x4E>(v);
+    v += dpp_int<0x141>(v);
+    v += dpp_int<0x140>(v);
+    v += __builtin_amdgcn_ds_swizzle(v, 0x401f);
+    const auto h = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return static_cast<int>(h[0] + h[1]);
+}
+__device__ __forceinline__ int wave_max_int(int v) {
+    v = max(v, dpp_int<0xB1>(v));
+    v = max(v, dpp_int<0x4E>(v));
+    v = max(v, dpp_int<0x141>(v));
+    v = max(v, dpp_int<0x140>(v));
+    v = max(v, __builtin_amdgcn_ds_swizzle(v, 0x401f));
+    const auto h = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return max(static_cast<int>(h[0]), static_cast<int>(h[1]));
+}
+__device__ __forceinline__ int wave_inclusive_scan_int(int v) {
+    v += dpp_int<0x111>(v);               // row_shr:1
+    v += dpp_int<0x112>(v);               // row_shr:2
+    v += dpp_int<0x114>(v);               // row_shr:4
+    v += dpp_int<0x118>(v);               // row_shr:8
+    v += dpp_int<0x142, 0xa>(v);          // row_bcast:15 into rows 1, 3
+    v += dpp_int<0x143, 0xc>(v);          // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 __device__ __forceinline__ float dot4(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }

@@ -297,6 +297,8 @@ __device__ __forceinline__ void gqa_partial_unit(
         }
         wave_lds_sync();
     };
+    // (issuing both stages before the q work was measured slower: 254
+    // VGPRs and a longer issue stall ahead of the q loads)
     int p0 = p_start;
     for (; p0 + kDecTile < p_end; p0 += 2 * kDecTile) {
         load(tb, p0 + kDecTile);
@@ -322,28 +324,85 @@ __device__ __forceinline__ void gqa_partial_unit(
     }
 }
 
-// grid (2 kv heads x chunks, 1, batch), one wave each; the kv head is the fastest-varying block index, so the two
-// heads' workgroups of a chunk are dispatched together and stream the
-// interleaved halves of the same cache records at the same time. Two
-// single-wave workgroups per SIMD stay resident, each with its next tile in
-// flight. Lengths come from the
-// device `positions` array; waves past a sequence's last chunk exit at once.
+// ---- split of a call's positions into chunks ----------------------------------
+//
+// Every workgroup of the partial and combine launches derives the same split
+// from the device `positions` (no host sync, no atomics): the chunk length
+// ch (a multiple of 32 positions, at least 32) makes about `target` chunks
+// per kv head out of the batch's total attended length P = sum_b L_b,
+// whatever the individual lengths, and at most `cap` chunks per sequence;
+// sequence b takes nc_b = ceil(L_b / ch) chunks, numbered from
+// first_b = sum_{b' < b} nc_b'. A sequence whose position lies outside the
+// cache has length 0 (no chunks; its outputs are NaN).
+__device__ __forceinline__ int gqa_len(const int32_t* __restrict__ positions, int b, int max_ctx) {
+    const int pos = positions[b];
+    return (pos >= 0 && pos < max_ctx) ? pos + 1 : 0;
+}
+
+// The split as seen by one wave: chunk length ch (every lane) and, for
+// global chunk index g, its (sequence, chunk), or seq = -1 past the last
+// chunk, and that sequence's length len = position + 1.
+// Lane l reads positions l, l + 64, ...; batches up to 64 read them
+// once. The K/V streams of a partial workgroup wait for this, so the
+// reductions and the prefix run on DPP moves, not LDS permutes.
+__device__ __forceinline__ void gqa_split(const int32_t* __restrict__ positions, int batch, int max_ctx, int target,
+                                          int cap, int g, int lane, int& ch, int& seq, int& c, int& len) {
+    const int L0 = lane < batch ? gqa_len(positions, lane, max_ctx) : 0;
+    long long P = wave_sum_int(L0);
+    int maxL = wave_max_int(L0);
+    for (int b0 = 64; b0 < batch; b0 += 64) {
+        const int L = b0 + lane < batch ? gqa_len(positions, b0 + lane, max_ctx) : 0;
+        P += wave_sum_int(L);
+        maxL = max(maxL, wave_max_int(L));
+    }
+    const int by_total = static_cast<int>((P + target - 1) / target), by_cap = (maxL + cap - 1) / cap;
+    ch = (max(max(by_total, by_cap), 1) + 31) / 32 * 32;
+    seq = -1;
+    c = 0;
+    len = 0;
+    int base = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+        const int L = b0 == 0 ? L0 : (b0 + lane < batch ? gqa_len(positions, b0 + lane, max_ctx) : 0);
+        const int nc = (L + ch - 1) / ch;
+        const int incl = base + wave_inclusive_scan_int(nc);   // chunks of sequences b0 .. b0 + lane
+        // the first lane whose inclusive count exceeds g holds chunk g
+        const unsigned long long hit = __ballot(incl > g);
+        if (hit) {
+            const int src = static_cast<int>(__builtin_ctzll(hit));
+            seq = b0 + src;
+            c = g - (__builtin_amdgcn_readlane(incl, src) - __builtin_amdgcn_readlane(nc, src));
+            len = __builtin_amdgcn_readlane(L, src);
+            return;
+        }
+        base = __builtin_amdgcn_readlane(incl, 63);
+    }
+}
+
+// grid 2 x (target + batch), one wave each: workgroup u takes kv head u & 1
+// of global chunk u >> 1 of the split above (workgroups past the last chunk
+// exit at once). The kv head is the fastest-varying index, so the two heads'
+// workgroups of a chunk are dispatched together and stream the interleaved
+// halves of the same cache records at the same time. Two single-wave
+// workgroups per SIMD stay resident, each with its next tile in flight.
 template <int IN_DT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ positions, int max_ctx, int chunk_len, int cstride, float* __restrict__ pm,
-    float* __restrict__ pd, float* __restrict__ po) {
-    const int kvh = blockIdx.x & 1, c = blockIdx.x >> 1, seq = blockIdx.z;
-    const int pos = positions[seq];
-    // a position outside the cache is the caller's error: skip the sequence
-    // (the combine writes NaN for it) rather than touch memory past the cache
-    if (pos < 0 || pos >= max_ctx || c * chunk_len > pos) return;
+    const int32_t* __restrict__ positions, int batch, int max_ctx, int target, int cstride,
+    float* __restrict__ pm, float* __restrict__ pd, float* __restrict__ po) {
+    const int lane = threadIdx.x & 63;
+    const int kvh = blockIdx.x & 1;
+    int chunk_len, seq, c, len;
+    gqa_split(positions, batch, max_ctx, target, cstride, static_cast<int>(blockIdx.x >> 1), lane, chunk_len, seq, c,
+              len);
+    // past the last chunk; sequences whose position lies outside the cache
+    // (the caller's error) have no chunks: the combine writes NaN for them
+    if (seq < 0) return;
+    const int pos = len - 1;
     __shared__ __attribute__((aligned(16))) DecLds lds;
     __shared__ float freqs[32];
-    const int lane = threadIdx.x & 63;
     if (lane < 32) freqs[lane] = rf.f[lane];
     wave_lds_sync();
     gqa_partial_unit<IN_DT>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
@@ -359,7 +418,7 @@ void gqa_decode_partial_kernel(
 // flight per lane, and their sums are added in LDS in a fixed order.
 template <int IN_DT, int OUT_DT, int DS>
 __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
-    const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int max_ctx, int chunk_len,
+    const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int batch, int max_ctx, int target,
     int cstride, const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
     constexpr int kDims = 256 / DS, kLanes = 64 / DS, kStreams = 8 * DS;
@@ -375,6 +434,8 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
         if (t < kDims) elem<OUT_DT>::store(out, qi * 256 + d0 + t, __builtin_nanf(""));
         return;
     }
+    int chunk_len, unused_seq, unused_c, unused_len;
+    gqa_split(positions, batch, max_ctx, target, cstride, 0, lane, chunk_len, unused_seq, unused_c, unused_len);
     const int L = pos + 1;
     const int nc = (L + chunk_len - 1) / chunk_len;
     const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * cstride;
@@ -431,26 +492,11 @@ int gqa_chunk_cap(const qff_ctx_cfg& cfg, int batch) {
     return cap < kGqaMaxChunks ? cap : kGqaMaxChunks;
 }
 
-// Chunk length for `waves` one-wave partial workgroups over the batch, at
-// most `cap` chunks per sequence, multiples of 32 positions (2 MFMA tiles).
-static int gqa_chunk_len_for(int max_ctx, int batch, int cap, int waves) {
-    int target = waves / (2 * batch);
-    if (target < 1) target = 1;
-    if (target > cap) target = cap;
-    const int per = (max_ctx + target - 1) / target;
-    const int ch = ((per + 31) / 32) * 32;
-    return ch < 32 ? 32 : ch;
-}
-
-// One round of resident waves (two per SIMD) when that still gives chunks of
-// 512 positions or more, else two rounds: long contexts lose less to a
-// second round's tail than short ones gain from more waves (measured: config
-// 4 at 32K 2.7 % faster with one round, config 2 at 8K 6 % slower).
-int gqa_chunk_len(int max_ctx, int batch, int cap, int num_cu) {
-    const int resident = 8 * num_cu;
-    const int one = gqa_chunk_len_for(max_ctx, batch, cap, resident);
-    return one >= 512 ? one : gqa_chunk_len_for(max_ctx, batch, cap, 2 * resident);
-}
+// Chunks per kv head a call aims for: half a round of resident one-wave
+// workgroups (two per SIMD, 8 per CU) over both kv heads. Measured at
+// context 8192 with random lengths and config 4: 2 x CUs beat 4 x (batch 8
+// 26.6 vs 28.9 us, config 4 at batch 16 3.72 vs 3.81 ms) and 8 x.
+static int gqa_target_chunks(int num_cu) { return 2 * (num_cu > 0 ? num_cu : 256); }
 
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
                              const void* q_gate, const void* k_new, const void* v_new,
@@ -468,17 +514,20 @@ hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream
                                   const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                                   int max_ctx) {
     const int cap = ws.cap;
-    const int ch = gqa_chunk_len(max_ctx, batch, cap, ws.num_cu);
-    const int nc = (max_ctx + ch - 1) / ch;
+    // the split is derived from the device positions inside the kernels; at
+    // most target + batch chunks per kv head (rounding up adds at most one
+    // per sequence), so the grid covers every chunk of any length mix
+    const int target = gqa_target_chunks(ws.num_cu);
+    const int units = 2 * (target + batch);
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     {
         ProfScope prof(ctx, stream, "gqa_decode_partial");
-#define QFF_PART(I)                                                                                            \
-    gqa_decode_partial_kernel<I><<<dim3(2 * nc, 1, batch), 64, 0, stream>>>(                                   \
-        q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, kc, vc, positions, max_ctx, ch, cap, \
-        ws.m, ws.d, ws.o)
+#define QFF_PART(I)                                                                                             \
+    gqa_decode_partial_kernel<I><<<units, 64, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf,   \
+                                                          p->scale, p->eps, kc, vc, positions, batch, max_ctx,  \
+                                                          target, cap, ws.m, ws.d, ws.o)
         if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
 #undef QFF_PART
     }
@@ -488,11 +537,11 @@ hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream
     ProfScope prof(ctx, stream, "gqa_decode_combine");
 #define QFF_COMB(I, O)                                                                                      \
     if (ds == 4)                                                                                            \
-        gqa_decode_combine_kernel<I, O, 4><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
-                                                                      ws.m, ws.d, ws.o, out);               \
+        gqa_decode_combine_kernel<I, O, 4><<<cgrid, 512, 0, stream>>>(q_gate, positions, batch, max_ctx,   \
+                                                                      target, cap, ws.m, ws.d, ws.o, out);  \
     else                                                                                                    \
-        gqa_decode_combine_kernel<I, O, 1><<<cgrid, 512, 0, stream>>>(q_gate, positions, max_ctx, ch, cap,  \
-                                                                      ws.m, ws.d, ws.o, out)
+        gqa_decode_combine_kernel<I, O, 1><<<cgrid, 512, 0, stream>>>(q_gate, positions, batch, max_ctx,   \
+                                                                      target, cap, ws.m, ws.d, ws.o, out)
     if (in_dtype == QFF_BF16) {
         if (out_dtype == QFF_BF16) { QFF_COMB(1, 1); } else { QFF_COMB(1, 0); }
     } else {
