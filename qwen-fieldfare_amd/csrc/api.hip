@@ -40,8 +40,8 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * (64 + 1) * sizeof(float));   // 64 group sums + inverse RMS
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(float));
-    L.dn_o = take(B * 4096 * sizeof(float));
     L.sched = take(2 * kSchedSlots * sizeof(unsigned));
+    L.dn_arrive = take(B * 16 * sizeof(unsigned));
     const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
     L.wh = take(big); L.wl = take(big);
     L.qeh = take(big); L.qel = take(big);
@@ -159,10 +159,11 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
     c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
-    c->dn_o = reinterpret_cast<float*>(base + L.dn_o);
     c->sched = reinterpret_cast<unsigned*>(base + L.sched);
     c->num_cu = prop.multiProcessorCount;
-    if (hipMemset(c->sched, 0, 2 * kSchedSlots * sizeof(unsigned)) != hipSuccess) {
+    c->dn_arrive = reinterpret_cast<unsigned*>(base + L.dn_arrive);
+    if (hipMemset(c->sched, 0, 2 * kSchedSlots * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(c->dn_arrive, 0, static_cast<size_t>(c->cfg.max_batch) * 16 * sizeof(unsigned)) != hipSuccess) {
         (void)hipFree(c->ws);
         delete c;
         (void)hipSetDevice(prev);

@@ -46,8 +46,9 @@ struct qff_ctx {
     // chunk intermediates.
     float* pf_o = nullptr;
     qff_dn_bufs dn{};
-    // DeltaNet decode: pre-norm outputs [max_batch][32][128] fp32.
-    float* dn_o = nullptr;
+    // DeltaNet decode: per (sequence, key head) arrival counters [max_batch][16],
+    // zero between launches (the second arrival resets its counter).
+    unsigned* dn_arrive = nullptr;
     // Work-queue counters of the persistent kernels, zero between launches
     // (each launch's last workgroup resets its pair); kSchedSlots pairs.
     unsigned* sched = nullptr;
@@ -70,7 +71,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, pf_o, dn_o, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, pf_o, dn_arrive, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

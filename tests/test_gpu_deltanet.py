@@ -35,7 +35,7 @@ def _oracle_decode(p, inp, in_f32=False):
     return np.stack(outs), np.stack(convs), np.stack(ssms)
 
 
-@pytest.mark.parametrize("B", [1, 3, 16, 20])
+@pytest.mark.parametrize("B", [1, 3, 16, 20, 32])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
     import qff
@@ -61,8 +61,7 @@ def test_deltanet_decode_matches_oracle(hip, B, out_dtype):
 @pytest.mark.parametrize("B", [4, 6])
 def test_deltanet_decode_f32_inputs_and_repeat(hip, B):
     """fp32 activations, and three steps in a row on the same context and
-    state buffers (batch 4 takes the two-launch split, 6 the one-launch
-    kernel)."""
+    state buffers."""
     import qff
     p = synth.deltanet_params()
     inp = synth.deltanet_decode_inputs(B, seed=7)
@@ -162,10 +161,9 @@ def test_deltanet_decode_consecutive_steps(hip, B, T):
     """qff_deltanet_decode, the reference's per-token path
     (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561 -> deltanet.metal
     :250-356), T steps in a row on the config-1 inputs from zero state (batch
-    1: 4096 steps, the two-launch small-batch kernels; batch 6: 1024 steps
-    of six independent sequences, the one-launch kernel), against the
-    sequential fp32 oracle: every step's output within the bf16 bar and the
-    state rel <= 1e-4 at the end."""
+    1: 4096 steps; batch 6: 1024 steps of six independent sequences),
+    against the sequential fp32 oracle: every step's output within the bf16
+    bar and the state rel <= 1e-4 at the end."""
     import qff
     print(f"deltanet_decode {T} consecutive steps B={B} (oracle running)", flush=True)
     p = synth.deltanet_params()
@@ -227,3 +225,61 @@ def test_deltanet_prefill_f32_inputs(hip, T):
             assert_bf16_output_close(to_np(out), ref_o)
         assert np.array_equal(to_np(conv), ref_c)
         assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+
+
+def test_deltanet_decode_batches_alternate_and_graph_replay(hip):
+    """The two value heads of a key head share its q/k conv-state slots; the
+    second workgroup to finish reading them rewrites them, counted on
+    per-(sequence, key head) counters in the context that every launch
+    leaves at zero. Calls of different batch sizes on one context, then a
+    captured step replayed three times (eager work and a sync between the
+    replays): every output, conv state and state against the oracle."""
+    import qff
+    p = synth.deltanet_params()
+    pg = _params_gpu(p)
+    ctx = qff.Context(max_batch=32, max_prefill_tokens=1)
+    for B in (32, 2, 17, 1, 32):
+        print(f"deltanet_decode alternate B={B}", flush=True)
+        inp = synth.deltanet_decode_inputs(B, seed=300 + B)
+        ref_o, ref_c, ref_s = _oracle_decode(p, inp)
+        conv = f32_tensor(inp["conv_state"])
+        ssm = f32_tensor(inp["ssm_state"])
+        out = qff.deltanet_decode(ctx, pg, bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"]), f32_tensor(inp["a"]),
+                                  f32_tensor(inp["b"]), conv, ssm, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert_f32_output_close(to_np(out), ref_o)
+        assert np.array_equal(to_np(conv), ref_c)
+        assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
+
+    B = 5
+    print(f"deltanet_decode graph replay B={B}", flush=True)
+    inp = synth.deltanet_decode_inputs(B, seed=77)
+    qkv, z = bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"])
+    a, b = f32_tensor(inp["a"]), f32_tensor(inp["b"])
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = torch.empty(B, 4096, dtype=torch.float32, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        # warm-up call outside the graph, on scratch copies of the state
+        c2, s2 = conv.clone(), ssm.clone()
+        qff.deltanet_decode(ctx, pg, qkv, z, a, b, c2, s2, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qff.deltanet_decode(ctx, pg, qkv, z, a, b, conv, ssm, out=out)
+    cs, ss = inp["conv_state"], inp["ssm_state"]
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        inp["conv_state"], inp["ssm_state"] = cs, ss
+        ref_o, cs, ss = _oracle_decode(p, inp)
+        assert_f32_output_close(to_np(out), ref_o)
+        assert np.array_equal(to_np(conv), cs), f"replay {rep}: conv state"
+        assert state_rel_err(to_np(ssm), ss) <= 1e-4, f"replay {rep}"
+        # eager work between replays on the same context
+        c2, s2 = conv.clone(), ssm.clone()
+        qff.deltanet_decode(ctx, pg, qkv, z, a, b, c2, s2)
+        torch.cuda.synchronize()
