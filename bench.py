@@ -484,17 +484,128 @@ def copy_probe():
     torch.cuda.synchronize()
 
 
-def traffic_for(kernel):
-    """HBM bytes per launch of `kernel` from the committed counter summary
-    (profiles/traffic_c1.json, FETCH_SIZE + WRITE_SIZE scaled by the copy
-    probe), or None when it holds no figure for that kernel."""
-    path = os.path.join(ROOT, "profiles", "traffic_c1.json")
+COUNTERS_JSON = os.path.join(ROOT, "profiles", "counters.json")
+
+
+def traffic_for(kernel, workload="c1"):
+    """HBM bytes per launch of `kernel` in `workload` from the committed
+    counter summary (profiles/counters.json: FETCH_SIZE + WRITE_SIZE scaled
+    by the copy probe), or None when it holds no figure for that kernel."""
     try:
-        with open(path) as f:
-            rec = json.load(f)
-        return rec["kernels"][kernel]["bytes_per_launch"]
-    except (OSError, KeyError, ValueError):
+        with open(COUNTERS_JSON) as f:
+            W = json.load(f)["workloads"][workload]
+        hits = [r for k, r in W.items() if k.split("@")[0] == kernel and "traffic_bytes" in r]
+        return hits[0]["traffic_bytes"] if len(hits) == 1 else None
+    except (OSError, KeyError, ValueError, TypeError):
         return None
+
+
+def _kernel_key(name):
+    """qff::dn_chunk_state_kernel<...>(...) -> dn_chunk_state; torch's
+    elementwise negation (the copy probe) -> copy_probe; other kernels keep
+    the first 60 characters of their name."""
+    if "qff::" in name:
+        n = name.split("qff::", 1)[1].split("(")[0].split("<")[0].strip()
+        return n[:-len("_kernel")] if n.endswith("_kernel") else n
+    if "neg" in name and "elementwise" in name:
+        return "copy_probe"
+    return name[:60]
+
+
+def _geometry(gx, gy, gz, wx, wy, wz):
+    """'workgroups x.y.z / threads' of a dispatch (rocprofv3 grid sizes
+    count work-items)."""
+    g = [a // b if b and a % b == 0 else a for a, b in ((gx, wx), (gy, wy), (gz, wz))]
+    return f"{g[0]}.{g[1]}.{g[2]}/{wx * wy * wz}"
+
+
+def summarize_trace(db, out_md, title, command):
+    """Kernel-trace summary of one rocprofv3 --kernel-trace database as a
+    markdown table: one row per (kernel, launch geometry), calls and
+    dispatch durations in microseconds, sorted by total time."""
+    import sqlite3
+    con = sqlite3.connect(db)
+    rows = {}
+    for name, start, end, gx, gy, gz, wx, wy, wz in con.execute(
+            "select S.display_name, K.start, K.end, K.grid_size_x, K.grid_size_y, K.grid_size_z,"
+            " K.workgroup_size_x, K.workgroup_size_y, K.workgroup_size_z from rocpd_kernel_dispatch K"
+            " join rocpd_info_kernel_symbol S on S.id = K.kernel_id and S.guid = K.guid"):
+        short = name.split("(")[0].replace("void ", "").strip()
+        key = (short, _geometry(gx, gy, gz, wx, wy, wz))
+        rows.setdefault(key, []).append((end - start) / 1000.0)
+    con.close()
+    total = sum(sum(v) for v in rows.values()) or 1.0
+    lines = [f"# {title}", "", "Command:", "", "    " + command, "",
+             "One row per kernel and launch geometry (workgroups x.y.z / threads per workgroup); "
+             "durations are rocprofv3 dispatch times in microseconds.", "",
+             "| kernel | geometry | calls | avg us | min us | max us | % of kernel time |",
+             "|---|---|---:|---:|---:|---:|---:|"]
+    for (k, g), v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {k} | {g} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
+                     f"{100.0 * sum(v) / total:.1f} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
+def summarize_pmc(root, out_json):
+    """Per-kernel means of the counter passes under `root` (one rocprofv3
+    --pmc output directory per pass, named <pass>_<workload>, pass one of
+    mfma / fetch / write) into `out_json`. FETCH_SIZE and WRITE_SIZE are
+    scaled to bytes by what the same counter reads for the copy probe of the
+    same run (COPY_PROBE_BYTES read and written); MFMA flops are the MOPS
+    counters x 512; MFMA utilisation is busy cycles over GUI-active cycles of
+    every SIMD."""
+    import glob
+    import sqlite3
+    res = {"copy_probe_bytes": COPY_PROBE_BYTES, "factors": {}, "workloads": {}}
+    for d in sorted(glob.glob(os.path.join(root, "*_*"))):
+        if not os.path.isdir(d):
+            continue
+        kind, wl = os.path.basename(d).split("_", 1)
+        dbs = glob.glob(os.path.join(d, "**", "*.db"), recursive=True)
+        if not dbs:
+            continue
+        sums, disp = {}, {}
+        for db in dbs:
+            con = sqlite3.connect(db)
+            for did, kname, cname, val, gx, gy, gz, wx, wy, wz in con.execute(
+                    "select dispatch_id, kernel_name, counter_name, value, grid_size_x, grid_size_y, grid_size_z,"
+                    " workgroup_size_x, workgroup_size_y, workgroup_size_z from counters_collection"):
+                k = _kernel_key(kname)
+                if k != "copy_probe":
+                    k += "@" + _geometry(gx, gy, gz, wx, wy, wz)
+                sums[(k, cname)] = sums.get((k, cname), 0.0) + float(val)
+                disp.setdefault((k, cname), set()).add((db, did))
+            con.close()
+        mean = {key: v / len(disp[key]) for key, v in sums.items()}
+        W = res["workloads"].setdefault(wl, {})
+        for (k, cname), v in mean.items():
+            rec = W.setdefault(k, {})
+            rec[cname] = v
+            rec.setdefault("dispatches", {})[kind] = len(disp[(k, cname)])
+        if kind in ("fetch", "write"):
+            cname = "FETCH_SIZE" if kind == "fetch" else "WRITE_SIZE"
+            probe = [v for (k, c), v in mean.items() if c == cname and k == "copy_probe"]
+            if probe:
+                res["factors"].setdefault(wl, {})[cname] = COPY_PROBE_BYTES / 1024.0 / probe[0]
+    for wl, W in res["workloads"].items():
+        f = res["factors"].get(wl, {})
+        for k, rec in W.items():
+            if "FETCH_SIZE" in rec and "FETCH_SIZE" in f:
+                rec["read_bytes"] = rec["FETCH_SIZE"] * 1024.0 * f["FETCH_SIZE"]
+            if "WRITE_SIZE" in rec and "WRITE_SIZE" in f:
+                rec["write_bytes"] = rec["WRITE_SIZE"] * 1024.0 * f["WRITE_SIZE"]
+            if "read_bytes" in rec and "write_bytes" in rec:
+                rec["traffic_bytes"] = rec["read_bytes"] + rec["write_bytes"]
+            mops = sum(rec.get(c, 0.0) for c in ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16",
+                                                   "SQ_INSTS_VALU_MFMA_MOPS_F32"))
+            if mops:
+                rec["mfma_flops"] = mops * 512.0
+            if "MfmaUtil" in rec:
+                rec["mfma_util_pct"] = rec["MfmaUtil"]
+    with open(out_json, "w") as fh:
+        json.dump(res, fh, indent=1, sort_keys=True)
+    return res
 
 
 def main():
@@ -506,7 +617,18 @@ def main():
     ap.add_argument("--only", default="", help="comma list of c0,c1,c2,c3,c4,dnb,rt")
     ap.add_argument("--copy-probe", action="store_true", help="also run one copy of known size "
                     "(calibrates FETCH_SIZE / WRITE_SIZE in a counter run)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("DIR", "OUT_JSON"),
+                    help="summarise rocprofv3 --pmc pass directories DIR/<pass>_<workload> into OUT_JSON "
+                    "and exit (no GPU work)")
+    ap.add_argument("--summarize-trace", nargs=4, metavar=("DB", "OUT_MD", "TITLE", "COMMAND"),
+                    help="summarise a rocprofv3 --kernel-trace database into a markdown table and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1])
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         sys.exit(2)
