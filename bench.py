@@ -701,7 +701,13 @@ def main():
                    "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)"},
         "roofline": roof, "cpu_baseline": cpu, "configs": configs,
     }
-    print(json.dumps(line))
+    # leave nothing behind on the GPU: the context's workspace and torch's
+    # cached blocks are released before the line is printed and the
+    # process exits
+    torch.cuda.synchronize()
+    ctx.close()
+    torch.cuda.empty_cache()
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

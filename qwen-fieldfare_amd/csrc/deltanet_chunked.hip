@@ -82,7 +82,7 @@ template <int IN_DT>
 struct UnitIn {
     RawPair<IN_DT> r[3][11];
     float4 w[3][2];
-    float av, bv;
+    float av, bv, alog, dtb;
 };
 
 __device__ __forceinline__ void unit_coords(int u, int& c, int& h) {
@@ -93,6 +93,7 @@ __device__ __forceinline__ void unit_coords(int u, int& c, int& h) {
 template <int IN_DT>
 __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, const void* __restrict__ qkv,
                                            const float* __restrict__ a, const float* __restrict__ b,
+                                           const float* __restrict__ a_log, const float* __restrict__ dt_bias,
                                            const float* __restrict__ conv_w, const float* __restrict__ conv_state,
                                            int wave, int lane) {
     int c, h;
@@ -112,6 +113,8 @@ __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, cons
     const size_t gi = static_cast<size_t>(min(t0 + lane, T - 1)) * 32 + h;
     in.av = a[gi];
     in.bv = b[gi];
+    in.alog = a_log[h];
+    in.dtb = dt_bias[h];
 }
 
 // Conv inputs e[i][c] of pass p, channels ch + c, at positions tw-3+i: the
@@ -133,6 +136,9 @@ __device__ __forceinline__ void unit_rows(const UnitIn<IN_DT>& in, int p, int tw
             e[i][0] = conv_state[ch * 4 + 1 + i];
             e[i][1] = conv_state[(ch + 1) * 4 + 1 + i];
         }
+        // waited for here, on the one wave that reads them: a wait after the
+        // branch would hold every wave until the previous unit's stores drain
+        __builtin_amdgcn_s_waitcnt(0);
     }
 }
 
@@ -254,7 +260,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 
     int u = blockIdx.x, un = blockIdx.x + grid;
     UnitIn<IN_DT> in;
-    fetch_unit<IN_DT>(in, u, T, qkv, a, b, conv_w, conv_state, threadIdx.x >> 6, threadIdx.x & 63);
+    fetch_unit<IN_DT>(in, u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, threadIdx.x >> 6, threadIdx.x & 63);
     if (threadIdx.x == 0) s_next = 2 * grid + static_cast<int>(atomicAdd(sched, 1u));
     // Wait here for the first unit's loads: the loop's own waits then only
     // count the operations of the previous iteration, which issues stores
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     // tokens have log g = 0 and beta = 0, so they change nothing.
     if (wave == 0) {
         const bool ok = lane < nv;
-        float x = ok ? -expf(a_log[h]) * softplus(in.av + dt_bias[h]) : 0.0f;
+        float x = ok ? -expf(in.alog) * softplus(in.av + in.dtb) : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o, 64);
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     // the unit after next, and the next unit's inputs (the unit index is
     // clamped, so the loads stay in bounds when the queue has run out)
     const int unn = s_next;
-    fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, conv_w, conv_state, wave, lane);
+    fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, wave, lane);
     __syncthreads();
     // grabbed now, published at the end of the unit, when it has long arrived
     unsigned grabbed = 0;
