@@ -70,24 +70,25 @@ template <> struct RawPair<0> {
     __device__ __forceinline__ float hi() const { return v.y; }
 };
 
-// Everything one (chunk, value head) unit reads from global memory, for one
+// Everything one (chunk, key head) unit reads from global memory, for one
 // thread (wave w: tokens 8w .. 8w+7 of the chunk; lane l: channels 2l, 2l+1
-// of the q, k and v blocks): the conv input rows at positions tok-3 ..
-// tok+7 clamped into [0, T), the conv weights and the gate inputs of
-// token lane. Every load is unconditional and in bounds, so the loads of the
-// next unit can be issued while the current one is processed and the
-// compiler's vmcnt accounting stays exact. (The conv-state slots that
-// chunk 0 needs are read when that unit is processed.)
+// of the key head's q and k blocks and of the v blocks of its two value
+// heads): the conv input rows at positions tok-3 .. tok+7 clamped into
+// [0, T), the conv weights, and per value head the gate inputs of token
+// lane and the head's A_log and dt_bias. Every load is unconditional and in
+// bounds, so the loads of the next unit can be issued while the current one
+// is processed and the compiler's vmcnt accounting stays exact. (The
+// conv-state slots that chunk 0 needs are read when that unit is processed.)
 template <int IN_DT>
 struct UnitIn {
-    RawPair<IN_DT> r[3][11];
-    float4 w[3][2];
-    float av, bv, alog, dtb;
+    RawPair<IN_DT> r[4][11];
+    float4 w[4][2];
+    float av[2], bv[2], alog[2], dtb[2];
 };
 
-__device__ __forceinline__ void unit_coords(int u, int& c, int& h) {
-    c = u >> 5;
-    h = u & 31;
+__device__ __forceinline__ void unit_coords(int u, int& c, int& kh) {
+    c = u >> 4;
+    kh = u & 15;
 }
 
 template <int IN_DT>
@@ -96,12 +97,13 @@ __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, cons
                                            const float* __restrict__ a_log, const float* __restrict__ dt_bias,
                                            const float* __restrict__ conv_w, const float* __restrict__ conv_state,
                                            int wave, int lane) {
-    int c, h;
-    unit_coords(u, c, h);
-    const int kh = h >> 1, t0 = c * kC, tw = t0 + 8 * wave;
-    const int chs[3] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + h * 128 + 2 * lane};
+    int c, kh;
+    unit_coords(u, c, kh);
+    const int t0 = c * kC, tw = t0 + 8 * wave;
+    const int chs[4] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + 2 * kh * 128 + 2 * lane,
+                        4096 + (2 * kh + 1) * 128 + 2 * lane};
 #pragma unroll
-    for (int p = 0; p < 3; ++p) {
+    for (int p = 0; p < 4; ++p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) in.w[p][j] = reinterpret_cast<const float4*>(conv_w)[chs[p] + j];
 #pragma unroll
@@ -110,11 +112,14 @@ __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, cons
             in.r[p][i].load(qkv, static_cast<size_t>(pos) * 8192 + chs[p]);
         }
     }
-    const size_t gi = static_cast<size_t>(min(t0 + lane, T - 1)) * 32 + h;
-    in.av = a[gi];
-    in.bv = b[gi];
-    in.alog = a_log[h];
-    in.dtb = dt_bias[h];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const size_t gi = static_cast<size_t>(min(t0 + lane, T - 1)) * 32 + 2 * kh + hh;
+        in.av[hh] = a[gi];
+        in.bv[hh] = b[gi];
+        in.alog[hh] = a_log[2 * kh + hh];
+        in.dtb[hh] = dt_bias[2 * kh + hh];
+    }
 }
 
 // Conv inputs e[i][c] of pass p, channels ch + c, at positions tw-3+i: the
@@ -211,29 +216,85 @@ __device__ __forceinline__ void unswz(int p, int& r, int& k8) {
     k8 = (q % (K / 32)) * 4 + ((p >> 4) & 3);
 }
 
+// bf16x3 block product like mma_block_x3 (NN), with the k elements of A
+// scaled by asc[k] on the way in: the A operand (hi, lo) is recombined,
+// scaled in fp32 and split again (exact to ~2^-16 like the operands
+// themselves).
+template <int K, int NC>
+__device__ __forceinline__ void mma_block_x3_ascale(f32x4_t (&acc)[1][NC], const uint16_t* ah, const uint16_t* al,
+                                                    int lda, int ar, const float* asc, const uint16_t* bh,
+                                                    const uint16_t* bl, int ldb, int bc, int lane) {
+    const int n = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        const int ao = (ar + n) * lda + k0 + 8 * kb;
+        const u32x4_t h = *reinterpret_cast<const u32x4_t*>(ah + ao);
+        const u32x4_t l = *reinterpret_cast<const u32x4_t*>(al + ao);
+        const float4 s0 = *reinterpret_cast<const float4*>(asc + k0 + 8 * kb);
+        const float4 s1 = *reinterpret_cast<const float4*>(asc + k0 + 8 * kb + 4);
+        const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        u32x4_t a_h, a_l;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x0 = (__uint_as_float(h[e] << 16) + __uint_as_float(l[e] << 16)) * sc[2 * e];
+            const float x1 = (__uint_as_float(h[e] & 0xffff0000u) + __uint_as_float(l[e] & 0xffff0000u)) * sc[2 * e + 1];
+            uint32_t hw, lw;
+            split_bf16x2(x0, x1, hw, lw);
+            a_h[e] = hw;
+            a_l[e] = lw;
+        }
+        u32x4_t b_h[NC], b_l[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int bo = (k0 + 8 * kb + (n >> 2)) * ldb + bc + 16 * c + 4 * (n & 3);
+            const u32x2_t h0 = lds_read_tr16(bh + bo), h1 = lds_read_tr16(bh + bo + 4 * ldb);
+            const u32x2_t l0 = lds_read_tr16(bl + bo), l1 = lds_read_tr16(bl + bo + 4 * ldb);
+            b_h[c] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+            b_l[c] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_l, b_h[c], acc[0][c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_h, b_l[c], acc[0][c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_h, b_h[c], acc[0][c]);
+    }
+}
+
+// Packed lower triangle (j <= i) of a 64 x 64 matrix.
+__device__ __forceinline__ int tri(int i, int j) { return i * (i + 1) / 2 + j; }
+
 // LDS carve-up of the chunk-local kernel (bytes)
 constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
-constexpr int kOffK = 0;                          // K hi, lo; then X = beta e^G K; then P W, Qe (fp32)
+constexpr int kOffK = 0;                          // K hi, lo (both value heads)
 constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T (fp32) + scratch; then W hi, lo
-constexpr int kOffV = 4 * kTile128;               // beta V hi, lo
+constexpr int kOffV = 4 * kTile128;               // beta V hi, lo; then P W, Qe (fp32 [64][132])
 constexpr int kOffA = 6 * kTile128;               // A fp32 [64][65]
 constexpr int kOffT = kOffA + kC * 65 * 4;        // P hi, lo, then T hi, lo, then P again: [64][72]
-constexpr int kOffG = kOffT + 2 * kC * kLT * 2;   // G[64], beta[64]
-constexpr int kLocalSmem = kOffG + 2 * kC * 4;
+constexpr int kTri = kC * (kC + 1) / 2;           // packed lower triangle
+constexpr int kOffR = kOffT + 2 * kC * kLT * 2;   // raw K K^T and Q K^T lower triangles (fp32)
+constexpr int kOffG = kOffR + 2 * kTri * 4;       // per value head: G[64], beta[64], beta e^G [64]
+constexpr int kLocalSmem = kOffG + 2 * 3 * kC * 4;
 
 // Persistent: grid = min(units, CUs) workgroups of 512 threads (eight
-// waves, two per SIMD) walk the (chunk, value head) units. Units 0 .. 2g-1
+// waves, two per SIMD) walk the (chunk, key head) units. Units 0 .. 2g-1
 // go out statically (g = grid size), the rest through an atomic counter, so
 // a workgroup on a CU that runs slow (or shares its XCD with other work)
 // simply takes fewer units; the launch's last workgroup resets the counter.
-// While a unit is processed the inputs of the workgroup's next unit are
-// already loading into registers (UnitIn).
+// A key head's q and k feed both of its value heads, so a unit runs the
+// conv, norms and the Gram products K K^T and Q K^T once and keeps the raw
+// products (packed lower triangles) for the second head, whose A and P
+// differ only by the per-head gates. Per value head: K~^T out, beta V, A
+// and P, T = (I + A)^-1, W = T diag(beta e^G) K (the scaling applied to T's
+// operand, so K stays as it is for the other head), U~ = T (beta V), P W
+// and Qe. While a unit is processed the inputs of the workgroup's next unit
+// are already loading into registers (UnitIn), issued once the second
+// head's v has been convolved.
 // Conv passes map wave w to tokens 8w .. 8w+7 and lane l to channels 2l,
 // 2l+1 of a 128-channel block, so a lane's 8 tokens of a channel are one
 // K~^T operand piece and each conv input row is one 256-B load per wave.
-// Every global load of a unit is issued before its first global store: on
-// gfx950 vmcnt counts stores too, so a load consumed after stores would
-// wait for them.
+// Global loads are issued before the stores of the same head (vmcnt counts
+// stores too on gfx950, so a load consumed after stores would wait for them).
 constexpr int kLocalThreads = 512;
 
 template <int IN_DT>
@@ -241,7 +302,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     int T, const void* __restrict__ qkv, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ a_log, const float* __restrict__ dt_bias, const float* __restrict__ conv_w,
     const float* __restrict__ conv_state, qff_dn_bufs out, unsigned* __restrict__ sched) {
-    const int units = ((T + kC - 1) / kC) * 32;
+    const int units = ((T + kC - 1) / kC) * 16;
     const int grid = gridDim.x;
 
     __shared__ __attribute__((aligned(16))) unsigned char smem[kLocalSmem];
@@ -255,8 +316,11 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     float* Am = reinterpret_cast<float*>(smem + kOffA);
     uint16_t* Th = reinterpret_cast<uint16_t*>(smem + kOffT);
     uint16_t* Tl = Th + kC * kLT;
-    float* G = reinterpret_cast<float*>(smem + kOffG);
-    float* Bt = G + kC;
+    float* KKr = reinterpret_cast<float*>(smem + kOffR);
+    float* QKr = KKr + kTri;
+    float* Gs = reinterpret_cast<float*>(smem + kOffG);   // [hh][64]
+    float* Bs = Gs + 2 * kC;                              // [hh][64]
+    float* Ss = Bs + 2 * kC;                              // [hh][64]: beta e^G
 
     int u = blockIdx.x, un = blockIdx.x + grid;
     UnitIn<IN_DT> in;
@@ -277,30 +341,35 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     const int lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
     const int rt = wave & 3, role = wave >> 2;   // MFMA row tile; which of a wave pair's two products
-    int c, h;
-    unit_coords(u, c, h);
-    const int kh = h >> 1;
+    int c, kh;
+    unit_coords(u, c, kh);
     const int t0 = c * kC;
     const int nv = min(kC, T - t0);
-    const size_t ch = static_cast<size_t>(u);    // == c * 32 + h
     const int tw = t0 + 8 * wave;                  // this wave's first token
 
-    // gates (deltanet.metal:250-280): log g = -e^{A_log} softplus(a + dt_bias),
-    // beta = sigmoid(b); G = inclusive prefix sum over the chunk. Padded
-    // tokens have log g = 0 and beta = 0, so they change nothing.
-    if (wave == 0) {
+    // gates (deltanet.metal:250-280), waves 0 and 1 one value head each:
+    // log g = -e^{A_log} softplus(a + dt_bias), beta = sigmoid(b); G =
+    // inclusive prefix sum over the chunk. Padded tokens have log g = 0 and
+    // beta = 0, so they change nothing.
+    if (wave < 2) {
+        const int hh = wave;
         const bool ok = lane < nv;
-        float x = ok ? -expf(in.alog) * softplus(in.av + in.dtb) : 0.0f;
+        const float av = hh ? in.av[1] : in.av[0], bv = hh ? in.bv[1] : in.bv[0];
+        const float alog = hh ? in.alog[1] : in.alog[0], dtb = hh ? in.dtb[1] : in.dtb[0];
+        float x = ok ? -expf(alog) * softplus(av + dtb) : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o, 64);
             if (lane >= o) x += y;
         }
-        G[lane] = x;
-        Bt[lane] = ok ? sigmoid(in.bv) : 0.0f;
-        if (lane == 63) out.gam[ch] = expf(x);
+        const float beta = ok ? sigmoid(bv) : 0.0f;
+        Gs[hh * kC + lane] = x;
+        Bs[hh * kC + lane] = beta;
+        Ss[hh * kC + lane] = beta * __builtin_amdgcn_exp2f(x * kLog2e);
+        if (lane == 63) out.gam[static_cast<size_t>(c) * 32 + 2 * kh + hh] = expf(x);
     }
-    const int chs[3] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + h * 128 + 2 * lane};
+    const int chs[4] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + 2 * kh * 128 + 2 * lane,
+                        4096 + (2 * kh + 1) * 128 + 2 * lane};
     const bool tail = t0 + kC > T;
     auto conv = [&](int p, float (&y)[8][2]) {
         float e[11][2];
@@ -332,28 +401,46 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             *reinterpret_cast<uint32_t*>(dl + o) = ll;
         }
     };
-    float qn[8][2], kn[8][2], vn[8][2];
-    conv(0, qn);
-    norm_store(qn, 0.08838834764831845f, Qh, Ql);   // 1 / sqrt(128)
-    conv(1, kn);
-    norm_store(kn, 1.0f, Kh, Kl);
-    conv(2, vn);
-    // the unit after next, and the next unit's inputs (the unit index is
-    // clamped, so the loads stay in bounds when the queue has run out)
-    const int unn = s_next;
-    fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, wave, lane);
+    // (k is kept in LDS only: K~^T is formed from the hi/lo copy)
+    float qn[8][2], vn[2][8][2];
+    {
+        float kn[8][2];
+        conv(0, qn);
+        norm_store(qn, 0.08838834764831845f, Qh, Ql);   // 1 / sqrt(128)
+        conv(1, kn);
+        norm_store(kn, 1.0f, Kh, Kl);
+    }
+    conv(2, vn[0]);
+    conv(3, vn[1]);
     __syncthreads();
+
     // grabbed now, published at the end of the unit, when it has long arrived
     unsigned grabbed = 0;
     if (t == 0) grabbed = atomicAdd(sched, 1u);
+    int unn = 0;
+
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+    const int h = 2 * kh + hh;
+    const size_t ch = static_cast<size_t>(c) * 32 + h;   // (chunk, value head) record
+    const float* G = Gs + hh * kC;
+    const float* Bt = Bs + hh * kC;
 
     // ---- K~^T out (channels 2l, 2l+1 x this wave's 8 tokens: one operand
-    // piece each), beta v to LDS, Q~ = e^G q kept for Qe ------------------------
+    // piece each), beta v to LDS; A and P -------------------------------------
     {
         const float gc = G[kC - 1];
         float gw[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) gw[i] = G[8 * wave + i];
+        float kn[8][2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t kh2 = *reinterpret_cast<const uint32_t*>(Kh + (8 * wave + i) * kLD + 2 * lane);
+            const uint32_t kl2 = *reinterpret_cast<const uint32_t*>(Kl + (8 * wave + i) * kLD + 2 * lane);
+            kn[i][0] = __uint_as_float(kh2 << 16) + __uint_as_float(kl2 << 16);
+            kn[i][1] = __uint_as_float(kh2 & 0xffff0000u) + __uint_as_float(kl2 & 0xffff0000u);
+        }
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             uint32_t hw[4], lw[4];
@@ -368,25 +455,24 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float bb = Bt[8 * wave + i];
-            uint32_t hh, ll;
-            split_bf16x2(bb * vn[i][0], bb * vn[i][1], hh, ll);
+            uint32_t hq, lq;
+            split_bf16x2(bb * vn[hh][i][0], bb * vn[hh][i][1], hq, lq);
             const int o = (8 * wave + i) * kLD + 2 * lane;
-            *reinterpret_cast<uint32_t*>(Vh + o) = hh;
-            *reinterpret_cast<uint32_t*>(Vl + o) = ll;
-            const float eg = __builtin_amdgcn_exp2f(gw[i] * kLog2e);
-            qn[i][0] *= eg;
-            qn[i][1] *= eg;
+            *reinterpret_cast<uint32_t*>(Vh + o) = hq;
+            *reinterpret_cast<uint32_t*>(Vl + o) = lq;
         }
     }
-    __syncthreads();
-
-    // ---- waves 0-3: K K^T -> A (strictly lower, scaled); waves 4-7: Q K^T ->
-    // P (lower incl. diagonal); row tile rt each ---------------------------------
+    // waves 0-3: K K^T -> A (strictly lower, scaled); waves 4-7: Q K^T -> P
+    // (lower incl. diagonal); row tile rt each. The first head forms the
+    // products and keeps them raw; the second reads them back.
     {
         f32x4_t acc[1][4];
+        if (hh == 0) {
 #pragma unroll
-        for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
+            for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
+        }
+        float* raw = role ? QKr : KKr;
         float gi[4], bi[4], gj[4];
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
@@ -400,15 +486,22 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
                 const int i = 16 * rt + 4 * kb + ii;
+                float g;
+                if (hh == 0) {
+                    g = acc[0][cj][ii];
+                    if (j <= i) raw[tri(i, j)] = g;
+                } else {
+                    g = j <= i ? raw[tri(i, j)] : 0.0f;
+                }
                 // e^{G_i - G_j}; for j > i the product is discarded by the select
-                const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * acc[0][cj][ii];
+                const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * g;
                 if (role == 0) {
                     Am[i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
                 } else {
-                    uint16_t hh, ll;
-                    split_bf16(j <= i ? v : 0.0f, hh, ll);
-                    Th[i * kLT + j] = hh;
-                    Tl[i * kLT + j] = ll;
+                    uint16_t hq, lq;
+                    split_bf16(j <= i ? v : 0.0f, hq, lq);
+                    Th[i * kLT + j] = hq;
+                    Tl[i * kLT + j] = lq;
                 }
             }
         }
@@ -424,7 +517,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         pkeep[1] = *reinterpret_cast<const u32x4_t*>(Tl + row * kLT + 8 * k8);
         // P and Qe are read only by the output pass, after the state pass:
         // streamed past the caches so that W, K~ and U~, which the state pass
-        // reads next, stay in the last-level cache (state pass 107 -> 90 us)
+        // reads next, stay in the last-level cache
         __builtin_nontemporal_store(pkeep[0], reinterpret_cast<u32x4_t*>(out.ph + ch * kC * kC + 8 * t));
         __builtin_nontemporal_store(pkeep[1], reinterpret_cast<u32x4_t*>(out.pl + ch * kC * kC + 8 * t));
     }
@@ -440,10 +533,10 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             float tc[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                float ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < i; ++j) acc[j & 3] = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], acc[j & 3]);
-                tc[i] = (i == lane ? 1.0f : 0.0f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
+                for (int j = 0; j < i; ++j) ac[j & 3] = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], ac[j & 3]);
+                tc[i] = (i == lane ? 1.0f : 0.0f) - ((ac[0] + ac[1]) + (ac[2] + ac[3]));
                 Tm[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
             }
         }
@@ -459,11 +552,11 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     if (wave < 3) {
         const int bj = wave;
         for (int bi = bj + 1; bi < 4; ++bi) {
-            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            f32x4_t ac = f32x4_t{0.f, 0.f, 0.f, 0.f};
             for (int bk = bj; bk < bi; ++bk)
-                acc = mm16_f32(Am + (16 * bi) * 65 + 16 * bk, 65, Tm + (16 * bk) * 65 + 16 * bj, 65, acc, lane);
+                ac = mm16_f32(Am + (16 * bi) * 65 + 16 * bk, 65, Tm + (16 * bk) * 65 + 16 * bj, 65, ac, lane);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) scr[(4 * kb + ii) * 17 + n] = acc[ii];
+            for (int ii = 0; ii < 4; ++ii) scr[(4 * kb + ii) * 17 + n] = ac[ii];
             __builtin_amdgcn_wave_barrier();
             const f32x4_t res = mm16_f32(Tm + (16 * bi) * 65 + 16 * bi, 65, scr, 17,
                                          f32x4_t{0.f, 0.f, 0.f, 0.f}, lane);
@@ -473,32 +566,26 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         }
     }
     __syncthreads();
-    // ---- T -> bf16 hi/lo; X = beta e^G K in place of K --------------------------
+    if (hh == 1) {
+        // the next unit's inputs (the unit index is clamped, so the loads stay
+        // in bounds when the queue has run out), early enough to land before
+        // it starts and late enough to keep them out of the registers of
+        // the rest of the unit
+        unn = s_next;
+        fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, wave, lane);
+    }
+    // ---- T -> bf16 hi/lo ----------------------------------------------------
     for (int idx = t; idx < kC * kC; idx += kLocalThreads) {
         const int i = idx >> 6, j = idx & 63;
-        uint16_t hh, ll;
-        split_bf16(Tm[i * 65 + j], hh, ll);
-        Th[i * kLT + j] = hh;
-        Tl[i * kLT + j] = ll;
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int q = t + kLocalThreads * k, row = q >> 4, c8 = 8 * (q & 15);
-        const float s = Bt[row] * __builtin_amdgcn_exp2f(G[row] * kLog2e);
-        const u32x4_t hv = *reinterpret_cast<const u32x4_t*>(Kh + row * kLD + c8);
-        const u32x4_t lv = *reinterpret_cast<const u32x4_t*>(Kl + row * kLD + c8);
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            x[2 * e] = s * (__uint_as_float(hv[e] << 16) + __uint_as_float(lv[e] << 16));
-            x[2 * e + 1] = s * (__uint_as_float(hv[e] & 0xffff0000u) + __uint_as_float(lv[e] & 0xffff0000u));
-        }
-        store_split8(Kh + row * kLD + c8, Kl + row * kLD + c8, x);
+        uint16_t hq, lq;
+        split_bf16(Tm[i * 65 + j], hq, lq);
+        Th[i * kLT + j] = hq;
+        Tl[i * kLT + j] = lq;
     }
     __syncthreads();
-    // ---- waves 0-3: W = T X -> LDS (Q region); waves 4-7: U~ = T (beta V) ->
-    // U~^T out. Row tile rt (16 tokens), 8 column tiles of 16 dims in two
-    // halves. -----------------------------------------------------------------
+    // ---- waves 0-3: W = T diag(beta e^G) K -> LDS (Q region); waves 4-7:
+    // U~ = T (beta V) -> U~^T out. Row tile rt (16 tokens), 8 column tiles of
+    // 16 dims in two halves. -------------------------------------------------
     uint16_t* Wh = Qh;
     uint16_t* Wl = Ql;
 #pragma unroll
@@ -506,7 +593,10 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         f32x4_t w[1][4];
 #pragma unroll
         for (int cd = 0; cd < 4; ++cd) w[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * rt, role ? Vh : Kh, role ? Vl : Kl, kLD, 64 * half, lane);
+        if (role == 0)
+            mma_block_x3_ascale<kC, 4>(w, Th, Tl, kLT, 16 * rt, Ss + hh * kC, Kh, Kl, kLD, 64 * half, lane);
+        else
+            mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * rt, Vh, Vl, kLD, 64 * half, lane);
 #pragma unroll
         for (int cd = 0; cd < 4; ++cd) {
             const int d = 64 * half + 16 * cd + n;
@@ -548,9 +638,9 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         *reinterpret_cast<u32x4_t*>(Tl + row * kLT + 8 * k8) = pkeep[1];
     }
     __syncthreads();
-    // ---- P W -> fp32 [64][132] in the K region (X is consumed); wave -> row
-    // tile rt, column half `role` -----------------------------------------------
-    float* PW = reinterpret_cast<float*>(smem + kOffK);
+    // ---- P W -> fp32 [64][132] in the V region (beta V is consumed); wave ->
+    // row tile rt, column half `role` -------------------------------------------
+    float* PW = reinterpret_cast<float*>(smem + kOffV);
     {
         f32x4_t pw[1][4];
 #pragma unroll
@@ -563,12 +653,13 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
                 PW[(16 * rt + 4 * kb + ii) * 132 + 64 * role + 16 * cd + n] = pw[0][cd][ii];
     }
     __syncthreads();
-    // ---- Qe = Q~ - P W, in place (each thread its own channel pairs) -----------
+    // ---- Qe = e^G q - P W, in place (each thread its own channel pairs) --------
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+        const float eg = __builtin_amdgcn_exp2f(G[8 * wave + i] * kLog2e);
         float2* pp = reinterpret_cast<float2*>(PW + (8 * wave + i) * 132 + 2 * lane);
         const float2 pw = *pp;
-        *pp = make_float2(qn[i][0] - pw.x, qn[i][1] - pw.y);
+        *pp = make_float2(qn[i][0] * eg - pw.x, qn[i][1] * eg - pw.y);
     }
     __syncthreads();
     // ---- Qe out (coalesced) -----------------------------------------------------
@@ -583,10 +674,12 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
         const size_t o = ch * kC * 128 + 8 * p;
         uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) split_bf16x2(y[2 * k], y[2 * k + 1], hw[k], lw[k]);
+        for (int k2 = 0; k2 < 4; ++k2) split_bf16x2(y[2 * k2], y[2 * k2 + 1], hw[k2], lw[k2]);
         __builtin_nontemporal_store(u32x4_t{hw[0], hw[1], hw[2], hw[3]}, reinterpret_cast<u32x4_t*>(out.qeh + o));
         __builtin_nontemporal_store(u32x4_t{lw[0], lw[1], lw[2], lw[3]}, reinterpret_cast<u32x4_t*>(out.qel + o));
     }
+    __syncthreads();
+    }   // value heads
     if (t == 0) s_next = 2 * grid + static_cast<int>(grabbed);
     __syncthreads();
     u = un;
@@ -843,7 +936,7 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
     const int nch = (T + kC - 1) / kC;
     {
         ProfScope prof(ctx, stream, "dn_chunk_local");
-        const int units = nch * 32;
+        const int units = nch * 16;   // (chunk, key head)
         const int grid = std::min(units, std::max(ctx->num_cu, 1));
         unsigned* sched = ctx->sched + 2 * kSchedChunkLocal;
         if (in_dtype == QFF_BF16)
