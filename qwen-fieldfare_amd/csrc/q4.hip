@@ -92,6 +92,41 @@ struct Q4Parts {
     int n;
 };
 
+// The residual of element i of part p (0 without one), read early. Both
+// dtypes are loaded unconditionally, each from an in-bounds address (the
+// part's weights stand in for the one not needed), and selected: a branch
+// around a load would make the compiler wait for every load in flight at
+// the join.
+__device__ __forceinline__ float q4_res1(const Q4Parts& parts, int p, size_t i) {
+    const bool has = parts.res[p] != nullptr, bf = parts.ybf16[p] != 0;
+    const uint16_t* r16 = has && bf ? static_cast<const uint16_t*>(parts.res[p]) + i
+                                    : reinterpret_cast<const uint16_t*>(parts.w[p]);
+    const uint32_t* r32 = has && !bf ? static_cast<const uint32_t*>(parts.res[p]) + i : parts.w[p];
+    const uint32_t h = *r16, f = *r32;
+    return has ? __uint_as_float(bf ? h << 16 : f) : 0.0f;
+}
+// ... of elements i .. i+3, when ok (i a multiple of 4, so the loads are
+// aligned): one 8-B (bf16) and one 16-B (fp32) load
+__device__ __forceinline__ f32x4_t q4_res4(const Q4Parts& parts, int p, size_t i, bool ok) {
+    const bool has = ok && parts.res[p] != nullptr, bf = parts.ybf16[p] != 0;
+    const u32x2_t* r16 = has && bf ? reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(parts.res[p]) + i)
+                                   : reinterpret_cast<const u32x2_t*>(parts.w[p]);
+    const u32x4_t* r32 = has && !bf ? reinterpret_cast<const u32x4_t*>(static_cast<const float*>(parts.res[p]) + i)
+                                    : reinterpret_cast<const u32x4_t*>(parts.w[p]);
+    const u32x2_t a = *r16;
+    const u32x4_t b = *r32;
+    const f32x4_t r = bf ? f32x4_t{__uint_as_float(a[0] << 16), __uint_as_float(a[0] & 0xffff0000u),
+                                   __uint_as_float(a[1] << 16), __uint_as_float(a[1] & 0xffff0000u)}
+                         : f32x4_t{__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[2]),
+                                   __uint_as_float(b[3])};
+    return has ? r : f32x4_t{0.f, 0.f, 0.f, 0.f};
+}
+// y[i] of part p = v, in the part's output dtype
+__device__ __forceinline__ void q4_put(const Q4Parts& parts, int p, size_t i, float v) {
+    if (parts.ybf16[p]) elem<1>::store(parts.y[p], i, v);
+    else elem<0>::store(parts.y[p], i, v);
+}
+
 // y[i] of part p = v (+ residual[i]), in the part's output dtype
 __device__ __forceinline__ void q4_store(const Q4Parts& parts, int p, size_t i, float v) {
     const bool bf = parts.ybf16[p];
@@ -185,6 +220,17 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     // the weight and scale loads stay ahead of the x loads below, so the LDS
     // staging of the weights waits for them alone
     __builtin_amdgcn_sched_barrier(0);
+    // the residuals of the outputs this wave stores at the end (its tile
+    // wave of the RT x NBT output tiles, when it has one), requested now
+    // (rows a multiple of 4 and a 16-B aligned residual, so each lane's four
+    // rows are one aligned access; otherwise the store reads it itself)
+    const bool res_ok = (rows & 3) == 0 && (reinterpret_cast<uintptr_t>(parts.res[p]) & 15) == 0;
+    f32x4_t resv = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (RT * NBT <= kQ4GemvMaxWaves) {
+        const int tile = min(wave, RT * NBT - 1), rt = tile / NBT, bt = tile % NBT;
+        const int m = min(16 * bt + n, batch - 1), r = min(R0 + 16 * rt + 4 * kb, rows - 4);
+        resv = q4_res4(parts, p, res_ok ? static_cast<size_t>(m) * rows + r : 0, res_ok);
+    }
     // this lane's x (16 values per group and token tile): bf16 activations
     // for all GPW groups of its wave up front; fp32 ones (converted to bf16
     // as they arrive) group by group in the product loop. With NORM the
@@ -406,7 +452,11 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = R0 + 16 * rt + 4 * kb + j;
-                if (r < rows) q4_store(parts, p, static_cast<size_t>(m) * rows + r, v[j]);
+                if (r < rows) {
+                    const size_t i = static_cast<size_t>(m) * rows + r;
+                    if (RT * NBT <= kQ4GemvMaxWaves && tile == wave && res_ok) q4_put(parts, p, i, v[j] + resv[j]);
+                    else q4_store(parts, p, i, v[j]);
+                }
             }
         }
     }
@@ -484,6 +534,9 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
         if (NORM) q4_norm_weights<8>(nrm, 8 * ic, wn[k]);
     }
 
+    // the residual of the row this lane stores at the end (lanes 16 j store
+    // row R0 + j), requested now
+    const float resv = q4_res1(parts, p, static_cast<size_t>(min(R0 + (lane >> 4), rows - 1)));
     // weights and group constants of this wave's rows, all in flight
     u32x4_t wq[kQ4VecRows][KW];
     float sv[kQ4VecRows][KW], bv[kQ4VecRows][KW];
@@ -608,7 +661,7 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
     // lane 16 * (2 b5 + b4) holds row 2 b5 + b4
     if ((lane & 15) == 0) {
         const int r = R0 + (lane >> 4);
-        if (r < rows) q4_store(parts, p, r, q1);
+        if (r < rows) q4_put(parts, p, r, q1 + resv);
     }
 }
 
