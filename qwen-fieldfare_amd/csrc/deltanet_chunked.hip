@@ -18,18 +18,20 @@
 // sequential pass forms U and O from the same S0 in one step.
 //
 // Two kernels:
-//   dn_chunk_local_kernel  one workgroup per (chunk, value head), all chunks
-//       at once: conv1d + SiLU of the chunk's q, k, v channels straight from
-//       the projection (3 tokens of history from the input or the conv
-//       state), L2 norms, gates, then A, P, T (16x16 blocks: diagonal blocks
-//       by substitution, the rest on fp32 MFMAs), W, U~ and Qe; writes W, Qe,
-//       K~^T, U~^T, P (bf16 hi/lo) and e^{G_C}.
-//   dn_chunk_state_kernel  one workgroup per (block of RB state rows, value
-//       head) walks the chunks in order with its state rows in registers:
-//       U^T = U~^T - S W^T and O^T = S Qe^T + U~^T P^T in one pass over
-//       [S | U~^T], then S = e^{G_C} S + U^T K~. Its MFMA B operands are read
-//       from global memory straight into registers in operand layout, one
-//       chunk ahead.
+//   dn_chunk_local_kernel  persistent, one (chunk, key head) unit at a time
+//       from a work queue, all chunks independent: conv1d + SiLU of the
+//       chunk's q, k and both value heads' v channels straight from the
+//       projection (3 tokens of history from the input or the conv state),
+//       L2 norms, gates, the Gram products K K^T and Q K^T once for both
+//       value heads, then per value head A, P, T (16x16 blocks: diagonal
+//       blocks by substitution, the rest on fp32 MFMAs), W, U~ and Qe;
+//       writes W, Qe, K~^T, U~^T, P (bf16 hi/lo) and e^{G_C}.
+//   dn_chunk_state_kernel  one workgroup per (16 state rows, value head)
+//       walks the chunks in order with its state rows in registers, twelve
+//       waves in three roles: U = U~ - W S^T, S = e^{G_C} S + U^T K~ and the
+//       pre-norm output O^T = S Qe^T + U~^T P^T. Its MFMA operands come from
+//       global memory straight into registers in operand layout, one or two
+//       chunks ahead.
 // Every product runs as bf16x3 on v_mfma_f32_16x16x32_bf16 (a b ~ a_hi b_hi
 // + a_hi b_lo + a_lo b_hi, ~2^-16 relative per product), which keeps the
 // fp32 state within 1e-4 of the sequential fp32 recurrence; plain bf16
@@ -288,8 +290,10 @@ constexpr int kLocalSmem = kOffG + 2 * 3 * kC * 4;
 // and P, T = (I + A)^-1, W = T diag(beta e^G) K (the scaling applied to T's
 // operand, so K stays as it is for the other head), U~ = T (beta V), P W
 // and Qe. While a unit is processed the inputs of the workgroup's next unit
-// are already loading into registers (UnitIn), issued once the second
-// head's v has been convolved.
+// are already loading into registers (UnitIn), issued by the second head
+// once its T = (I + A)^-1 is complete (earlier, they would not fit the
+// registers of the rest of the unit: issuing them on the waves idle during
+// the off-diagonal solve spilled 170 registers).
 // Conv passes map wave w to tokens 8w .. 8w+7 and lane l to channels 2l,
 // 2l+1 of a 128-channel block, so a lane's 8 tokens of a channel are one
 // K~^T operand piece and each conv input row is one 256-B load per wave.
