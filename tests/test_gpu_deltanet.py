@@ -227,6 +227,54 @@ def test_deltanet_prefill_f32_inputs(hip, T):
         assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
 
 
+def test_deltanet_prefill_graph_replay(hip):
+    """The chunk-local pass takes its (chunk, key head) units from a work-queue
+    counter in the context that each launch's last workgroup resets. A
+    captured prefill (T = 200, four chunks with a ragged tail) is replayed
+    three times, each replay continuing from the conv state and state the
+    previous one left, with an eager prefill of another length on the same
+    context between replays: every replay's output, conv state and state
+    against the sequential oracle."""
+    import qff
+    p = synth.deltanet_params()
+    pg = _params_gpu(p)
+    ctx = qff.Context(max_batch=1, max_prefill_tokens=256)
+    T = 200
+    inp = synth.deltanet_prefill_inputs(T, seed=900)
+    qkv, z = bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"])
+    a, b = f32_tensor(inp["a"]), f32_tensor(inp["b"])
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = torch.empty(T, 4096, dtype=torch.bfloat16, device=DEV)
+    other = synth.deltanet_prefill_inputs(70, seed=901)
+    o_args = [bf16_tensor(other["qkv"]), bf16_tensor(other["z"]), f32_tensor(other["a"]), f32_tensor(other["b"])]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        # warm-up call outside the graph, on scratch copies of the state
+        qff.deltanet_prefill(ctx, pg, qkv, z, a, b, conv.clone(), ssm.clone(), out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    print(f"deltanet_prefill graph capture T={T}", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qff.deltanet_prefill(ctx, pg, qkv, z, a, b, conv, ssm, out=out)
+    x, zz = O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"])
+    cs, ss = inp["conv_state"], inp["ssm_state"]
+    for rep in range(3):
+        print(f"deltanet_prefill graph replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_o, cs, ss = O.deltanet_sequence(x, zz, inp["a"], inp["b"], p["a_log"], p["dt_bias"], p["conv_w"],
+                                            p["norm_w"], cs, ss)
+        assert_bf16_output_close(to_np(out), ref_o)
+        assert np.array_equal(to_np(conv), cs), f"replay {rep}: conv state"
+        assert state_rel_err(to_np(ssm), ss) <= 1e-4, f"replay {rep}"
+        # an eager prefill of another length on the same context
+        qff.deltanet_prefill(ctx, pg, *o_args, f32_tensor(other["conv_state"]), f32_tensor(other["ssm_state"]))
+        torch.cuda.synchronize()
+
+
 def test_deltanet_decode_batches_alternate_and_graph_replay(hip):
     """The two value heads of a key head share its q/k conv-state slots; the
     second workgroup to finish reading them rewrites them, counted on
