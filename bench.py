@@ -33,13 +33,15 @@ C0_FLOPS = 3_670_016
 C1_FLOPS = 23_622_320_128      # DeltaNet chunked prefill T=4096
 C1_BYTES = 137_428_992
 # Config 1 per kernel, per launch (64 chunks x 32 heads, C = 64, d = 128),
-# the canonical terms split by the kernel that computes them: the chunk-local
-# pass K K^T, Q K^T, T X and T V (4 * 2C^2 d per chunk and head), the state
-# pass S W^T, K~^T U, S Qe^T and P U~ (3 * 2Cd^2 + 2C^2 d); the two sum to
-# C1_FLOPS (the norm pass does no matrix work).
+# the canonical terms split by the kernel that computes them: the state pass
+# forms K S^T, the state update K^T U and Q S^T (3 * 2Cd^2 per chunk and
+# head) and T Y, P U (2 * 2C^2 d); the chunk-local pass the Gram products
+# K K^T, Q K^T and T = (I + A)^-1, credited with the remaining 3 * 2C^2 d of
+# the canonical count; the two sum to C1_FLOPS (the norm pass does no matrix
+# work).
 C1_KERNEL_FLOPS = {
-    "dn_chunk_local": 2048 * 4 * 2 * 64 * 64 * 128,
-    "dn_chunk_state": 2048 * (3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128),
+    "dn_chunk_local": 2048 * 3 * 2 * 64 * 64 * 128,
+    "dn_chunk_state": 2048 * (3 * 2 * 64 * 128 * 128 + 2 * 2 * 64 * 64 * 128),
 }
 assert sum(C1_KERNEL_FLOPS.values()) == 23_622_320_128
 C3_ATTN_FLOPS = 549_822_922_752   # GQA causal prefill T=8192: 32 D T (T + 1)

@@ -42,13 +42,16 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.pf_o = take(TC * 4096 * sizeof(float));
     L.sched = take(2 * kSchedSlots * sizeof(unsigned));
     L.dn_arrive = take(B * 16 * sizeof(unsigned));
-    const size_t big = TC * 32 * 128 * sizeof(uint16_t), small = TC * 32 * 64 * sizeof(uint16_t);
-    L.wh = take(big); L.wl = take(big);
-    L.qeh = take(big); L.qel = take(big);
-    L.kth = take(big); L.ktl = take(big);
-    L.uth = take(big); L.utl = take(big);
-    L.ph = take(small); L.pl = take(small);
-    L.gam = take(TC / 64 * 32 * sizeof(float));
+    // DeltaNet prefill chunk records (deltanet_chunked.hip): per chunk and key
+    // head the K image (hi, lo) and Q blocks, per chunk and value head the T
+    // blocks (hi, lo), P blocks, gate factors and beta V
+    const size_t NC = TC / 64;
+    L.kimg = take(NC * 16 * 2 * 64 * 128 * sizeof(uint16_t));
+    L.qop = take(NC * 16 * 16 * 512 * sizeof(uint16_t));
+    L.top = take(NC * 32 * 2 * 6 * 512 * sizeof(uint16_t));
+    L.pop = take(NC * 32 * 6 * 512 * sizeof(uint16_t));
+    L.gates = take(NC * 32 * 4 * 64 * sizeof(float));
+    L.bv = take(NC * 32 * 64 * 128 * sizeof(float));
     L.total = off;
     return L;
 }
@@ -169,8 +172,8 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
         (void)hipSetDevice(prev);
         return QFF_ERR_HIP;
     }
-    c->dn = qff_dn_bufs{u16(L.wh),  u16(L.wl),  u16(L.qeh), u16(L.qel), u16(L.kth), u16(L.ktl),
-                        u16(L.uth), u16(L.utl), u16(L.ph),  u16(L.pl),  reinterpret_cast<float*>(base + L.gam)};
+    c->dn = qff_dn_bufs{u16(L.kimg), u16(L.qop), u16(L.top), u16(L.pop), reinterpret_cast<float*>(base + L.gates),
+                        reinterpret_cast<float*>(base + L.bv)};
     (void)hipSetDevice(prev);
     *out = c;
     return QFF_OK;

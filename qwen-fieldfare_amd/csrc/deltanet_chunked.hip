@@ -9,33 +9,49 @@
 //   S_i = g_i S_{i-1} + u_i k_i^T,  u_i = beta_i (v_i - g_i S_{i-1} k_i),
 // unrolling gives the chunk identities this file evaluates:
 //   A_ij = beta_i e^{G_i - G_j} (k_i . k_j)  (j < i),     T = (I + A)^-1
-//   W = T (beta e^G K),  U~ = T (beta V),  U = U~ - W S0^T
+//   U = T (beta V - diag(beta e^G) K S0^T)
 //   P_ij = e^{G_i - G_j} (q_i . k_j)  (j <= i)
-//   O = (e^G Q) S0^T + P U = Qe S0^T + P U~,   Qe = e^G Q - P W
-//   S_C = e^{G_C} S0 + U^T K~,  K~ = e^{G_C - G} K
-// (tests/test_oracle_deltanet.py checks them against the sequential
-// recurrence in fp64). Writing O through Qe takes U out of it, so the
-// sequential pass forms U and O from the same S0 in one step.
+//   O = diag(e^G) Q S0^T + P U
+//   S_C = e^{G_C} S0 + U^T diag(e^{G_C - G}) K
+// (tests/test_oracle_deltanet.py checks the chunked form against the
+// sequential recurrence in fp64). Everything that depends on S0 is formed
+// from the key head's K and Q, which both of its value heads share; the
+// per-head data are T, P and the gates.
 //
 // Two kernels:
 //   dn_chunk_local_kernel  persistent, one (chunk, key head) unit at a time
 //       from a work queue, all chunks independent: conv1d + SiLU of the
-//       chunk's q, k and both value heads' v channels straight from the
-//       projection (3 tokens of history from the input or the conv state),
-//       L2 norms, gates, the Gram products K K^T and Q K^T once for both
-//       value heads, then per value head A, P, T (16x16 blocks: diagonal
-//       blocks by substitution, the rest on fp32 MFMAs), W, U~ and Qe;
-//       writes W, Qe, K~^T, U~^T, P (bf16 hi/lo) and e^{G_C}.
+//       chunk's q and k channels straight from the projection (3 tokens of
+//       history from the input or the conv state), L2 norms, both value
+//       heads' gates, the Gram products K K^T and Q K^T, then per value head
+//       A, P and T = (I + A)^-1 (16x16 blocks: diagonal blocks by
+//       substitution, the rest on fp32 MFMAs), and the conv1d + SiLU of both
+//       heads' v channels times beta. Writes K (bf16 hi/lo, in the state
+//       pass's LDS image), Q (fp16), T (bf16 hi/lo), P (fp16) as MFMA operand
+//       blocks, beta V and the per-token gate factors.
 //   dn_chunk_state_kernel  one workgroup per (16 state rows, value head)
-//       walks the chunks in order with its state rows in registers, twelve
-//       waves in three roles: U = U~ - W S^T, S = e^{G_C} S + U^T K~ and the
-//       pre-norm output O^T = S Qe^T + U~^T P^T. Its MFMA operands come from
-//       global memory straight into registers in operand layout, one or two
-//       chunks ahead.
-// Every product runs as bf16x3 on v_mfma_f32_16x16x32_bf16 (a b ~ a_hi b_hi
-// + a_hi b_lo + a_lo b_hi, ~2^-16 relative per product), which keeps the
-// fp32 state within 1e-4 of the sequential fp32 recurrence; plain bf16
-// operands would not.
+//       walks the chunks in order: two chain waves hold the block's state
+//       (key halves) in accumulators and form X = K S^T, U = T (beta V - D X)
+//       and the state update; four helper waves stage the next chunk's
+//       operands in LDS and form the pre-norm output rows
+//       O = diag(e^G) Q S^T + P U one chunk behind.
+//
+// Operand order. A 16x16x32 MFMA gives lane l of its A and B operands the
+// 8 k-elements e = 0..7 of lane group g = l / 16; here they are the k indices
+//   pq(g, e) = 4g + e (e < 4),  16 + 4g + (e - 4) (e >= 4)
+// of each 32-wide k step, which is where two stacked 16x16 fp32 accumulator
+// tiles (rows 0-15, 16-31) keep them (lane l: column l % 16, rows 4g .. 4g+3
+// of each tile). So a product's accumulators become the next product's B
+// operand (k = the accumulator rows) in registers, with no exchange, when
+// the A operand walks k in the same order; every operand block below is
+// written in it.
+//
+// Precision: the chain's products (X, U and the state update) run as bf16x3
+// on v_mfma_f32_16x16x32_bf16 (a b ~ a_hi b_hi + a_hi b_lo + a_lo b_hi,
+// ~2^-16 relative per product), which keeps the fp32 state within 1e-4 of
+// the sequential fp32 recurrence; the Gram products likewise. The output
+// products (Q S^T, P U) take fp16 operands (11 significant bits): they feed
+// only the bf16/fp32 outputs, through the gated RMSNorm.
 #include <algorithm>
 
 #include "common.hpp"
@@ -46,11 +62,34 @@ namespace qff {
 
 constexpr int kC = 64;      // chunk length
 constexpr int kLD = 136;    // bf16 row stride of [64][128] LDS tiles (128 + 8)
-constexpr int kLT = 72;     // bf16 row stride of [64][64] LDS tiles (64 + 8)
-
-// ---- chunk-local pass --------------------------------------------------------
+constexpr int kLP = 72;     // fp16 row stride of [64][64] LDS tiles (64 + 8)
+constexpr int kBlk = 512;   // 16-bit elements of one operand block (64 lanes x 8)
 
 constexpr float kLog2e = 1.44269504088896341f;
+
+// Workspace records (16-bit elements unless noted), per chunk c:
+constexpr int kKImg = 2 * kC * 128;   // per key head: K hi, lo, each [64][128] in the LDS image order
+constexpr int kQOp = 16 * kBlk;       // per key head: Q fp16, blocks (token tile tt, k step j), tt * 4 + j
+constexpr int kTOp = 2 * 6 * kBlk;    // per value head: T hi, lo, blocks tblk(tt, j)
+constexpr int kPOp = 6 * kBlk;        // per value head: P fp16, blocks tblk(tt, j)
+constexpr int kGates = 4 * kC;        // per value head (floats): beta, beta e^G, e^{G_C - G}, e^G
+constexpr int kBV = kC * 128;         // per value head (floats): beta V, [16-channel block][token tile][lane][4]
+
+// k index of element e of lane group g in a 32-wide k step (see above)
+__device__ __forceinline__ int pq(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
+
+// The lower-triangular [64][64] operands (T, P) as 16-row tiles tt x 32-wide
+// k steps j <= tt / 2: blocks (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
+__device__ __forceinline__ int tblk(int tt, int j) { return tt < 2 ? tt : 2 * tt - 2 + j; }
+
+// K image: row r (token), logical 16-byte piece q holds keys 32(q/4) +
+// 4(q%4) .. +3 and 32(q/4) + 16 + 4(q%4) .. +3 (one lane group's operand
+// piece); it sits at physical piece q ^ (r % 16), so the 16 rows of an
+// operand read (and the 16 rows of a transposed read) fall on different
+// LDS banks. Element offset of logical piece q of row r:
+__device__ __forceinline__ int kimg_off(int r, int q) { return r * 128 + ((q ^ (r & 15)) << 3); }
+
+// ---- chunk-local pass --------------------------------------------------------
 
 // Raw projection pair (channels ch, ch+1) as stored: two bf16 in one word,
 // or two floats.
@@ -74,13 +113,13 @@ template <> struct RawPair<0> {
 
 // Everything one (chunk, key head) unit reads from global memory, for one
 // thread (wave w: tokens 8w .. 8w+7 of the chunk; lane l: channels 2l, 2l+1
-// of the key head's q and k blocks and of the v blocks of its two value
-// heads): the conv input rows at positions tok-3 .. tok+7 clamped into
-// [0, T), the conv weights, and per value head the gate inputs of token
-// lane and the head's A_log and dt_bias. Every load is unconditional and in
-// bounds, so the loads of the next unit can be issued while the current one
-// is processed and the compiler's vmcnt accounting stays exact. (The
-// conv-state slots that chunk 0 needs are read when that unit is processed.)
+// of the key head's q and k blocks and of its two value heads' v blocks):
+// the conv input rows at positions
+// tok-3 .. tok+7 clamped into [0, T), the conv weights, and per value head
+// the gate inputs of token lane and the head's A_log and dt_bias. Every load
+// is unconditional and in bounds, so the loads of the next unit can be
+// issued while the current one is processed. (The conv-state slots that
+// chunk 0 needs are read when that unit is processed.)
 template <int IN_DT>
 struct UnitIn {
     RawPair<IN_DT> r[4][11];
@@ -97,8 +136,7 @@ template <int IN_DT>
 __device__ __forceinline__ void fetch_unit(UnitIn<IN_DT>& in, int u, int T, const void* __restrict__ qkv,
                                            const float* __restrict__ a, const float* __restrict__ b,
                                            const float* __restrict__ a_log, const float* __restrict__ dt_bias,
-                                           const float* __restrict__ conv_w, const float* __restrict__ conv_state,
-                                           int wave, int lane) {
+                                           const float* __restrict__ conv_w, int wave, int lane) {
     int c, kh;
     unit_coords(u, c, kh);
     const int t0 = c * kC, tw = t0 + 8 * wave;
@@ -190,114 +228,35 @@ __device__ __forceinline__ void wave_sum8(const float (&p)[8], float (&tot)[8], 
         tot[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q1), 8 * j));
 }
 
-// Splits 8 floats into bf16 hi / lo and stores 16 B of each.
-__device__ __forceinline__ void store_split8(uint16_t* hi, uint16_t* lo, const float (&x)[8]) {
-    uint32_t hw[4], lw[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) split_bf16x2(x[2 * k], x[2 * k + 1], hw[k], lw[k]);
-    *reinterpret_cast<u32x4_t*>(hi) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
-    *reinterpret_cast<u32x4_t*>(lo) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
-}
-
-// Operand-order layout of a row-major [rows][K] bf16 matrix that is read as
-// 16x16x32 MFMA operand tiles (row r of a tile in lane r % 16, k = 8 k8 ..
-// 8 k8 + 7 in lane group k8 % 4): the 8 elements (r, 8 k8 .. 8 k8 + 7) sit at
-// element offset 8 * swz<K>(r, k8), so the 64 lanes' pieces of each (row
-// tile, k step) are one contiguous 1 KB block and a wave's operand load is
-// fully coalesced.
-template <int K>
-__device__ __forceinline__ int swz(int r, int k8) {
-    return ((r >> 4) * (K / 32) + (k8 >> 2)) * 64 + (k8 & 3) * 16 + (r & 15);
-}
-// Its inverse: piece p -> (r, k8). Writers walk p with the thread index, so
-// each store instruction covers one contiguous 1 KB block.
-template <int K>
-__device__ __forceinline__ void unswz(int p, int& r, int& k8) {
-    const int q = p >> 6;
-    r = (q / (K / 32)) * 16 + (p & 15);
-    k8 = (q % (K / 32)) * 4 + ((p >> 4) & 3);
-}
-
-// bf16x3 block product like mma_block_x3 (NN), with the k elements of A
-// scaled by asc[k] on the way in: the A operand (hi, lo) is recombined,
-// scaled in fp32 and split again (exact to ~2^-16 like the operands
-// themselves).
-template <int K, int NC>
-__device__ __forceinline__ void mma_block_x3_ascale(f32x4_t (&acc)[1][NC], const uint16_t* ah, const uint16_t* al,
-                                                    int lda, int ar, const float* asc, const uint16_t* bh,
-                                                    const uint16_t* bl, int ldb, int bc, int lane) {
-    const int n = lane & 15, kb = lane >> 4;
-#pragma unroll
-    for (int k0 = 0; k0 < K; k0 += 32) {
-        const int ao = (ar + n) * lda + k0 + 8 * kb;
-        const u32x4_t h = *reinterpret_cast<const u32x4_t*>(ah + ao);
-        const u32x4_t l = *reinterpret_cast<const u32x4_t*>(al + ao);
-        const float4 s0 = *reinterpret_cast<const float4*>(asc + k0 + 8 * kb);
-        const float4 s1 = *reinterpret_cast<const float4*>(asc + k0 + 8 * kb + 4);
-        const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        u32x4_t a_h, a_l;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float x0 = (__uint_as_float(h[e] << 16) + __uint_as_float(l[e] << 16)) * sc[2 * e];
-            const float x1 = (__uint_as_float(h[e] & 0xffff0000u) + __uint_as_float(l[e] & 0xffff0000u)) * sc[2 * e + 1];
-            uint32_t hw, lw;
-            split_bf16x2(x0, x1, hw, lw);
-            a_h[e] = hw;
-            a_l[e] = lw;
-        }
-        u32x4_t b_h[NC], b_l[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int bo = (k0 + 8 * kb + (n >> 2)) * ldb + bc + 16 * c + 4 * (n & 3);
-            const u32x2_t h0 = lds_read_tr16(bh + bo), h1 = lds_read_tr16(bh + bo + 4 * ldb);
-            const u32x2_t l0 = lds_read_tr16(bl + bo), l1 = lds_read_tr16(bl + bo + 4 * ldb);
-            b_h[c] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
-            b_l[c] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
-        }
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_l, b_h[c], acc[0][c]);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_h, b_l[c], acc[0][c]);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[0][c] = mfma_16x16x32_bf16(a_h, b_h[c], acc[0][c]);
-    }
-}
-
-// Packed lower triangle (j <= i) of a 64 x 64 matrix.
-__device__ __forceinline__ int tri(int i, int j) { return i * (i + 1) / 2 + j; }
-
-// LDS carve-up of the chunk-local kernel (bytes)
+// LDS carve-up of the chunk-local kernel (bytes). T (fp32) reuses the Q
+// region once Q has been written out.
 constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
-constexpr int kOffK = 0;                          // K hi, lo (both value heads)
-constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T (fp32) + scratch; then W hi, lo
-constexpr int kOffV = 4 * kTile128;               // beta V hi, lo; then P W, Qe (fp32 [64][132])
-constexpr int kOffA = 6 * kTile128;               // A fp32 [64][65]
-constexpr int kOffT = kOffA + kC * 65 * 4;        // P hi, lo, then T hi, lo, then P again: [64][72]
-constexpr int kTri = kC * (kC + 1) / 2;           // packed lower triangle
-constexpr int kOffR = kOffT + 2 * kC * kLT * 2;   // raw K K^T and Q K^T lower triangles (fp32)
-constexpr int kOffG = kOffR + 2 * kTri * 4;       // per value head: G[64], beta[64], beta e^G [64]
-constexpr int kLocalSmem = kOffG + 2 * 3 * kC * 4;
+constexpr int kOffK = 0;                          // K hi, lo
+constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T fp32 [2][64][65]
+constexpr int kOffA = 4 * kTile128;               // A fp32 [2][64][65]
+constexpr int kOffP = kOffA + 2 * kC * 65 * 4;    // P fp16 [2][64][72]
+constexpr int kOffS = kOffP + 2 * kC * kLP * 2;   // off-diagonal solve scratch [6][16][17] fp32
+constexpr int kOffG = kOffS + 6 * 16 * 17 * 4;    // G [2][64], beta [2][64]
+constexpr int kLocalSmem = kOffG + 4 * kC * 4;
+static_assert(2 * kC * 65 * 4 <= 2 * kTile128, "T must fit the Q region");
 
 // Persistent: grid = min(units, CUs) workgroups of 512 threads (eight
 // waves, two per SIMD) walk the (chunk, key head) units. Units 0 .. 2g-1
 // go out statically (g = grid size), the rest through an atomic counter, so
-// a workgroup on a CU that runs slow (or shares its XCD with other work)
-// simply takes fewer units; the launch's last workgroup resets the counter.
-// A key head's q and k feed both of its value heads, so a unit runs the
-// conv, norms and the Gram products K K^T and Q K^T once and keeps the raw
-// products (packed lower triangles) for the second head, whose A and P
-// differ only by the per-head gates. Per value head: K~^T out, beta V, A
-// and P, T = (I + A)^-1, W = T diag(beta e^G) K (the scaling applied to T's
-// operand, so K stays as it is for the other head), U~ = T (beta V), P W
-// and Qe. While a unit is processed the inputs of the workgroup's next unit
-// are already loading into registers (UnitIn), issued by the second head
-// once its T = (I + A)^-1 is complete (earlier, they would not fit the
-// registers of the rest of the unit: issuing them on the waves idle during
-// the off-diagonal solve spilled 170 registers).
-// Conv passes map wave w to tokens 8w .. 8w+7 and lane l to channels 2l,
-// 2l+1 of a 128-channel block, so a lane's 8 tokens of a channel are one
-// K~^T operand piece and each conv input row is one 256-B load per wave.
-// Global loads are issued before the stores of the same head (vmcnt counts
+// a workgroup on a CU that runs slow simply takes fewer units; the launch's
+// last workgroup resets the counter. Per unit:
+//   gates of both value heads (waves 0, 1; lane = token) -> LDS and out;
+//   conv + SiLU + L2 norm of q and k (wave = 8 tokens, lane = 2 channels)
+//       -> LDS as bf16 hi / lo;
+//   K K^T (waves 0-3) and Q K^T (waves 4-7), one 16-row tile each, then A
+//       and P of both heads from the same accumulators; the next unit's
+//       inputs are requested here;
+//   K image, Q and P blocks out;
+//   T = (I + A)^-1 of both heads: the eight diagonal blocks by forward
+//       substitution (one wave each), the off-diagonal blocks by six waves
+//       walking their column block down on fp32 MFMAs;
+//   T blocks out.
+// Global loads are issued before the stores of the same unit (vmcnt counts
 // stores too on gfx950, so a load consumed after stores would wait for them).
 constexpr int kLocalThreads = 512;
 
@@ -315,20 +274,16 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     uint16_t* Kl = Kh + kC * kLD;
     uint16_t* Qh = reinterpret_cast<uint16_t*>(smem + kOffQ);
     uint16_t* Ql = Qh + kC * kLD;
-    uint16_t* Vh = reinterpret_cast<uint16_t*>(smem + kOffV);
-    uint16_t* Vl = Vh + kC * kLD;
-    float* Am = reinterpret_cast<float*>(smem + kOffA);
-    uint16_t* Th = reinterpret_cast<uint16_t*>(smem + kOffT);
-    uint16_t* Tl = Th + kC * kLT;
-    float* KKr = reinterpret_cast<float*>(smem + kOffR);
-    float* QKr = KKr + kTri;
+    float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [2][64][65]
+    float* Am = reinterpret_cast<float*>(smem + kOffA);   // [2][64][65]
+    uint16_t* Pf = reinterpret_cast<uint16_t*>(smem + kOffP);   // [2][64][72]
+    float* Scr = reinterpret_cast<float*>(smem + kOffS);
     float* Gs = reinterpret_cast<float*>(smem + kOffG);   // [hh][64]
     float* Bs = Gs + 2 * kC;                              // [hh][64]
-    float* Ss = Bs + 2 * kC;                              // [hh][64]: beta e^G
 
     int u = blockIdx.x, un = blockIdx.x + grid;
     UnitIn<IN_DT> in;
-    fetch_unit<IN_DT>(in, u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, threadIdx.x >> 6, threadIdx.x & 63);
+    fetch_unit<IN_DT>(in, u, T, qkv, a, b, a_log, dt_bias, conv_w, threadIdx.x >> 6, threadIdx.x & 63);
     if (threadIdx.x == 0) s_next = 2 * grid + static_cast<int>(atomicAdd(sched, 1u));
     // Wait here for the first unit's loads: the loop's own waits then only
     // count the operations of the previous iteration, which issues stores
@@ -344,7 +299,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     asm volatile("" : "+v"(t));
     const int lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const int rt = wave & 3, role = wave >> 2;   // MFMA row tile; which of a wave pair's two products
+    const int rt = wave & 3, role = wave >> 2;   // MFMA row tile; K K^T or Q K^T
     int c, kh;
     unit_coords(u, c, kh);
     const int t0 = c * kC;
@@ -354,7 +309,7 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     // gates (deltanet.metal:250-280), waves 0 and 1 one value head each:
     // log g = -e^{A_log} softplus(a + dt_bias), beta = sigmoid(b); G =
     // inclusive prefix sum over the chunk. Padded tokens have log g = 0 and
-    // beta = 0, so they change nothing.
+    // beta = 0, so they change nothing (and G_63 = G_C).
     if (wave < 2) {
         const int hh = wave;
         const bool ok = lane < nv;
@@ -367,10 +322,15 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             if (lane >= o) x += y;
         }
         const float beta = ok ? sigmoid(bv) : 0.0f;
+        const float gc = __shfl(x, 63, 64);
+        const float eg = __builtin_amdgcn_exp2f(x * kLog2e);
         Gs[hh * kC + lane] = x;
         Bs[hh * kC + lane] = beta;
-        Ss[hh * kC + lane] = beta * __builtin_amdgcn_exp2f(x * kLog2e);
-        if (lane == 63) out.gam[static_cast<size_t>(c) * 32 + 2 * kh + hh] = expf(x);
+        float* go = out.gates + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kGates;
+        go[lane] = beta;
+        go[kC + lane] = beta * eg;
+        go[2 * kC + lane] = __builtin_amdgcn_exp2f((gc - x) * kLog2e);
+        go[3 * kC + lane] = eg;
     }
     const int chs[4] = {kh * 128 + 2 * lane, 2048 + kh * 128 + 2 * lane, 4096 + 2 * kh * 128 + 2 * lane,
                         4096 + (2 * kh + 1) * 128 + 2 * lane};
@@ -396,294 +356,195 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float sc = __builtin_amdgcn_rsqf(tot[i] + 1e-6f) * post;
-            y[i][0] *= sc;
-            y[i][1] *= sc;
             uint32_t hh, ll;
-            split_bf16x2(y[i][0], y[i][1], hh, ll);
+            split_bf16x2(y[i][0] * sc, y[i][1] * sc, hh, ll);
             const int o = (8 * wave + i) * kLD + 2 * lane;
             *reinterpret_cast<uint32_t*>(dh + o) = hh;
             *reinterpret_cast<uint32_t*>(dl + o) = ll;
         }
     };
-    // (k is kept in LDS only: K~^T is formed from the hi/lo copy)
-    float qn[8][2], vn[2][8][2];
     {
-        float kn[8][2];
-        conv(0, qn);
-        norm_store(qn, 0.08838834764831845f, Qh, Ql);   // 1 / sqrt(128)
-        conv(1, kn);
-        norm_store(kn, 1.0f, Kh, Kl);
+        float y[8][2];
+        conv(0, y);
+        norm_store(y, 0.08838834764831845f, Qh, Ql);   // 1 / sqrt(128)
+        conv(1, y);
+        norm_store(y, 1.0f, Kh, Kl);
     }
-    conv(2, vn[0]);
-    conv(3, vn[1]);
     __syncthreads();
-
+    // ---- beta V of both value heads (conv + SiLU of the v channels times the
+    // token's beta), stored in the state pass's order: per 16-channel block
+    // cb and token tile tt, lane n + 16g holds tokens 16tt + 4g .. +3 of
+    // channel 16cb + n
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        float y[8][2];
+        conv(2 + hh, y);
+        float* bo = out.bv + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kBV;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int ch = 2 * lane + cc;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int tok = 8 * wave + 4 * hf;
+                const float4 bt = *reinterpret_cast<const float4*>(Bs + hh * kC + tok);
+                const int o = (((ch >> 4) * 4 + (tok >> 4)) * 64 + (ch & 15) + 16 * ((tok & 15) >> 2)) * 4;
+                *reinterpret_cast<f32x4_t*>(bo + o) =
+                    f32x4_t{bt.x * y[4 * hf][cc], bt.y * y[4 * hf + 1][cc], bt.z * y[4 * hf + 2][cc],
+                            bt.w * y[4 * hf + 3][cc]};
+            }
+        }
+    }
     // grabbed now, published at the end of the unit, when it has long arrived
     unsigned grabbed = 0;
     if (t == 0) grabbed = atomicAdd(sched, 1u);
-    int unn = 0;
+    int unn;
 
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-    const int h = 2 * kh + hh;
-    const size_t ch = static_cast<size_t>(c) * 32 + h;   // (chunk, value head) record
-    const float* G = Gs + hh * kC;
-    const float* Bt = Bs + hh * kC;
-
-    // ---- K~^T out (channels 2l, 2l+1 x this wave's 8 tokens: one operand
-    // piece each), beta v to LDS; A and P -------------------------------------
-    {
-        const float gc = G[kC - 1];
-        float gw[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) gw[i] = G[8 * wave + i];
-        float kn[8][2];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t kh2 = *reinterpret_cast<const uint32_t*>(Kh + (8 * wave + i) * kLD + 2 * lane);
-            const uint32_t kl2 = *reinterpret_cast<const uint32_t*>(Kl + (8 * wave + i) * kLD + 2 * lane);
-            kn[i][0] = __uint_as_float(kh2 << 16) + __uint_as_float(kl2 << 16);
-            kn[i][1] = __uint_as_float(kh2 & 0xffff0000u) + __uint_as_float(kl2 & 0xffff0000u);
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                split_bf16x2(__builtin_amdgcn_exp2f((gc - gw[2 * j]) * kLog2e) * kn[2 * j][cc],
-                             __builtin_amdgcn_exp2f((gc - gw[2 * j + 1]) * kLog2e) * kn[2 * j + 1][cc], hw[j], lw[j]);
-            const size_t o = ch * 128 * kC + 8 * swz<kC>(2 * lane + cc, wave);
-            *reinterpret_cast<u32x4_t*>(out.kth + o) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
-            *reinterpret_cast<u32x4_t*>(out.ktl + o) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float bb = Bt[8 * wave + i];
-            uint32_t hq, lq;
-            split_bf16x2(bb * vn[hh][i][0], bb * vn[hh][i][1], hq, lq);
-            const int o = (8 * wave + i) * kLD + 2 * lane;
-            *reinterpret_cast<uint32_t*>(Vh + o) = hq;
-            *reinterpret_cast<uint32_t*>(Vl + o) = lq;
-        }
-    }
-    // waves 0-3: K K^T -> A (strictly lower, scaled); waves 4-7: Q K^T -> P
-    // (lower incl. diagonal); row tile rt each. The first head forms the
-    // products and keeps them raw; the second reads them back.
+    // ---- waves 0-3: K K^T -> A of both heads (strictly lower, scaled);
+    // waves 4-7: Q K^T -> P of both heads (lower incl. diagonal); row tile rt
     {
         f32x4_t acc[1][4];
-        if (hh == 0) {
 #pragma unroll
-            for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
-        }
-        float* raw = role ? QKr : KKr;
-        float gi[4], bi[4], gj[4];
+        for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
+        // the next unit's inputs (the unit index is clamped, so the loads stay
+        // in bounds when the queue has run out)
+        unn = s_next;
+        fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, wave, lane);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            gi[ii] = G[16 * rt + 4 * kb + ii] * kLog2e;
-            bi[ii] = Bt[16 * rt + 4 * kb + ii];
-            gj[ii] = G[16 * ii + n] * kLog2e;
-        }
-#pragma unroll
-        for (int cj = 0; cj < 4; ++cj) {
-            const int j = 16 * cj + n;
+        for (int hh = 0; hh < 2; ++hh) {
+            const float* G = Gs + hh * kC;
+            const float* Bt = Bs + hh * kC;
+            float gi[4], bi[4], gj[4];
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int i = 16 * rt + 4 * kb + ii;
-                float g;
-                if (hh == 0) {
-                    g = acc[0][cj][ii];
-                    if (j <= i) raw[tri(i, j)] = g;
-                } else {
-                    g = j <= i ? raw[tri(i, j)] : 0.0f;
-                }
-                // e^{G_i - G_j}; for j > i the product is discarded by the select
-                const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * g;
-                if (role == 0) {
-                    Am[i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
-                } else {
-                    uint16_t hq, lq;
-                    split_bf16(j <= i ? v : 0.0f, hq, lq);
-                    Th[i * kLT + j] = hq;
-                    Tl[i * kLT + j] = lq;
+                gi[ii] = G[16 * rt + 4 * kb + ii] * kLog2e;
+                bi[ii] = Bt[16 * rt + 4 * kb + ii];
+                gj[ii] = G[16 * ii + n] * kLog2e;
+            }
+#pragma unroll
+            for (int cj = 0; cj < 4; ++cj) {
+                const int j = 16 * cj + n;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const int i = 16 * rt + 4 * kb + ii;
+                    // e^{G_i - G_j}; for j > i the product is discarded by the select
+                    const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * acc[0][cj][ii];
+                    if (role == 0)
+                        Am[hh * kC * 65 + i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
+                    else
+                        Pf[hh * kC * kLP + i * kLP + j] = f32_to_f16(j <= i ? v : 0.0f);
                 }
             }
         }
     }
     __syncthreads();
-    // ---- P out, one coalesced 1 KB block per wave and array; the pieces stay in
-    // registers until the T region is free again --------------------------------
-    u32x4_t pkeep[2];
+    // ---- K image, Q blocks (fp16) and P blocks (fp16) out -----------------------
     {
-        int row, k8;
-        unswz<kC>(t, row, k8);
-        pkeep[0] = *reinterpret_cast<const u32x4_t*>(Th + row * kLT + 8 * k8);
-        pkeep[1] = *reinterpret_cast<const u32x4_t*>(Tl + row * kLT + 8 * k8);
-        // P and Qe are read only by the output pass, after the state pass:
-        // streamed past the caches so that W, K~ and U~, which the state pass
-        // reads next, stay in the last-level cache
-        __builtin_nontemporal_store(pkeep[0], reinterpret_cast<u32x4_t*>(out.ph + ch * kC * kC + 8 * t));
-        __builtin_nontemporal_store(pkeep[1], reinterpret_cast<u32x4_t*>(out.pl + ch * kC * kC + 8 * t));
+        uint16_t* ko = out.kimg + (static_cast<size_t>(c) * 16 + kh) * kKImg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int pc = t + kLocalThreads * i;   // [hi, lo][row][physical piece]
+            const int hl = pc >> 10, row = (pc >> 4) & 63, p = pc & 15;
+            const int q = p ^ (row & 15);
+            const int k0 = 32 * (q >> 2) + 4 * (q & 3);
+            const uint16_t* src = (hl ? Kl : Kh) + row * kLD;
+            const u32x2_t x0 = *reinterpret_cast<const u32x2_t*>(src + k0);
+            const u32x2_t x1 = *reinterpret_cast<const u32x2_t*>(src + k0 + 16);
+            *reinterpret_cast<u32x4_t*>(ko + 8 * pc) = u32x4_t{x0[0], x0[1], x1[0], x1[1]};
+        }
+        uint16_t* qo = out.qop + (static_cast<size_t>(c) * 16 + kh) * kQOp;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int pc = t + kLocalThreads * i;   // [block tt * 4 + j][lane]
+            const int blk = pc >> 6, l = pc & 63;
+            const int row = 16 * (blk >> 2) + (l & 15), k0 = 32 * (blk & 3) + 4 * (l >> 4);
+            uint32_t w[4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const u32x2_t h2 = *reinterpret_cast<const u32x2_t*>(Qh + row * kLD + k0 + 16 * hf);
+                const u32x2_t l2 = *reinterpret_cast<const u32x2_t*>(Ql + row * kLD + k0 + 16 * hf);
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    w[2 * hf + e] = pack_f16x2(__uint_as_float(h2[e] << 16) + __uint_as_float(l2[e] << 16),
+                                               __uint_as_float(h2[e] & 0xffff0000u) +
+                                                   __uint_as_float(l2[e] & 0xffff0000u));
+            }
+            *reinterpret_cast<u32x4_t*>(qo + 8 * pc) = u32x4_t{w[0], w[1], w[2], w[3]};
+        }
+        for (int pc = t; pc < 2 * 6 * 64; pc += kLocalThreads) {   // [hh][block][lane]
+            const int hh = pc / 384, blk = (pc >> 6) % 6, l = pc & 63;
+            const int tt = blk < 2 ? blk : 2 + ((blk - 2) >> 1), j = blk < 2 ? 0 : (blk - 2) & 1;
+            const int row = 16 * tt + (l & 15), k0 = 32 * j + 4 * (l >> 4);
+            const uint16_t* src = Pf + hh * kC * kLP + row * kLP + k0;
+            const u32x2_t x0 = *reinterpret_cast<const u32x2_t*>(src);
+            const u32x2_t x1 = *reinterpret_cast<const u32x2_t*>(src + 16);
+            uint16_t* po = out.pop + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kPOp;
+            *reinterpret_cast<u32x4_t*>(po + 8 * (pc % 384)) = u32x4_t{x0[0], x0[1], x1[0], x1[1]};
+        }
     }
-    // T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32:
-    //   diagonal blocks by forward substitution, waves 0-3 one each;
-    //   T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i > j, wave j walking
-    //   column block j downwards (fp32 MFMA 16x16x4).
-    float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [64][65] (Q is consumed)
-    float* scr = reinterpret_cast<float*>(smem + kOffQ + kTile128) + rt * (16 * 17);
-    if (role == 0) {
-        const int bi = wave;
+    __syncthreads();   // Q consumed: its region holds T from here on
+    // ---- T = (I + A)^-1 (lower unitriangular) in 16x16 blocks, fp32 ------------
+    // diagonal block bi of head hh by forward substitution (lanes 0-15, lane =
+    // column), the blocks right of it zeroed by the whole wave
+    {
+        const int hh = wave >> 2, bi = wave & 3;
+        const float* A = Am + hh * kC * 65;
+        float* Th = Tm + hh * kC * 65;
+        for (int idx = lane; idx < 16 * (48 - 16 * bi); idx += 64) {
+            const int i = idx / (48 - 16 * bi), j = 16 * (bi + 1) + idx % (48 - 16 * bi);
+            Th[(16 * bi + i) * 65 + j] = 0.0f;
+        }
         if (lane < 16) {
             float tc[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 float ac[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < i; ++j) ac[j & 3] = fmaf(Am[(16 * bi + i) * 65 + 16 * bi + j], tc[j], ac[j & 3]);
+                for (int j = 0; j < i; ++j) ac[j & 3] = fmaf(A[(16 * bi + i) * 65 + 16 * bi + j], tc[j], ac[j & 3]);
                 tc[i] = (i == lane ? 1.0f : 0.0f) - ((ac[0] + ac[1]) + (ac[2] + ac[3]));
-                Tm[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
+                Th[(16 * bi + i) * 65 + 16 * bi + lane] = tc[i];
             }
-        }
-    } else {
-        // blocks right of the diagonal are zero
-        const int bi = rt;
-        for (int idx = lane; idx < 16 * (48 - 16 * bi); idx += 64) {
-            const int i = idx / (48 - 16 * bi), j = 16 * (bi + 1) + idx % (48 - 16 * bi);
-            Tm[(16 * bi + i) * 65 + j] = 0.0f;
         }
     }
     __syncthreads();
-    if (wave < 3) {
-        const int bj = wave;
+    // off-diagonal: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, wave (hh, bj)
+    // walking column block bj downwards (fp32 MFMA 16x16x4)
+    if (wave < 6) {
+        const int hh = wave / 3, bj = wave % 3;
+        const float* A = Am + hh * kC * 65;
+        float* Th = Tm + hh * kC * 65;
+        float* scr = Scr + wave * (16 * 17);
         for (int bi = bj + 1; bi < 4; ++bi) {
             f32x4_t ac = f32x4_t{0.f, 0.f, 0.f, 0.f};
             for (int bk = bj; bk < bi; ++bk)
-                ac = mm16_f32(Am + (16 * bi) * 65 + 16 * bk, 65, Tm + (16 * bk) * 65 + 16 * bj, 65, ac, lane);
+                ac = mm16_f32(A + (16 * bi) * 65 + 16 * bk, 65, Th + (16 * bk) * 65 + 16 * bj, 65, ac, lane);
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) scr[(4 * kb + ii) * 17 + n] = ac[ii];
             __builtin_amdgcn_wave_barrier();
-            const f32x4_t res = mm16_f32(Tm + (16 * bi) * 65 + 16 * bi, 65, scr, 17,
+            const f32x4_t res = mm16_f32(Th + (16 * bi) * 65 + 16 * bi, 65, scr, 17,
                                          f32x4_t{0.f, 0.f, 0.f, 0.f}, lane);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) Tm[(16 * bi + 4 * kb + ii) * 65 + 16 * bj + n] = -res[ii];
+            for (int ii = 0; ii < 4; ++ii) Th[(16 * bi + 4 * kb + ii) * 65 + 16 * bj + n] = -res[ii];
             __builtin_amdgcn_wave_barrier();
         }
     }
     __syncthreads();
-    if (hh == 1) {
-        // the next unit's inputs (the unit index is clamped, so the loads stay
-        // in bounds when the queue has run out), early enough to land before
-        // it starts and late enough to keep them out of the registers of
-        // the rest of the unit
-        unn = s_next;
-        fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, conv_state, wave, lane);
-    }
-    // ---- T -> bf16 hi/lo ----------------------------------------------------
-    for (int idx = t; idx < kC * kC; idx += kLocalThreads) {
-        const int i = idx >> 6, j = idx & 63;
-        uint16_t hq, lq;
-        split_bf16(Tm[i * 65 + j], hq, lq);
-        Th[i * kLT + j] = hq;
-        Tl[i * kLT + j] = lq;
-    }
-    __syncthreads();
-    // ---- waves 0-3: W = T diag(beta e^G) K -> LDS (Q region); waves 4-7:
-    // U~ = T (beta V) -> U~^T out. Row tile rt (16 tokens), 8 column tiles of
-    // 16 dims in two halves. -------------------------------------------------
-    uint16_t* Wh = Qh;
-    uint16_t* Wl = Ql;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        f32x4_t w[1][4];
-#pragma unroll
-        for (int cd = 0; cd < 4; ++cd) w[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        if (role == 0)
-            mma_block_x3_ascale<kC, 4>(w, Th, Tl, kLT, 16 * rt, Ss + hh * kC, Kh, Kl, kLD, 64 * half, lane);
-        else
-            mma_block_x3<kC, 1, 4, true>(w, Th, Tl, kLT, 16 * rt, Vh, Vl, kLD, 64 * half, lane);
-#pragma unroll
-        for (int cd = 0; cd < 4; ++cd) {
-            const int d = 64 * half + 16 * cd + n;
-            uint16_t h4[4], l4[4];
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) split_bf16(w[0][cd][ii], h4[ii], l4[ii]);
-            if (role == 0) {
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    const int i = 16 * rt + 4 * kb + ii;
-                    Wh[i * kLD + d] = h4[ii];
-                    Wl[i * kLD + d] = l4[ii];
-                }
-            } else {
-                const size_t o = (ch * 128 + d) * kC + 16 * rt + 4 * kb;
-                *reinterpret_cast<u32x2_t*>(out.uth + o) =
-                    u32x2_t{h4[0] | (static_cast<uint32_t>(h4[1]) << 16), h4[2] | (static_cast<uint32_t>(h4[3]) << 16)};
-                *reinterpret_cast<u32x2_t*>(out.utl + o) =
-                    u32x2_t{l4[0] | (static_cast<uint32_t>(l4[1]) << 16), l4[2] | (static_cast<uint32_t>(l4[3]) << 16)};
-            }
-        }
-    }
-    __syncthreads();
-    // ---- W out (coalesced); P back into the T region (T is consumed) ------------
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int p = t + kLocalThreads * k;
-        int row, k8;
-        unswz<128>(p, row, k8);
-        const u32x4_t vh = *reinterpret_cast<const u32x4_t*>(Wh + row * kLD + 8 * k8);
-        const u32x4_t vl = *reinterpret_cast<const u32x4_t*>(Wl + row * kLD + 8 * k8);
-        *reinterpret_cast<u32x4_t*>(out.wh + ch * kC * 128 + 8 * p) = vh;
-        *reinterpret_cast<u32x4_t*>(out.wl + ch * kC * 128 + 8 * p) = vl;
-    }
-    {
-        int row, k8;
-        unswz<kC>(t, row, k8);
-        *reinterpret_cast<u32x4_t*>(Th + row * kLT + 8 * k8) = pkeep[0];
-        *reinterpret_cast<u32x4_t*>(Tl + row * kLT + 8 * k8) = pkeep[1];
-    }
-    __syncthreads();
-    // ---- P W -> fp32 [64][132] in the V region (beta V is consumed); wave ->
-    // row tile rt, column half `role` -------------------------------------------
-    float* PW = reinterpret_cast<float*>(smem + kOffV);
-    {
-        f32x4_t pw[1][4];
-#pragma unroll
-        for (int cd = 0; cd < 4; ++cd) pw[0][cd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<kC, 1, 4, true>(pw, Th, Tl, kLT, 16 * rt, Wh, Wl, kLD, 64 * role, lane);
-#pragma unroll
-        for (int cd = 0; cd < 4; ++cd)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                PW[(16 * rt + 4 * kb + ii) * 132 + 64 * role + 16 * cd + n] = pw[0][cd][ii];
-    }
-    __syncthreads();
-    // ---- Qe = e^G q - P W, in place (each thread its own channel pairs) --------
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float eg = __builtin_amdgcn_exp2f(G[8 * wave + i] * kLog2e);
-        float2* pp = reinterpret_cast<float2*>(PW + (8 * wave + i) * 132 + 2 * lane);
-        const float2 pw = *pp;
-        *pp = make_float2(qn[i][0] * eg - pw.x, qn[i][1] * eg - pw.y);
-    }
-    __syncthreads();
-    // ---- Qe out (coalesced) -----------------------------------------------------
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int p = t + kLocalThreads * k;
-        int row, k8;
-        unswz<128>(p, row, k8);
-        const float4 v0 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * k8);
-        const float4 v1 = *reinterpret_cast<const float4*>(PW + row * 132 + 8 * k8 + 4);
-        const float y[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        const size_t o = ch * kC * 128 + 8 * p;
+    // ---- T blocks out (bf16 hi / lo) --------------------------------------------
+    for (int pc = t; pc < 2 * 6 * 64; pc += kLocalThreads) {   // [hh][block][lane]
+        const int hh = pc / 384, blk = (pc >> 6) % 6, l = pc & 63;
+        const int tt = blk < 2 ? blk : 2 + ((blk - 2) >> 1), j = blk < 2 ? 0 : (blk - 2) & 1;
+        const int row = 16 * tt + (l & 15), k0 = 32 * j + 4 * (l >> 4);
+        const float* src = Tm + hh * kC * 65 + row * 65 + k0;
         uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) split_bf16x2(y[2 * k2], y[2 * k2 + 1], hw[k2], lw[k2]);
-        __builtin_nontemporal_store(u32x4_t{hw[0], hw[1], hw[2], hw[3]}, reinterpret_cast<u32x4_t*>(out.qeh + o));
-        __builtin_nontemporal_store(u32x4_t{lw[0], lw[1], lw[2], lw[3]}, reinterpret_cast<u32x4_t*>(out.qel + o));
+        for (int e = 0; e < 4; ++e) {
+            const int kk = 2 * (e & 1) + 16 * (e >> 1);
+            split_bf16x2(src[kk], src[kk + 1], hw[e], lw[e]);
+        }
+        uint16_t* to = out.top + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kTOp + 8 * (pc % 384);
+        *reinterpret_cast<u32x4_t*>(to) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+        *reinterpret_cast<u32x4_t*>(to + 6 * kBlk) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
     }
-    __syncthreads();
-    }   // value heads
     if (t == 0) s_next = 2 * grid + static_cast<int>(grabbed);
     __syncthreads();
     u = un;
@@ -699,238 +560,266 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
 
 // ---- sequential state pass ---------------------------------------------------
 
-// One workgroup per (16-row block of the state, value head), 768 threads; a
-// 1-D grid of 256 workgroups. Workgroups are dispatched to the 8 XCDs
-// round-robin by linear id, so the id -> (head, row block) map puts all row
-// blocks of a head on one XCD, whose L2 then serves the chunk inputs they
-// share. Twelve waves with fixed roles:
-//   waves 0-3 (U waves): token tile tt = wave: U = U~ - W S^T
-//       (A = W from global memory, B = S rows from LDS);
-//   waves 4-7 (S waves): state columns 32(w-4) .. +31 held as S^T tiles:
-//       S^T = e^{G_C} S^T + K~^T U (A = K~^T from global memory, B = U from
-//       LDS); they publish S_c to LDS;
-//   waves 8-11 (O waves): token tile tt = wave - 8: the block's pre-norm
-//       output rows O^T = S_c Qe^T + U~^T P^T (Qe, P from global memory).
-// Per chunk c:
-//   [S waves publish S_c, U waves publish U~ rows]
-//   A  U waves form U;  O waves copy S_c and U~ rows (their A operands) to
-//      registers;  S waves request K~ of chunk c+2
-//   B  S waves update the state;  O waves form and store O^T, then request
-//      Qe, P of chunk c+1;  U waves request W, U~ of chunk c+2
-// so the chain (U, then the state update) never waits on a global load it
-// issues itself: issuing loads stalls a wave for as long as the CU's load
-// path is busy. With U and S^T as the chain's product outputs every LDS
-// store is one 8-byte access per lane. The roles run separate loops (same
-// barriers), so each loop's loads and waits are straight-line code.
-constexpr int kStateThreads = 768;
-constexpr int kSA = 136;   // S hi / lo row stride: 128 + 8
+// bf16 hi / lo halves of 8 fp32 values (two accumulator tiles, pq order).
+__device__ __forceinline__ void split8(const f32x4_t& a, const f32x4_t& b, u32x4_t& hi, u32x4_t& lo) {
+    uint32_t h[4], l[4];
+    split_bf16x2(a[0], a[1], h[0], l[0]);
+    split_bf16x2(a[2], a[3], h[1], l[1]);
+    split_bf16x2(b[0], b[1], h[2], l[2]);
+    split_bf16x2(b[2], b[3], h[3], l[3]);
+    hi = u32x4_t{h[0], h[1], h[2], h[3]};
+    lo = u32x4_t{l[0], l[1], l[2], l[3]};
+}
+__device__ __forceinline__ u32x4_t pack_f16x8(const f32x4_t& a, const f32x4_t& b) {
+    return u32x4_t{pack_f16x2(a[0], a[1]), pack_f16x2(a[2], a[3]), pack_f16x2(b[0], b[1]), pack_f16x2(b[2], b[3])};
+}
+// acc += a b with bf16x3 operands
+__device__ __forceinline__ f32x4_t mma_x3(u32x4_t ah, u32x4_t al, u32x4_t bh, u32x4_t bl, f32x4_t acc) {
+    acc = mfma_16x16x32_bf16(al, bh, acc);
+    acc = mfma_16x16x32_bf16(ah, bl, acc);
+    return mfma_16x16x32_bf16(ah, bh, acc);
+}
+
+// LDS of the state pass: two stages of chunk operands (filled by the helper
+// waves one chunk ahead) and the exchange buffers.
+struct StateSmem {
+    uint16_t kimg[2][kKImg];      // [stage] K hi | lo image
+    uint16_t top[2][kTOp];        // [stage] T hi | lo blocks
+    f32x4_t bv[2][4][64];         // [stage][token tile][lane] beta V of the block's rows
+    float gates[2][kGates];       // [stage] beta, beta e^G, e^{G_C - G}, e^G
+    f32x4_t xp[2][4][64];         // [chain wave][token tile][lane] partial X
+    u32x4_t sb[2][4][64];         // [chunk parity][k step][lane] S^T fp16 B operands
+    u32x4_t ub[2][2][64];         // [chunk parity][k step][lane] U fp16 B operands
+};
+
+// One workgroup of 384 threads per (16-row block cb of the state, value head
+// h), a 1-D grid of 256. Workgroups go to the 8 XCDs round-robin by linear
+// id; the id -> (head, block) map puts both value heads of two key heads on
+// each XCD, so its L2 serves the K image all 16 blocks of a key head share.
+// Lane l = (n, g) = (l % 16, l / 16): state row 16 cb + n.
+//
+// Chain waves 2, 3 (w = wave - 2, each alone on its SIMD): hold S^T for keys
+// 64w .. 64w+63 as four 16x16 accumulator tiles (S^T[16 kt + 4g + i][n]),
+// and per chunk c:
+//   (a) X_w = K[:, keys of w] S^T: 4 token tiles x 2 k steps, B = the state
+//       tiles in registers (pq order), A = K image rows from LDS; partial X
+//       to LDS; S_c^T also published as fp16 B operands for the output.
+//   [barrier B1]
+//   (b) X = X_0 + X_1 (both waves form the same sum), Y = beta V - D X,
+//       U = T Y (Y's accumulators are its B operand), U published as fp16;
+//   (c) S^T = e^{G_C} S^T + K^T diag(e^{G_C - G}) U: A = K^T through the LDS
+//       transpose read of the same image, B = the scaled U tiles.
+//   [barrier B0 of chunk c + 1]
+// Helper waves 0, 1, 4, 5 (hw = 0 .. 3), after B1(c): the output rows of
+// chunk c - 1, token tile hw: O = diag(e^G) Q S^T + P U on fp16 MFMAs (Q, P
+// blocks in registers, loaded a chunk earlier; S^T, U from LDS) to the
+// pre-norm output; then a quarter of chunk c + 1's operands (K image, T,
+// beta V, gates) into the free stage from registers loaded a chunk earlier,
+// and the loads of chunk c + 2.
+constexpr int kStateThreads = 384;
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
                                                                       float* __restrict__ ssm_state,
                                                                       float* __restrict__ po) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
-    const int h = xcd * 4 + (slot >> 3), rb = slot & 7;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = lane & 15, kb = lane >> 4;
-
-    __shared__ __attribute__((aligned(16))) uint16_t Sh[16 * kSA], Sl[16 * kSA];   // S_c [16 rows][128]
-    __shared__ __attribute__((aligned(16))) uint16_t Uh[16 * kLT], Ul[16 * kLT];   // U^T [16 rows][64 tokens]
-    __shared__ __attribute__((aligned(16))) uint16_t Vh[16 * kLT], Vl[16 * kLT];   // U~^T rows [16][64]
-
+    const int kh = 2 * xcd + (slot >> 4), h = 2 * kh + ((slot >> 3) & 1), cb = slot & 7;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n = lane & 15, g = lane >> 4;
     const int nch = (T + kC - 1) / kC;
-    if (wave >= 8) {
-        // ---- O waves ------------------------------------------------------
-        const int tt = wave - 8;
-        struct Stage {
-            u32x4_t qe[8];   // Qe token tile tt: [k step][hi, lo]
-            u32x4_t p[4];    // P token tile tt: [k step][hi, lo]
-        };
-        auto fetch = [&](Stage& S, int c) {
-            const size_t ch = static_cast<size_t>(c) * 32 + h;
-            const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
+
+    __shared__ StateSmem sm;
+
+    if (wave == 2 || wave == 3) {
+        // ---- chain waves ----------------------------------------------------
+        const int w = wave - 2;
+        float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * cb + n) * 128 + 64 * w + 4 * g;
+        f32x4_t sT[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                S.qe[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.qeh + ow + 512 * ks);
-                S.qe[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.qel + ow + 512 * ks);
-            }
-            const size_t op = ch * kC * kC + 8 * (tt * 2 * 64 + lane);
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                S.p[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.ph + op + 512 * ks);
-                S.p[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.pl + op + 512 * ks);
-            }
-        };
-        Stage st;
-        fetch(st, 0);
+        for (int k4 = 0; k4 < 4; ++k4) sT[k4] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * k4);
         for (int c = 0; c < nch; ++c) {
-            __syncthreads();   // A(c)
-            u32x4_t sa_h[4], sa_l[4], ua_h[2], ua_l[2];
+            const int s = c & 1;
+            __syncthreads();   // B0(c): stage s holds chunk c
+            const uint16_t* kh_ = sm.kimg[s];
+            const uint16_t* kl_ = sm.kimg[s] + kC * 128;
+            const float* gt = sm.gates[s];
+            // every LDS operand of (a) and (b) requested at once: a wave alone
+            // on its SIMD cannot hide LDS latency behind another wave
+            u32x4_t ka[2][4][2], tb[6][2];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                sa_h[ks] = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
-                sa_l[ks] = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
-            }
+            for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                ua_h[ks] = *reinterpret_cast<const u32x4_t*>(Vh + n * kLT + 32 * ks + 8 * kb);
-                ua_l[ks] = *reinterpret_cast<const u32x4_t*>(Vl + n * kLT + 32 * ks + 8 * kb);
-            }
-            __syncthreads();   // B(c): (the barrier waits for these LDS reads)
-            f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+                for (int tt = 0; tt < 4; ++tt) {
+                    const int o = kimg_off(16 * tt + n, 4 * (2 * w + jj) + g);
+                    ka[jj][tt][0] = *reinterpret_cast<const u32x4_t*>(kh_ + o);
+                    ka[jj][tt][1] = *reinterpret_cast<const u32x4_t*>(kl_ + o);
+                }
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                a0 = mfma_16x16x32_bf16(sa_l[ks], st.qe[2 * ks], a0);
-                a1 = mfma_16x16x32_bf16(sa_h[ks], st.qe[2 * ks + 1], a1);
-                a2 = mfma_16x16x32_bf16(sa_h[ks], st.qe[2 * ks], a2);
+            for (int b6 = 0; b6 < 6; ++b6) {
+                tb[b6][0] = *reinterpret_cast<const u32x4_t*>(sm.top[s] + b6 * kBlk + 8 * lane);
+                tb[b6][1] = *reinterpret_cast<const u32x4_t*>(sm.top[s] + 6 * kBlk + b6 * kBlk + 8 * lane);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            // S_c^T operands for k steps 2w, 2w + 1 (state tiles 2jj, 2jj + 1)
+            u32x4_t bh[2], bl[2];
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                a0 = mfma_16x16x32_bf16(ua_l[ks], st.p[2 * ks], a0);
-                a1 = mfma_16x16x32_bf16(ua_h[ks], st.p[2 * ks + 1], a1);
-                a2 = mfma_16x16x32_bf16(ua_h[ks], st.p[2 * ks], a2);
+            for (int jj = 0; jj < 2; ++jj) {
+                split8(sT[2 * jj], sT[2 * jj + 1], bh[jj], bl[jj]);
+                sm.sb[s][2 * w + jj][lane] = pack_f16x8(sT[2 * jj], sT[2 * jj + 1]);
             }
-            fetch(st, min(c + 1, nch - 1));
-            // O^T[row 4kb + ii][token 16 tt + n] -> pre-norm output (token-major)
-            *reinterpret_cast<f32x4_t*>(po + static_cast<size_t>(c * kC + 16 * tt + n) * 4096 + h * 128 + 16 * rb +
-                                        4 * kb) = a0 + a1 + a2;
+            // (a) partial X over this wave's keys
+            f32x4_t xa[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) xa[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) xa[tt] = mma_x3(ka[jj][tt][0], ka[jj][tt][1], bh[jj], bl[jj], xa[tt]);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) sm.xp[w][tt][lane] = xa[tt];
+            // the transposed K operands of (c), requested before the barrier
+            u32x4_t kt_[2][4][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                // source lane n of group g points at token 32j + 4g + n/4 (+16),
+                // keys 16 kt + 4 (n % 4) .. +3
+                const int r = 32 * j + 4 * g + (n >> 2);
+#pragma unroll
+                for (int k4 = 0; k4 < 4; ++k4) {
+                    const int kt = 4 * w + k4;
+                    const int o = kimg_off(r, 4 * (kt >> 1) + (n & 3)) + 4 * (kt & 1);
+                    const u32x2_t h0 = lds_read_tr16(kh_ + o), h1 = lds_read_tr16(kh_ + o + 16 * 128);
+                    const u32x2_t l0 = lds_read_tr16(kl_ + o), l1 = lds_read_tr16(kl_ + o + 16 * 128);
+                    kt_[j][k4][0] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+                    kt_[j][k4][1] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+                }
+            }
+            __syncthreads();   // B1(c)
+            // (b) Y = beta V - D X; U = T Y
+            f32x4_t y[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const f32x4_t x = xa[tt] + sm.xp[1 - w][tt][lane];
+                const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(gt + kC + 16 * tt + 4 * g);
+                y[tt] = sm.bv[s][tt][lane] - d4 * x;
+            }
+            u32x4_t yh[2], yl[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) split8(y[2 * j], y[2 * j + 1], yh[j], yl[j]);
+            f32x4_t ua[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                ua[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j <= (tt >> 1); ++j)
+                    ua[tt] = mma_x3(tb[tblk(tt, j)][0], tb[tblk(tt, j)][1], yh[j], yl[j], ua[tt]);
+            }
+            // U as fp16 B operands: each chain wave publishes one k step
+            sm.ub[s][w][lane] = w ? pack_f16x8(ua[2], ua[3]) : pack_f16x8(ua[0], ua[1]);
+            // (c) S^T = e^{G_C} S^T + K^T (e^{G_C - G} U)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) ua[tt] *= *reinterpret_cast<const f32x4_t*>(gt + 2 * kC + 16 * tt + 4 * g);
+            u32x4_t uh[2], ul[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) split8(ua[2 * j], ua[2 * j + 1], uh[j], ul[j]);
+            const float gam = gt[3 * kC + kC - 1];
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4) sT[k4] *= gam;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int k4 = 0; k4 < 4; ++k4) sT[k4] = mma_x3(kt_[j][k4][0], kt_[j][k4][1], uh[j], ul[j], sT[k4]);
         }
-    } else if (wave < 4) {
-        // ---- U waves ------------------------------------------------------
-        const int tt = wave;
-        struct Stage {
-            u32x4_t w[8];   // W token tile tt: [k step][hi, lo]
-            u32x4_t ur;     // this thread's 16 B of the block's U~^T rows
-        };
-        auto fetch = [&](Stage& S, int c) {
-            const size_t ch = static_cast<size_t>(c) * 32 + h;
-            const size_t ow = ch * kC * 128 + 8 * (tt * 4 * 64 + lane);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                S.w[2 * ks] = *reinterpret_cast<const u32x4_t*>(in.wh + ow + 512 * ks);
-                S.w[2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.wl + ow + 512 * ks);
-            }
-            const int arr = t >> 7, rem = t & 127;
-            S.ur = *reinterpret_cast<const u32x4_t*>((arr ? in.utl : in.uth) +
-                                                     (ch * 128 + 16 * rb + (rem >> 3)) * kC + 8 * (rem & 7));
-        };
-        auto step = [&](Stage& S, int cn) {
-            {
-                const int arr = t >> 7, rem = t & 127;
-                *reinterpret_cast<u32x4_t*>((arr ? Vl : Vh) + (rem >> 3) * kLT + 8 * (rem & 7)) = S.ur;
-            }
-            __syncthreads();   // A: S_c and U~^T rows in LDS
-            // acc[tok][row] = sum_k W[tok][k] S[row][k] (three accumulators:
-            // lo*hi, hi*lo, hi*hi)
-            f32x4_t a0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const u32x4_t b_h = *reinterpret_cast<const u32x4_t*>(Sh + n * kSA + 32 * ks + 8 * kb);
-                const u32x4_t b_l = *reinterpret_cast<const u32x4_t*>(Sl + n * kSA + 32 * ks + 8 * kb);
-                a0 = mfma_16x16x32_bf16(S.w[2 * ks + 1], b_h, a0);
-                a1 = mfma_16x16x32_bf16(S.w[2 * ks], b_l, a1);
-                a2 = mfma_16x16x32_bf16(S.w[2 * ks], b_h, a2);
-            }
-            const f32x4_t acc = a0 + a1 + a2;
-            // U[tok][row] = U~[tok][row] - acc for row n, tokens 16 tt + 4 kb + ii:
-            // four consecutive tokens of row n in the [row][token] tiles
-            const int o = n * kLT + 16 * tt + 4 * kb;
-            const u32x2_t vh = *reinterpret_cast<const u32x2_t*>(Vh + o);
-            const u32x2_t vl = *reinterpret_cast<const u32x2_t*>(Vl + o);
-            float u[4];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                u[2 * e] = __uint_as_float(vh[e] << 16) + __uint_as_float(vl[e] << 16) - acc[2 * e];
-                u[2 * e + 1] = __uint_as_float(vh[e] & 0xffff0000u) + __uint_as_float(vl[e] & 0xffff0000u) -
-                               acc[2 * e + 1];
-            }
-            uint32_t h0, l0, h1, l1;
-            split_bf16x2(u[0], u[1], h0, l0);
-            split_bf16x2(u[2], u[3], h1, l1);
-            *reinterpret_cast<u32x2_t*>(Uh + o) = u32x2_t{h0, h1};
-            *reinterpret_cast<u32x2_t*>(Ul + o) = u32x2_t{l0, l1};
-            __syncthreads();   // B: U in LDS
-            fetch(S, cn);
-        };
-        Stage s0, s1;
-        fetch(s0, 0);
-        fetch(s1, min(1, nch - 1));
-        int c = 0;
-        for (; c + 1 < nch; c += 2) {
-            step(s0, min(c + 2, nch - 1));
-            step(s1, min(c + 3, nch - 1));
-        }
-        if (c < nch) step(s0, c);
+        for (int k4 = 0; k4 < 4; ++k4) *reinterpret_cast<f32x4_t*>(Sg + 16 * k4) = sT[k4];
+        __syncthreads();   // B0(nch): the helpers form the last chunk's output
     } else {
-        // ---- S waves ------------------------------------------------------
-        // sacc[ct][ii] = S[row n][col 32 sw + 16 ct + 4 kb + ii]: the C tile of
-        // S^T for state columns 32 sw + 16 ct .. +15
-        const int sw = wave - 4;
-        float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * rb + n) * 128 + 32 * sw + 4 * kb;
-        f32x4_t sacc[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) sacc[ct] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * ct);
+        // ---- helper waves ---------------------------------------------------
+        const int hw = wave < 2 ? wave : wave - 2;   // token tile and operand quarter
+        // this wave's quarter of a chunk's operands: K image blocks 8hw .. +7
+        // of 32 (hi then lo), T blocks 3hw .. +2 of 12, beta V token tile hw,
+        // gates (stored by hw 0); P blocks pb, pb + 1 (token tile hw uses
+        // tblk(hw, 0) = pb and, for hw >= 2, tblk(hw, 1) = pb + 1)
+        const int pb = hw < 2 ? hw : 2 * hw - 2;
         struct Stage {
-            u32x4_t k[2][4];   // K~^T column tiles 2 sw + ct: [k step][hi, lo]
-            float gam;
+            u32x4_t k[8];
+            u32x4_t t[3];
+            f32x4_t bv;
+            f32x4_t gt;
+        } hs;
+        struct Out {
+            u32x4_t q[4];   // Q blocks (hw, j)
+            u32x4_t p[2];   // P blocks pb, pb + 1
+        } ho;
+        f32x4_t eg, eg_next;
+        // every helper load is unconditional (a load under a divergent branch
+        // makes the compiler wait for all outstanding loads at the join)
+        auto load_stage = [&](int cc) {
+            const uint16_t* kg = in.kimg + (static_cast<size_t>(cc) * 16 + kh) * kKImg + hw * (8 * kBlk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hs.k[i] = *reinterpret_cast<const u32x4_t*>(kg + i * kBlk + 8 * lane);
+            const uint16_t* tg = in.top + (static_cast<size_t>(cc) * 32 + h) * kTOp + hw * (3 * kBlk);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) hs.t[i] = *reinterpret_cast<const u32x4_t*>(tg + i * kBlk + 8 * lane);
+            const float* vg = in.bv + (static_cast<size_t>(cc) * 32 + h) * kBV + (cb * 4 + hw) * 256;
+            hs.bv = *reinterpret_cast<const f32x4_t*>(vg + 4 * lane);
+            hs.gt = *reinterpret_cast<const f32x4_t*>(in.gates + (static_cast<size_t>(cc) * 32 + h) * kGates + 4 * lane);
         };
-        auto fetch = [&](Stage& S, int c) {
-            const size_t ch = static_cast<size_t>(c) * 32 + h;
+        auto store_stage = [&](int s) {
+            uint16_t* kd = sm.kimg[s] + hw * (8 * kBlk);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const size_t ok = ch * 128 * kC + 8 * ((2 * sw + ct) * 2 * 64 + lane);
+            for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4_t*>(kd + i * kBlk + 8 * lane) = hs.k[i];
+            uint16_t* td = sm.top[s] + hw * (3 * kBlk);
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    S.k[ct][2 * ks] = *reinterpret_cast<const u32x4_t*>(in.kth + ok + 512 * ks);
-                    S.k[ct][2 * ks + 1] = *reinterpret_cast<const u32x4_t*>(in.ktl + ok + 512 * ks);
-                }
-            }
-            S.gam = in.gam[ch];
+            for (int i = 0; i < 3; ++i) *reinterpret_cast<u32x4_t*>(td + i * kBlk + 8 * lane) = hs.t[i];
+            sm.bv[s][hw][lane] = hs.bv;
+            if (hw == 0) *reinterpret_cast<f32x4_t*>(sm.gates[s] + 4 * lane) = hs.gt;
         };
-        // step computes from stage S and refills stage F (last used in the
-        // previous step) with chunk cn = c + 2
-        auto step = [&](Stage& S, Stage& F, int cn) {
-            // publish S_c: row n, four consecutive columns per tile
+        auto load_out = [&](int cc) {
+            const uint16_t* qg = in.qop + (static_cast<size_t>(cc) * 16 + kh) * kQOp + 4 * hw * kBlk;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                uint32_t h0, l0, h1, l1;
-                split_bf16x2(sacc[ct][0], sacc[ct][1], h0, l0);
-                split_bf16x2(sacc[ct][2], sacc[ct][3], h1, l1);
-                const int o = n * kSA + 32 * sw + 16 * ct + 4 * kb;
-                *reinterpret_cast<u32x2_t*>(Sh + o) = u32x2_t{h0, h1};
-                *reinterpret_cast<u32x2_t*>(Sl + o) = u32x2_t{l0, l1};
-            }
-            __syncthreads();   // A
-            fetch(F, cn);
-            const float g = S.gam;
-            __syncthreads();   // B
-            // S^T = e^{G_C} S^T + K~^T U (k = token, 2 steps)
+            for (int i = 0; i < 4; ++i) ho.q[i] = *reinterpret_cast<const u32x4_t*>(qg + i * kBlk + 8 * lane);
+            const uint16_t* pg = in.pop + (static_cast<size_t>(cc) * 32 + h) * kPOp + pb * kBlk;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u32x4_t b_h = *reinterpret_cast<const u32x4_t*>(Uh + n * kLT + 32 * ks + 8 * kb);
-                const u32x4_t b_l = *reinterpret_cast<const u32x4_t*>(Ul + n * kLT + 32 * ks + 8 * kb);
+            for (int i = 0; i < 2; ++i) ho.p[i] = *reinterpret_cast<const u32x4_t*>(pg + i * kBlk + 8 * lane);
+        };
+        auto output = [&](int cc) {
+            const int s = cc & 1;
+            f32x4_t o = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    if (ks == 0) sacc[ct] *= g;
-                    f32x4_t s1 = mfma_16x16x32_bf16(S.k[ct][2 * ks + 1], b_h, f32x4_t{0.f, 0.f, 0.f, 0.f});
-                    s1 = mfma_16x16x32_bf16(S.k[ct][2 * ks], b_l, s1);
-                    sacc[ct] = mfma_16x16x32_bf16(S.k[ct][2 * ks], b_h, sacc[ct]);
-                    sacc[ct] += s1;
-                }
+            for (int j = 0; j < 4; ++j) o = mfma_16x16x32_f16(ho.q[j], sm.sb[s][j][lane], o);
+            o *= eg;
+            o = mfma_16x16x32_f16(ho.p[0], sm.ub[s][0][lane], o);
+            if (hw >= 2) o = mfma_16x16x32_f16(ho.p[1], sm.ub[s][1][lane], o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = cc * kC + 16 * hw + 4 * g + i;
+                if (tok < T) po[static_cast<size_t>(tok) * 4096 + 128 * h + 16 * cb + n] = o[i];
             }
         };
-        Stage s0, s1, s2;
-        fetch(s0, 0);
-        fetch(s1, min(1, nch - 1));
-        int c = 0;
-        for (; c + 2 < nch; c += 3) {
-            step(s0, s2, min(c + 2, nch - 1));
-            step(s1, s0, min(c + 3, nch - 1));
-            step(s2, s1, min(c + 4, nch - 1));
+        load_stage(0);
+        store_stage(0);
+        if (nch > 1) load_stage(1);
+        // step c: after B0(c) only e^G of chunk c is copied (stage c is
+        // rewritten in step c + 1), so the chain never waits for a helper at
+        // B1; after B1(c) the output of chunk c - 1 (its S^T and U stay in
+        // their parity buffers until step c + 1), then chunk c + 1 into the
+        // free stage and the loads of the next two chunks.
+        load_out(0);
+        for (int c = 0; c < nch; ++c) {
+            __syncthreads();   // B0(c)
+            eg_next = *reinterpret_cast<const f32x4_t*>(sm.gates[c & 1] + 3 * kC + 16 * hw + 4 * g);
+            __syncthreads();   // B1(c)
+            if (c > 0) {
+                output(c - 1);
+                load_out(c);
+            }
+            eg = eg_next;
+            if (c + 1 < nch) store_stage((c + 1) & 1);
+            if (c + 2 < nch) load_stage(c + 2);
         }
-        if (c < nch) step(s0, s2, min(c + 2, nch - 1));
-        if (c + 1 < nch) step(s1, s0, c + 1);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) *reinterpret_cast<f32x4_t*>(Sg + 16 * ct) = sacc[ct];
+        __syncthreads();   // B0(nch)
+        output(nch - 1);
     }
 }
 
@@ -938,12 +827,13 @@ hipError_t launch_deltanet_chunked(qff_ctx* ctx, hipStream_t stream, const qff_d
                                    const void* qkv, qff_dtype in_dtype, const float* a, const float* b,
                                    const float* conv_state, float* ssm_state, int T) {
     const int nch = (T + kC - 1) / kC;
+    const bool bf = in_dtype == QFF_BF16;
     {
         ProfScope prof(ctx, stream, "dn_chunk_local");
         const int units = nch * 16;   // (chunk, key head)
         const int grid = std::min(units, std::max(ctx->num_cu, 1));
         unsigned* sched = ctx->sched + 2 * kSchedChunkLocal;
-        if (in_dtype == QFF_BF16)
+        if (bf)
             dn_chunk_local_kernel<1><<<grid, kLocalThreads, 0, stream>>>(T, qkv, a, b, p->a_log, p->dt_bias,
                                                                          p->conv_w, conv_state, ctx->dn, sched);
         else

@@ -18,12 +18,12 @@ struct qff_prof_record {
 // Chunked DeltaNet prefill intermediates, one block per (chunk, value head),
 // each array split into bf16 hi / lo halves.
 struct qff_dn_bufs {
-    uint16_t *wh, *wl;      // W [64][128]
-    uint16_t *qeh, *qel;    // Qe = e^G Q - P W [64][128]
-    uint16_t *kth, *ktl;    // K~^T = (e^{G_C - G} K)^T [128][64]
-    uint16_t *uth, *utl;    // U~^T [128][64]
-    uint16_t *ph, *pl;      // P [64][64]
-    float* gam;             // e^{G_C}
+    uint16_t* kimg;   // per (chunk, key head): K hi, lo [64][128] in the state pass's LDS image order
+    uint16_t* qop;    // per (chunk, key head): Q fp16, 16 MFMA operand blocks
+    uint16_t* top;    // per (chunk, value head): T = (I + A)^-1 hi, lo, 6 operand blocks each
+    uint16_t* pop;    // per (chunk, value head): P fp16, 6 operand blocks
+    float* gates;     // per (chunk, value head): beta, beta e^G, e^{G_C - G}, e^G [4][64]
+    float* bv;        // per (chunk, value head): beta V [64][128] in the state pass's lane order
 };
 
 struct qff_ctx {
@@ -71,7 +71,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, pf_o, dn_arrive, sched, wh, wl, qeh, qel, kth, ktl, uth, utl, ph, pl, gam;
+    size_t gqa_qb, q4_xs, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);
