@@ -30,11 +30,11 @@
 //       pass's LDS image), Q (fp16), T (bf16 hi/lo), P (fp16) as MFMA operand
 //       blocks, beta V and the per-token gate factors.
 //   dn_chunk_state_kernel  one workgroup per (16 state rows, value head)
-//       walks the chunks in order: two chain waves hold the block's state
-//       (key halves) in accumulators and form X = K S^T, U = T (beta V - D X)
-//       and the state update; four helper waves stage the next chunk's
-//       operands in LDS and form the pre-norm output rows
-//       O = diag(e^G) Q S^T + P U one chunk behind.
+//       walks the chunks in order: four chain waves hold the block's state
+//       (key quarters) in accumulators and form X = K S^T, U = T (beta V -
+//       D X) and the state update, a token tile or key quarter each; four
+//       helper waves stage the next chunk's operands in LDS and form the
+//       pre-norm output rows O = diag(e^G) Q S^T + P U one chunk behind.
 //
 // Operand order. A 16x16x32 MFMA gives lane l of its A and B operands the
 // 8 k-elements e = 0..7 of lane group g = l / 16; here they are the k indices
@@ -581,42 +581,62 @@ __device__ __forceinline__ f32x4_t mma_x3(u32x4_t ah, u32x4_t al, u32x4_t bh, u3
 }
 
 // LDS of the state pass: two stages of chunk operands (filled by the helper
-// waves one chunk ahead) and the exchange buffers.
+// waves one chunk ahead) and the pieces the chain waves exchange.
 struct StateSmem {
-    uint16_t kimg[2][kKImg];      // [stage] K hi | lo image
-    uint16_t top[2][kTOp];        // [stage] T hi | lo blocks
-    f32x4_t bv[2][4][64];         // [stage][token tile][lane] beta V of the block's rows
-    float gates[2][kGates];       // [stage] beta, beta e^G, e^{G_C - G}, e^G
-    f32x4_t xp[2][4][64];         // [chain wave][token tile][lane] partial X
-    u32x4_t sb[2][4][64];         // [chunk parity][k step][lane] S^T fp16 B operands
-    u32x4_t ub[2][2][64];         // [chunk parity][k step][lane] U fp16 B operands
+    uint16_t kimg[2][kKImg];        // [stage] K hi | lo image
+    uint16_t top[2][kTOp];          // [stage] T hi | lo blocks
+    f32x4_t bv[2][4][64];           // [stage][token tile][lane] beta V of the block's rows
+    float gates[2][kGates];         // [stage] beta, beta e^G, e^{G_C - G}, e^G
+    u32x4_t sop[4][2][64];          // [k step][hi, lo][lane] S^T bf16 B operands
+    u32x4_t sf[3][4][64];           // [chunk % 3][k step][lane] S^T fp16 B operands
+    uint32_t yop[2][2][64][4];      // [k step][hi, lo][lane][tile parity x 2] Y bf16 B operands
+    uint32_t uop[2][2][64][4];      // [k step][hi, lo][lane][...] e^{G_C - G} U bf16 B operands
+    uint32_t uf[2][2][64][4];       // [chunk parity][k step][lane][...] U fp16 B operands
+    unsigned sync;                  // arrivals of the chain waves at their own barriers
 };
 
-// One workgroup of 384 threads per (16-row block cb of the state, value head
+// Barrier of the four chain waves only (the helper waves keep running): lane
+// 0 counts the wave in once its LDS writes have completed, then the wave
+// waits for the count of the barrier's round. Every chain wave arrives at
+// every round, so every wait ends.
+__device__ __forceinline__ void chain_sync(unsigned* cnt, unsigned target, int lane) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes done
+    if (lane == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+        __builtin_amdgcn_s_sleep(1);
+}
+
+// One workgroup of 512 threads per (16-row block cb of the state, value head
 // h), a 1-D grid of 256. Workgroups go to the 8 XCDs round-robin by linear
 // id; the id -> (head, block) map puts both value heads of two key heads on
 // each XCD, so its L2 serves the K image all 16 blocks of a key head share.
 // Lane l = (n, g) = (l % 16, l / 16): state row 16 cb + n.
 //
-// Chain waves 2, 3 (w = wave - 2, each alone on its SIMD): hold S^T for keys
-// 64w .. 64w+63 as four 16x16 accumulator tiles (S^T[16 kt + 4g + i][n]),
-// and per chunk c:
-//   (a) X_w = K[:, keys of w] S^T: 4 token tiles x 2 k steps, B = the state
-//       tiles in registers (pq order), A = K image rows from LDS; partial X
-//       to LDS; S_c^T also published as fp16 B operands for the output.
-//   [barrier B1]
-//   (b) X = X_0 + X_1 (both waves form the same sum), Y = beta V - D X,
-//       U = T Y (Y's accumulators are its B operand), U published as fp16;
-//   (c) S^T = e^{G_C} S^T + K^T diag(e^{G_C - G}) U: A = K^T through the LDS
-//       transpose read of the same image, B = the scaled U tiles.
-//   [barrier B0 of chunk c + 1]
-// Helper waves 0, 1, 4, 5 (hw = 0 .. 3), after B1(c): the output rows of
-// chunk c - 1, token tile hw: O = diag(e^G) Q S^T + P U on fp16 MFMAs (Q, P
-// blocks in registers, loaded a chunk earlier; S^T, U from LDS) to the
-// pre-norm output; then a quarter of chunk c + 1's operands (K image, T,
-// beta V, gates) into the free stage from registers loaded a chunk earlier,
-// and the loads of chunk c + 2.
-constexpr int kStateThreads = 384;
+// Chain waves 0-3 (w, one per SIMD) split every product of a chunk step four
+// ways, so each reads a quarter of its LDS operands (a wave draws ~1 KB per
+// 30 cycles from LDS, and one wave reading all of them was the bound). Wave
+// w holds S^T for keys 32w .. 32w+31 (key tiles 2w, 2w+1, S^T[16 kt + 4g +
+// i][n]) and owns token tile w. Per chunk c:
+//   (a) X_w = K[tokens of tile w, :] S^T over all four k steps: A = K image
+//       rows from LDS, B = S^T operands (its own k step from registers, the
+//       others as published by their waves); Y_w = beta V - D X_w, split
+//       bf16 hi / lo and published as its half of Y's k-step operand;
+//   [C1: the chain waves only]
+//   (b) U_w = T[tile w, :] Y (k steps j <= w / 2); U_w published as fp16 (for
+//       the output) and e^{G_C - G} U_w as bf16 hi / lo operand halves;
+//   [C2: the chain waves only]
+//   (c) S^T[keys of w] = e^{G_C} S^T + K^T diag(e^{G_C - G}) U: A = K^T through
+//       the LDS transpose read of the image, B = the scaled U operands; the
+//       new S^T published as bf16 (next step) and fp16 (output) operands.
+//   [B0 of chunk c + 1: the whole workgroup]
+// Helper waves 4-7 (hw, token tile hw) meet the chain only at B0. Between
+// B0(c) and B0(c + 1): the output rows of chunk c - 1, O = diag(e^G) Q S^T +
+// P U on fp16 MFMAs (Q, P blocks in registers, loaded a chunk earlier; S^T
+// of chunk c - 1 stays published until the end of step c + 1, hence three
+// buffers) to the pre-norm output; a quarter of chunk c + 1's operands (K
+// image, T, beta V, gates) into the free stage from registers loaded a chunk
+// earlier; the loads of chunk c + 2.
+constexpr int kStateThreads = 512;
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
                                                                       float* __restrict__ ssm_state,
@@ -629,113 +649,115 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
     const int nch = (T + kC - 1) / kC;
 
     __shared__ StateSmem sm;
+    if (t == 0) sm.sync = 0;   // published by the first B0
 
-    if (wave == 2 || wave == 3) {
+    if (wave < 4) {
         // ---- chain waves ----------------------------------------------------
-        const int w = wave - 2;
-        float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * cb + n) * 128 + 64 * w + 4 * g;
-        f32x4_t sT[4];
+        const int w = wave;
+        float* Sg = ssm_state + (static_cast<size_t>(h) * 128 + 16 * cb + n) * 128 + 32 * w + 4 * g;
+        f32x4_t sT[2];
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) sT[k4] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * k4);
+        for (int k2 = 0; k2 < 2; ++k2) sT[k2] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * k2);
+        u32x4_t bh, bl;   // this wave's k step of the S^T operands
+        auto publish_state = [&](int par) {
+            split8(sT[0], sT[1], bh, bl);
+            sm.sop[w][0][lane] = bh;
+            sm.sop[w][1][lane] = bl;
+            sm.sf[par][w][lane] = pack_f16x8(sT[0], sT[1]);
+        };
+        publish_state(0);
         for (int c = 0; c < nch; ++c) {
             const int s = c & 1;
-            __syncthreads();   // B0(c): stage s holds chunk c
+            __syncthreads();   // B0(c): stage s holds chunk c; S_c published
             const uint16_t* kh_ = sm.kimg[s];
             const uint16_t* kl_ = sm.kimg[s] + kC * 128;
             const float* gt = sm.gates[s];
-            // every LDS operand of (a) and (b) requested at once: a wave alone
-            // on its SIMD cannot hide LDS latency behind another wave
-            u32x4_t ka[2][4][2], tb[6][2];
+            // (a) X_w over all keys, then Y_w
+            u32x4_t ka[4][2], sb[4][2];
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
+            for (int j = 0; j < 4; ++j) {
+                const int o = kimg_off(16 * w + n, 4 * j + g);
+                ka[j][0] = *reinterpret_cast<const u32x4_t*>(kh_ + o);
+                ka[j][1] = *reinterpret_cast<const u32x4_t*>(kl_ + o);
+                sb[j][0] = sm.sop[j][0][lane];
+                sb[j][1] = sm.sop[j][1][lane];
+            }
+            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(gt + kC + 16 * w + 4 * g);
+            const f32x4_t bv = sm.bv[s][w][lane];
+            f32x4_t xa = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
-                    const int o = kimg_off(16 * tt + n, 4 * (2 * w + jj) + g);
-                    ka[jj][tt][0] = *reinterpret_cast<const u32x4_t*>(kh_ + o);
-                    ka[jj][tt][1] = *reinterpret_cast<const u32x4_t*>(kl_ + o);
+            for (int j = 0; j < 4; ++j) xa = mma_x3(ka[j][0], ka[j][1], sb[j][0], sb[j][1], xa);
+            const f32x4_t y = bv - d4 * xa;
+            {
+                uint32_t h0, l0, h1, l1;
+                split_bf16x2(y[0], y[1], h0, l0);
+                split_bf16x2(y[2], y[3], h1, l1);
+                uint32_t* yh = sm.yop[w >> 1][0][lane] + 2 * (w & 1);
+                uint32_t* yl = sm.yop[w >> 1][1][lane] + 2 * (w & 1);
+                *reinterpret_cast<u32x2_t*>(yh) = u32x2_t{h0, h1};
+                *reinterpret_cast<u32x2_t*>(yl) = u32x2_t{l0, l1};
+            }
+            chain_sync(&sm.sync, 8 * c + 4, lane);   // C1(c)
+            // (b) U_w = T[tile w, :] Y
+            f32x4_t ua = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (j <= (w >> 1)) {
+                    const int o = tblk(w, j) * kBlk + 8 * lane;
+                    const u32x4_t th = *reinterpret_cast<const u32x4_t*>(sm.top[s] + o);
+                    const u32x4_t tl = *reinterpret_cast<const u32x4_t*>(sm.top[s] + 6 * kBlk + o);
+                    ua = mma_x3(th, tl, *reinterpret_cast<const u32x4_t*>(sm.yop[j][0][lane]),
+                                *reinterpret_cast<const u32x4_t*>(sm.yop[j][1][lane]), ua);
                 }
-#pragma unroll
-            for (int b6 = 0; b6 < 6; ++b6) {
-                tb[b6][0] = *reinterpret_cast<const u32x4_t*>(sm.top[s] + b6 * kBlk + 8 * lane);
-                tb[b6][1] = *reinterpret_cast<const u32x4_t*>(sm.top[s] + 6 * kBlk + b6 * kBlk + 8 * lane);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            // S_c^T operands for k steps 2w, 2w + 1 (state tiles 2jj, 2jj + 1)
-            u32x4_t bh[2], bl[2];
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                split8(sT[2 * jj], sT[2 * jj + 1], bh[jj], bl[jj]);
-                sm.sb[s][2 * w + jj][lane] = pack_f16x8(sT[2 * jj], sT[2 * jj + 1]);
+            {
+                const f32x4_t e4 = *reinterpret_cast<const f32x4_t*>(gt + 2 * kC + 16 * w + 4 * g);
+                *reinterpret_cast<u32x2_t*>(sm.uf[s][w >> 1][lane] + 2 * (w & 1)) =
+                    u32x2_t{pack_f16x2(ua[0], ua[1]), pack_f16x2(ua[2], ua[3])};
+                const f32x4_t us = ua * e4;
+                uint32_t h0, l0, h1, l1;
+                split_bf16x2(us[0], us[1], h0, l0);
+                split_bf16x2(us[2], us[3], h1, l1);
+                *reinterpret_cast<u32x2_t*>(sm.uop[w >> 1][0][lane] + 2 * (w & 1)) = u32x2_t{h0, h1};
+                *reinterpret_cast<u32x2_t*>(sm.uop[w >> 1][1][lane] + 2 * (w & 1)) = u32x2_t{l0, l1};
             }
-            // (a) partial X over this wave's keys
-            f32x4_t xa[4];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) xa[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) xa[tt] = mma_x3(ka[jj][tt][0], ka[jj][tt][1], bh[jj], bl[jj], xa[tt]);
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) sm.xp[w][tt][lane] = xa[tt];
             // the transposed K operands of (c), requested before the barrier
-            u32x4_t kt_[2][4][2];
+            u32x4_t kt_[2][2][2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 // source lane n of group g points at token 32j + 4g + n/4 (+16),
-                // keys 16 kt + 4 (n % 4) .. +3
+                // keys 16 kt + 4 (n % 4) .. +3 of key tile kt = 2w + k2
                 const int r = 32 * j + 4 * g + (n >> 2);
+                const int o = kimg_off(r, 4 * w + (n & 3));
 #pragma unroll
-                for (int k4 = 0; k4 < 4; ++k4) {
-                    const int kt = 4 * w + k4;
-                    const int o = kimg_off(r, 4 * (kt >> 1) + (n & 3)) + 4 * (kt & 1);
-                    const u32x2_t h0 = lds_read_tr16(kh_ + o), h1 = lds_read_tr16(kh_ + o + 16 * 128);
-                    const u32x2_t l0 = lds_read_tr16(kl_ + o), l1 = lds_read_tr16(kl_ + o + 16 * 128);
-                    kt_[j][k4][0] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
-                    kt_[j][k4][1] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    const int ok = o + 4 * k2;
+                    const u32x2_t h0 = lds_read_tr16(kh_ + ok), h1 = lds_read_tr16(kh_ + ok + 16 * 128);
+                    const u32x2_t l0 = lds_read_tr16(kl_ + ok), l1 = lds_read_tr16(kl_ + ok + 16 * 128);
+                    kt_[j][k2][0] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+                    kt_[j][k2][1] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
                 }
             }
-            __syncthreads();   // B1(c)
-            // (b) Y = beta V - D X; U = T Y
-            f32x4_t y[4];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const f32x4_t x = xa[tt] + sm.xp[1 - w][tt][lane];
-                const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(gt + kC + 16 * tt + 4 * g);
-                y[tt] = sm.bv[s][tt][lane] - d4 * x;
-            }
-            u32x4_t yh[2], yl[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) split8(y[2 * j], y[2 * j + 1], yh[j], yl[j]);
-            f32x4_t ua[4];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                ua[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j <= (tt >> 1); ++j)
-                    ua[tt] = mma_x3(tb[tblk(tt, j)][0], tb[tblk(tt, j)][1], yh[j], yl[j], ua[tt]);
-            }
-            // U as fp16 B operands: each chain wave publishes one k step
-            sm.ub[s][w][lane] = w ? pack_f16x8(ua[2], ua[3]) : pack_f16x8(ua[0], ua[1]);
-            // (c) S^T = e^{G_C} S^T + K^T (e^{G_C - G} U)
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) ua[tt] *= *reinterpret_cast<const f32x4_t*>(gt + 2 * kC + 16 * tt + 4 * g);
-            u32x4_t uh[2], ul[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) split8(ua[2 * j], ua[2 * j + 1], uh[j], ul[j]);
             const float gam = gt[3 * kC + kC - 1];
+            chain_sync(&sm.sync, 8 * c + 8, lane);   // C2(c)
+            // (c) S^T[keys of w] = e^{G_C} S^T + K^T (e^{G_C - G} U)
 #pragma unroll
-            for (int k4 = 0; k4 < 4; ++k4) sT[k4] *= gam;
+            for (int k2 = 0; k2 < 2; ++k2) sT[k2] *= gam;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j) {
+                const u32x4_t uh = *reinterpret_cast<const u32x4_t*>(sm.uop[j][0][lane]);
+                const u32x4_t ul = *reinterpret_cast<const u32x4_t*>(sm.uop[j][1][lane]);
 #pragma unroll
-                for (int k4 = 0; k4 < 4; ++k4) sT[k4] = mma_x3(kt_[j][k4][0], kt_[j][k4][1], uh[j], ul[j], sT[k4]);
+                for (int k2 = 0; k2 < 2; ++k2) sT[k2] = mma_x3(kt_[j][k2][0], kt_[j][k2][1], uh, ul, sT[k2]);
+            }
+            publish_state((c + 1) % 3);
         }
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) *reinterpret_cast<f32x4_t*>(Sg + 16 * k4) = sT[k4];
+        for (int k2 = 0; k2 < 2; ++k2) *reinterpret_cast<f32x4_t*>(Sg + 16 * k2) = sT[k2];
         __syncthreads();   // B0(nch): the helpers form the last chunk's output
     } else {
         // ---- helper waves ---------------------------------------------------
-        const int hw = wave < 2 ? wave : wave - 2;   // token tile and operand quarter
+        const int hw = wave - 4;   // token tile and operand quarter
         // this wave's quarter of a chunk's operands: K image blocks 8hw .. +7
         // of 32 (hi then lo), T blocks 3hw .. +2 of 12, beta V token tile hw,
         // gates (stored by hw 0); P blocks pb, pb + 1 (token tile hw uses
@@ -784,13 +806,13 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             for (int i = 0; i < 2; ++i) ho.p[i] = *reinterpret_cast<const u32x4_t*>(pg + i * kBlk + 8 * lane);
         };
         auto output = [&](int cc) {
-            const int s = cc & 1;
+            const int par = cc & 1;
             f32x4_t o = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o = mfma_16x16x32_f16(ho.q[j], sm.sb[s][j][lane], o);
+            for (int j = 0; j < 4; ++j) o = mfma_16x16x32_f16(ho.q[j], sm.sf[cc % 3][j][lane], o);
             o *= eg;
-            o = mfma_16x16x32_f16(ho.p[0], sm.ub[s][0][lane], o);
-            if (hw >= 2) o = mfma_16x16x32_f16(ho.p[1], sm.ub[s][1][lane], o);
+            o = mfma_16x16x32_f16(ho.p[0], *reinterpret_cast<const u32x4_t*>(sm.uf[par][0][lane]), o);
+            if (hw >= 2) o = mfma_16x16x32_f16(ho.p[1], *reinterpret_cast<const u32x4_t*>(sm.uf[par][1][lane]), o);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tok = cc * kC + 16 * hw + 4 * g + i;
@@ -800,16 +822,12 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
         load_stage(0);
         store_stage(0);
         if (nch > 1) load_stage(1);
-        // step c: after B0(c) only e^G of chunk c is copied (stage c is
-        // rewritten in step c + 1), so the chain never waits for a helper at
-        // B1; after B1(c) the output of chunk c - 1 (its S^T and U stay in
-        // their parity buffers until step c + 1), then chunk c + 1 into the
-        // free stage and the loads of the next two chunks.
         load_out(0);
         for (int c = 0; c < nch; ++c) {
             __syncthreads();   // B0(c)
             eg_next = *reinterpret_cast<const f32x4_t*>(sm.gates[c & 1] + 3 * kC + 16 * hw + 4 * g);
-            __syncthreads();   // B1(c)
+            // chunk c - 1's S^T and U stay published until the chain's (c) and
+            // (b) of chunk c + 1
             if (c > 0) {
                 output(c - 1);
                 load_out(c);
