@@ -633,14 +633,14 @@ __device__ __forceinline__ void chain_sync(unsigned* cnt, unsigned target, int l
 // B0(c) and B0(c + 1): the output rows of chunk c - 1, O = diag(e^G) Q S^T +
 // P U on fp16 MFMAs (Q, P blocks in registers, loaded a chunk earlier; S^T
 // of chunk c - 1 stays published until the end of step c + 1, hence three
-// buffers) to the pre-norm output; a quarter of chunk c + 1's operands (K
+// buffers) to the pre-norm output (fp16: it only feeds the gated RMSNorm); a quarter of chunk c + 1's operands (K
 // image, T, beta V, gates) into the free stage from registers loaded a chunk
 // earlier; the loads of chunk c + 2.
 constexpr int kStateThreads = 512;
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
                                                                       float* __restrict__ ssm_state,
-                                                                      float* __restrict__ po) {
+                                                                      uint16_t* __restrict__ po) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
     const int kh = 2 * xcd + (slot >> 4), h = 2 * kh + ((slot >> 3) & 1), cb = slot & 7;
     const int t = threadIdx.x, lane = t & 63;
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tok = cc * kC + 16 * hw + 4 * g + i;
-                if (tok < T) po[static_cast<size_t>(tok) * 4096 + 128 * h + 16 * cb + n] = o[i];
+                if (tok < T) po[static_cast<size_t>(tok) * 4096 + 128 * h + 16 * cb + n] = f32_to_f16(o[i]);
             }
         };
         load_stage(0);

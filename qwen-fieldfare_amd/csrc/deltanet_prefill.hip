@@ -6,7 +6,7 @@
 // computes the same result for a whole sequence:
 //   chunked    conv1d + SiLU, L2 norms, gates and the chunked WY form of the
 //              gated delta rule (deltanet_chunked.hip), pre-norm outputs to
-//              workspace;
+//              workspace (fp16);
 //   norm       gated RMSNorm of every (token, value head) output row, and
 //              (32 extra workgroups of the same launch) the conv state after
 //              the last token.
@@ -25,7 +25,14 @@ __device__ __forceinline__ float conv_ext(const float* __restrict__ conv_state, 
 
 // 8 consecutive elements of a dtype-DT row in one or two 16-B accesses.
 template <int DT> __device__ __forceinline__ void load8(const void* p, size_t i, float (&x)[8]) {
-    if (DT == 1) {
+    if (DT == 2) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = f16_to_f32(static_cast<uint16_t>(v[k]));
+            x[2 * k + 1] = f16_to_f32(static_cast<uint16_t>(v[k] >> 16));
+        }
+    } else if (DT == 1) {
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -57,7 +64,7 @@ template <int DT> __device__ __forceinline__ void store8(void* p, size_t i, cons
 // grid (T + 32), 256 threads: thread -> value head t/8, rows 16*(t%8) .. +15;
 // the 32 workgroups past the tokens write the conv state after the last token.
 template <int IN_DT, int OUT_DT>
-__global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __restrict__ po,
+__global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const uint16_t* __restrict__ po,
                                                               const void* __restrict__ z,
                                                               const float* __restrict__ norm_w, float eps,
                                                               void* __restrict__ out, int T,
@@ -79,8 +86,8 @@ __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __res
     const int r0 = 16 * (t & 7);
     const size_t base = static_cast<size_t>(tok) * 4096 + (t >> 3) * 128 + r0;
     float o[2][8], zz[2][8], ss = 0.0f;
-    load8<0>(po, base, o[0]);
-    load8<0>(po, base + 8, o[1]);
+    load8<2>(po, base, o[0]);
+    load8<2>(po, base + 8, o[1]);
     load8<IN_DT>(z, base, zz[0]);
     load8<IN_DT>(z, base + 8, zz[1]);
 #pragma unroll

@@ -44,7 +44,7 @@ struct qff_ctx {
     int q4_xs_tokens = 0;
     // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
     // chunk intermediates.
-    float* pf_o = nullptr;
+    uint16_t* pf_o = nullptr;
     qff_dn_bufs dn{};
     // DeltaNet decode: per (sequence, key head) arrival counters [max_batch][16],
     // zero between launches (the second arrival resets its counter).
