@@ -423,6 +423,9 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             }
 #pragma unroll
             for (int cj = 0; cj < 4; ++cj) {
+                // A is read only on and below its diagonal blocks; P's operand
+                // blocks cover columns 0-31 for row tiles 0, 1
+                if (role == 0 ? cj > rt : (rt < 2 && cj >= 2)) continue;
                 const int j = 16 * cj + n;
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
