@@ -587,9 +587,6 @@ __device__ __forceinline__ f32x4_t mma_x3(u32x4_t ah, u32x4_t al, u32x4_t bh, u3
 // waves one chunk ahead) and the pieces the chain waves exchange.
 struct StateSmem {
     uint16_t kimg[2][kKImg];        // [stage] K hi | lo image
-    uint16_t top[2][kTOp];          // [stage] T hi | lo blocks
-    f32x4_t bv[2][4][64];           // [stage][token tile][lane] beta V of the block's rows
-    float gates[2][kGates];         // [stage] beta, beta e^G, e^{G_C - G}, e^G
     u32x4_t sop[4][2][64];          // [k step][hi, lo][lane] S^T bf16 B operands
     u32x4_t sf[3][4][64];           // [chunk % 3][k step][lane] S^T fp16 B operands
     uint32_t yop[2][2][64][4];      // [k step][hi, lo][lane][tile parity x 2] Y bf16 B operands
@@ -619,7 +616,9 @@ __device__ __forceinline__ void chain_sync(unsigned* cnt, unsigned target, int l
 // ways, so each reads a quarter of its LDS operands (a wave draws ~1 KB per
 // 30 cycles from LDS, and one wave reading all of them was the bound). Wave
 // w holds S^T for keys 32w .. 32w+31 (key tiles 2w, 2w+1, S^T[16 kt + 4g +
-// i][n]) and owns token tile w. Per chunk c:
+// i][n]) and owns token tile w; the chunk data only it reads (its T blocks,
+// beta V, gate factors) come from L2 into registers a chunk ahead, so only
+// the K image, which all four read, goes through LDS. Per chunk c:
 //   (a) X_w = K[tokens of tile w, :] S^T over all four k steps: A = K image
 //       rows from LDS, B = S^T operands (its own k step from registers, the
 //       others as published by their waves); Y_w = beta V - D X_w, split
@@ -636,9 +635,9 @@ __device__ __forceinline__ void chain_sync(unsigned* cnt, unsigned target, int l
 // B0(c) and B0(c + 1): the output rows of chunk c - 1, O = diag(e^G) Q S^T +
 // P U on fp16 MFMAs (Q, P blocks in registers, loaded a chunk earlier; S^T
 // of chunk c - 1 stays published until the end of step c + 1, hence three
-// buffers) to the pre-norm output (fp16: it only feeds the gated RMSNorm); a quarter of chunk c + 1's operands (K
-// image, T, beta V, gates) into the free stage from registers loaded a chunk
-// earlier; the loads of chunk c + 2.
+// buffers) to the pre-norm output (fp16: it only feeds the gated RMSNorm);
+// a quarter of chunk c + 1's K image into the free stage from registers
+// loaded a chunk earlier; the loads of chunk c + 2.
 constexpr int kStateThreads = 512;
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
@@ -669,12 +668,34 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             sm.sf[par][w][lane] = pack_f16x8(sT[0], sT[1]);
         };
         publish_state(0);
-        for (int c = 0; c < nch; ++c) {
+        // this wave's own chunk operands, loaded from L2 a chunk ahead: T
+        // blocks tblk(w, 0 .. 1) (hi, lo), beta V of token tile w, D and
+        // e^{G_C - G} of its tokens and e^{G_C}
+        struct ChainIn {
+            u32x4_t t[2][2];
+            f32x4_t bv, d4, e4;
+            float gam;
+        };
+        const int tb0 = w < 2 ? w : 2 * w - 2, tb1 = w < 2 ? tb0 : tb0 + 1;
+        auto load_in = [&](ChainIn& r, int cc) {
+            const uint16_t* tg = in.top + (static_cast<size_t>(cc) * 32 + h) * kTOp + 8 * lane;
+            r.t[0][0] = *reinterpret_cast<const u32x4_t*>(tg + tb0 * kBlk);
+            r.t[0][1] = *reinterpret_cast<const u32x4_t*>(tg + 6 * kBlk + tb0 * kBlk);
+            r.t[1][0] = *reinterpret_cast<const u32x4_t*>(tg + tb1 * kBlk);
+            r.t[1][1] = *reinterpret_cast<const u32x4_t*>(tg + 6 * kBlk + tb1 * kBlk);
+            r.bv = *reinterpret_cast<const f32x4_t*>(in.bv + (static_cast<size_t>(cc) * 32 + h) * kBV +
+                                                     (cb * 4 + w) * 256 + 4 * lane);
+            const float* gg = in.gates + (static_cast<size_t>(cc) * 32 + h) * kGates;
+            r.d4 = *reinterpret_cast<const f32x4_t*>(gg + kC + 16 * w + 4 * g);
+            r.e4 = *reinterpret_cast<const f32x4_t*>(gg + 2 * kC + 16 * w + 4 * g);
+            r.gam = gg[3 * kC + kC - 1];
+        };
+        auto step = [&](int c, const ChainIn& ci, ChainIn& next) {
             const int s = c & 1;
             __syncthreads();   // B0(c): stage s holds chunk c; S_c published
+            load_in(next, min(c + 1, nch - 1));
             const uint16_t* kh_ = sm.kimg[s];
             const uint16_t* kl_ = sm.kimg[s] + kC * 128;
-            const float* gt = sm.gates[s];
             // (a) X_w over all keys, then Y_w
             u32x4_t ka[4][2], sb[4][2];
 #pragma unroll
@@ -685,12 +706,10 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
                 sb[j][0] = sm.sop[j][0][lane];
                 sb[j][1] = sm.sop[j][1][lane];
             }
-            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(gt + kC + 16 * w + 4 * g);
-            const f32x4_t bv = sm.bv[s][w][lane];
             f32x4_t xa = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) xa = mma_x3(ka[j][0], ka[j][1], sb[j][0], sb[j][1], xa);
-            const f32x4_t y = bv - d4 * xa;
+            const f32x4_t y = ci.bv - ci.d4 * xa;
             {
                 uint32_t h0, l0, h1, l1;
                 split_bf16x2(y[0], y[1], h0, l0);
@@ -705,16 +724,12 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             f32x4_t ua = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                if (j <= (w >> 1)) {
-                    const int o = tblk(w, j) * kBlk + 8 * lane;
-                    const u32x4_t th = *reinterpret_cast<const u32x4_t*>(sm.top[s] + o);
-                    const u32x4_t tl = *reinterpret_cast<const u32x4_t*>(sm.top[s] + 6 * kBlk + o);
-                    ua = mma_x3(th, tl, *reinterpret_cast<const u32x4_t*>(sm.yop[j][0][lane]),
+                if (j <= (w >> 1))
+                    ua = mma_x3(ci.t[j][0], ci.t[j][1], *reinterpret_cast<const u32x4_t*>(sm.yop[j][0][lane]),
                                 *reinterpret_cast<const u32x4_t*>(sm.yop[j][1][lane]), ua);
-                }
             }
             {
-                const f32x4_t e4 = *reinterpret_cast<const f32x4_t*>(gt + 2 * kC + 16 * w + 4 * g);
+                const f32x4_t e4 = ci.e4;
                 *reinterpret_cast<u32x2_t*>(sm.uf[s][w >> 1][lane] + 2 * (w & 1)) =
                     u32x2_t{pack_f16x2(ua[0], ua[1]), pack_f16x2(ua[2], ua[3])};
                 const f32x4_t us = ua * e4;
@@ -741,7 +756,7 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
                     kt_[j][k2][1] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
                 }
             }
-            const float gam = gt[3 * kC + kC - 1];
+            const float gam = ci.gam;
             chain_sync(&sm.sync, 8 * c + 8, lane);   // C2(c)
             // (c) S^T[keys of w] = e^{G_C} S^T + K^T (e^{G_C - G} U)
 #pragma unroll
@@ -754,51 +769,44 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
                 for (int k2 = 0; k2 < 2; ++k2) sT[k2] = mma_x3(kt_[j][k2][0], kt_[j][k2][1], uh, ul, sT[k2]);
             }
             publish_state((c + 1) % 3);
+        };
+        ChainIn ia, ib;
+        load_in(ia, 0);
+        int c = 0;
+        for (; c + 1 < nch; c += 2) {
+            step(c, ia, ib);
+            step(c + 1, ib, ia);
         }
+        if (c < nch) step(c, ia, ib);
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) *reinterpret_cast<f32x4_t*>(Sg + 16 * k2) = sT[k2];
         __syncthreads();   // B0(nch): the helpers form the last chunk's output
     } else {
         // ---- helper waves ---------------------------------------------------
         const int hw = wave - 4;   // token tile and operand quarter
-        // this wave's quarter of a chunk's operands: K image blocks 8hw .. +7
-        // of 32 (hi then lo), T blocks 3hw .. +2 of 12, beta V token tile hw,
-        // gates (stored by hw 0); P blocks pb, pb + 1 (token tile hw uses
-        // tblk(hw, 0) = pb and, for hw >= 2, tblk(hw, 1) = pb + 1)
+        // this wave's quarter of a chunk's K image: blocks 8hw .. +7 of 32
+        // (hi then lo); P blocks pb, pb + 1 (token tile hw uses tblk(hw, 0) =
+        // pb and, for hw >= 2, tblk(hw, 1) = pb + 1)
         const int pb = hw < 2 ? hw : 2 * hw - 2;
         struct Stage {
             u32x4_t k[8];
-            u32x4_t t[3];
-            f32x4_t bv;
-            f32x4_t gt;
         } hs;
         struct Out {
             u32x4_t q[4];   // Q blocks (hw, j)
             u32x4_t p[2];   // P blocks pb, pb + 1
+            f32x4_t eg;     // e^G of the tile's tokens
         } ho;
-        f32x4_t eg, eg_next;
         // every helper load is unconditional (a load under a divergent branch
         // makes the compiler wait for all outstanding loads at the join)
         auto load_stage = [&](int cc) {
             const uint16_t* kg = in.kimg + (static_cast<size_t>(cc) * 16 + kh) * kKImg + hw * (8 * kBlk);
 #pragma unroll
             for (int i = 0; i < 8; ++i) hs.k[i] = *reinterpret_cast<const u32x4_t*>(kg + i * kBlk + 8 * lane);
-            const uint16_t* tg = in.top + (static_cast<size_t>(cc) * 32 + h) * kTOp + hw * (3 * kBlk);
-#pragma unroll
-            for (int i = 0; i < 3; ++i) hs.t[i] = *reinterpret_cast<const u32x4_t*>(tg + i * kBlk + 8 * lane);
-            const float* vg = in.bv + (static_cast<size_t>(cc) * 32 + h) * kBV + (cb * 4 + hw) * 256;
-            hs.bv = *reinterpret_cast<const f32x4_t*>(vg + 4 * lane);
-            hs.gt = *reinterpret_cast<const f32x4_t*>(in.gates + (static_cast<size_t>(cc) * 32 + h) * kGates + 4 * lane);
         };
         auto store_stage = [&](int s) {
             uint16_t* kd = sm.kimg[s] + hw * (8 * kBlk);
 #pragma unroll
             for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4_t*>(kd + i * kBlk + 8 * lane) = hs.k[i];
-            uint16_t* td = sm.top[s] + hw * (3 * kBlk);
-#pragma unroll
-            for (int i = 0; i < 3; ++i) *reinterpret_cast<u32x4_t*>(td + i * kBlk + 8 * lane) = hs.t[i];
-            sm.bv[s][hw][lane] = hs.bv;
-            if (hw == 0) *reinterpret_cast<f32x4_t*>(sm.gates[s] + 4 * lane) = hs.gt;
         };
         auto load_out = [&](int cc) {
             const uint16_t* qg = in.qop + (static_cast<size_t>(cc) * 16 + kh) * kQOp + 4 * hw * kBlk;
@@ -807,13 +815,15 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             const uint16_t* pg = in.pop + (static_cast<size_t>(cc) * 32 + h) * kPOp + pb * kBlk;
 #pragma unroll
             for (int i = 0; i < 2; ++i) ho.p[i] = *reinterpret_cast<const u32x4_t*>(pg + i * kBlk + 8 * lane);
+            ho.eg = *reinterpret_cast<const f32x4_t*>(in.gates + (static_cast<size_t>(cc) * 32 + h) * kGates + 3 * kC +
+                                                      16 * hw + 4 * g);
         };
         auto output = [&](int cc) {
             const int par = cc & 1;
             f32x4_t o = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) o = mfma_16x16x32_f16(ho.q[j], sm.sf[cc % 3][j][lane], o);
-            o *= eg;
+            o *= ho.eg;
             o = mfma_16x16x32_f16(ho.p[0], *reinterpret_cast<const u32x4_t*>(sm.uf[par][0][lane]), o);
             if (hw >= 2) o = mfma_16x16x32_f16(ho.p[1], *reinterpret_cast<const u32x4_t*>(sm.uf[par][1][lane]), o);
 #pragma unroll
@@ -828,14 +838,12 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
         load_out(0);
         for (int c = 0; c < nch; ++c) {
             __syncthreads();   // B0(c)
-            eg_next = *reinterpret_cast<const f32x4_t*>(sm.gates[c & 1] + 3 * kC + 16 * hw + 4 * g);
             // chunk c - 1's S^T and U stay published until the chain's (c) and
             // (b) of chunk c + 1
             if (c > 0) {
                 output(c - 1);
                 load_out(c);
             }
-            eg = eg_next;
             if (c + 1 < nch) store_stage((c + 1) & 1);
             if (c + 2 < nch) load_stage(c + 2);
         }
