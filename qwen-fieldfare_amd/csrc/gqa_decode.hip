@@ -17,15 +17,16 @@
 //            token also normalises/rotates k, appends k and v to the cache
 //            and keeps both in LDS for its own use. It then walks 16-position
 //            tiles with the next tile's K and V rows already in flight (two
-//            register stages): S^T = K Q^T with 16 MFMA 16x16x32
-//            (K rows straight from HBM, 16 B per lane; q as bf16 hi + lo,
-//            so the scores see ~16 bits of q, more than the reference's
-//            fp16 q), base-2 online softmax
+//            register stages): S^T = K Q^T with 8 MFMA 16x16x32
+//            (K rows straight from HBM, 16 B per lane; q as bf16 hi + lo
+//            in the two 8-column halves of the MFMA's 16 columns, so the
+//            scores see ~16 bits of q, more than the reference's fp16 q),
+//            base-2 online softmax
 //            per head whose running max is raised only past 2^8 (so O is
 //            rarely rescaled), the V tile copied row-major into LDS and read
 //            back as MFMA B operands with the gfx950 transpose read
-//            (ds_read_b64_tr_b16), O += P V with 32 MFMA 16x16x16 (P as
-//            bf16 hi + lo), and one
+//            (ds_read_b64_tr_b16), O += P V with 16 MFMA 16x16x16 (P as
+//            bf16 hi + lo in the two 8-row halves), and one
 //            (m, d, o[8][256]) partial per chunk (m in base-2 units).
 //   combine  grid (q head, sequence): merges the chunk partials and applies
 //            out = attn * sigmoid(gate).
@@ -68,13 +69,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 // kv head kvh, run by one wave on its own LDS. The wave normalises and
 // rotates the 8 q heads; if the chunk holds the new token it also
 // normalises / rotates k, appends k and v to the cache and keeps both in
-// LDS for its own use. It then walks 16-position tiles: S^T = K Q^T with 16
+// LDS for its own use. It then walks 16-position tiles: S^T = K Q^T with 8
 // MFMA 16x16x32 (K rows straight from HBM, 16 B per lane; q as bf16 hi +
-// lo), base-2 online softmax per head whose running max is raised only past
-// 2^8 (so O is rarely rescaled), the V tile copied row-major into LDS and
-// read back as MFMA B operands with the gfx950 transpose read
-// (ds_read_b64_tr_b16), O += P V with 32 MFMA 16x16x16 (P as bf16 hi + lo),
-// and writes one (m, d, o[8][256]) partial (m in base-2 units). The next
+// lo in columns 0-7 / 8-15), base-2 online softmax per head whose running
+// max is raised only past 2^8 (so O is rarely rescaled), the V tile copied
+// row-major into LDS and read back as MFMA B operands with the gfx950
+// transpose read (ds_read_b64_tr_b16), O += P V with 16 MFMA 16x16x16 (P as
+// bf16 hi + lo in rows 0-7 / 8-15, added at the end), and writes one (m, d, o[8][256]) partial (m in base-2 units). The next
 // tile's loads are in flight while a tile computes (two register stages).
 template <int IN_DT>
 __device__ __forceinline__ void gqa_partial_unit(
@@ -205,10 +206,11 @@ __device__ __forceinline__ void gqa_partial_unit(
     }
     wave_lds_sync();
 
-    // q^T (B of 16x16x32): col = head n (< 8 real), k = dims 32jj + 8kb .. +7,
-    // read from LDS per tile (registers are kept for the two tile stages)
-    const uint16_t* qrow = &L.qs[n & 7][8 * kb];
-    const uint16_t* qrow_lo = &L.ql[n & 7][8 * kb];
+    // q^T (B of 16x16x32): col n = head n & 7, its bf16 hi part for n < 8 and
+    // lo part for n >= 8 (the columns a group of 8 heads leaves free), k =
+    // dims 32jj + 8kb .. +7, read from LDS per tile (registers are kept for
+    // the two tile stages)
+    const uint16_t* qrow = n < 8 ? &L.qs[n][8 * kb] : &L.ql[n - 8][8 * kb];
     uint16_t* vsw = L.vs;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
 
@@ -229,16 +231,16 @@ __device__ __forceinline__ void gqa_partial_unit(
             }
         }
         // S^T = K Q^T, q as hi + lo (K is exact in bf16): the scores carry
-        // ~16 significant bits of q, finer than the reference's fp16 q
-        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f}, s_lo = s;
+        // ~16 significant bits of q, finer than the reference's fp16 q.
+        // Column n scores against head n & 7's hi (n < 8) or lo (n >= 8)
+        // part; lanes n and n ^ 8 (DPP row rotate by 8) add the two, so
+        // both hold head n & 7's scores from here on.
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const u32x4_t qv = n < 8 ? *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj) : u32x4_t{0u, 0u, 0u, 0u};
-            const u32x4_t qvl = n < 8 ? *reinterpret_cast<const u32x4_t*>(qrow_lo + 32 * jj) : u32x4_t{0u, 0u, 0u, 0u};
-            s = mfma_16x16x32_bf16(tl.k[jj], qv, s);
-            s_lo = mfma_16x16x32_bf16(tl.k[jj], qvl, s_lo);
-        }
-        s += s_lo;
+        for (int jj = 0; jj < 8; ++jj)
+            s = mfma_16x16x32_bf16(tl.k[jj], *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj), s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] += dpp_mov<0x128>(s[i]);
         // V tile row-major into LDS (the new token's row from LDS as well)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -278,12 +280,13 @@ __device__ __forceinline__ void gqa_partial_unit(
             pe[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
             d_run += pe[i];
         }
-        // A of O += P V (16x16x16): row = head n, k = positions 4kb .. +3,
-        // P as bf16 hi + lo (V is exact in bf16)
+        // A of O += P V (16x16x16): row n = head n & 7, k = positions 4kb ..
+        // +3, P's bf16 hi part in rows 0-7 and lo part in rows 8-15 (V is
+        // exact in bf16), so rows h and h + 8 of O sum to head h's output
         uint32_t ph0, pl0, ph1, pl1;
         split_bf16x2(pe[0], pe[1], ph0, pl0);
         split_bf16x2(pe[2], pe[3], ph1, pl1);
-        const u32x2_t pa = u32x2_t{ph0, ph1}, pl = u32x2_t{pl0, pl1};
+        const u32x2_t pa = n < 8 ? u32x2_t{ph0, ph1} : u32x2_t{pl0, pl1};
         // B = V^T block straight from the row-major tile with a transpose read:
         // source lane (group kb, s = n) points at row 4kb + n/4, dims
         // 16jd + 4(n%4) .. +3, and receives V[4kb + k][16jd + n], k = 0..3.
@@ -293,7 +296,6 @@ __device__ __forceinline__ void gqa_partial_unit(
         for (int jd = 0; jd < 16; ++jd) {
             const u32x2_t vb = lds_read_tr16(vsrc + 16 * jd);
             oacc[jd] = mfma_16x16x16_bf16(pa, vb, oacc[jd]);
-            oacc[jd] = mfma_16x16x16_bf16(pl, vb, oacc[jd]);
         }
         wave_lds_sync();
     };
@@ -307,7 +309,9 @@ __device__ __forceinline__ void gqa_partial_unit(
         compute(tb, p0 + kDecTile);
     }
     if (p0 < p_end) compute(ta, p0);
-    // ---- partial (m, d, o) of this chunk; oacc[jd][i] = O[head 4kb+i][dim 16jd+n]
+    // ---- partial (m, d, o) of this chunk; oacc[jd][i] = O[row 4kb+i][dim 16jd+n],
+    // rows 0-7 (lanes 0-31) the hi parts and rows 8-15 (lanes 32-63) the lo
+    // parts of heads 0-7
     d_run += __shfl_xor(d_run, 16, 64);
     d_run += __shfl_xor(d_run, 32, 64);
     const size_t pbase = (static_cast<size_t>(seq) * 2 + kvh) * cstride + c;
@@ -315,6 +319,14 @@ __device__ __forceinline__ void gqa_partial_unit(
         pm[pbase * 8 + lane] = m_run;
         pd[pbase * 8 + lane] = d_run;
     }
+#pragma unroll
+    for (int jd = 0; jd < 16; ++jd)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(oacc[jd][i]),
+                                                            __float_as_uint(oacc[jd][i]), false, false);
+            oacc[jd][i] = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+        }
     if (kb < 2) {
         float* orow = po + pbase * 8 * 256;
 #pragma unroll

@@ -86,7 +86,7 @@ def test_deltanet_decode_f32_inputs_and_repeat(hip, B):
         inp["conv_state"], inp["ssm_state"] = ref_c, ref_s
 
 
-@pytest.mark.parametrize("T", [1, 3, 64, 200])
+@pytest.mark.parametrize("T", [1, 3, 64, 130, 192, 200])
 def test_deltanet_prefill_matches_sequential_oracle(hip, T):
     import qff
     print(f"deltanet_prefill T={T}", flush=True)
