@@ -92,21 +92,36 @@ struct Q4Parts {
     int n;
 };
 
-// The residual of element i of part p (0 without one), read early. Both
-// dtypes are loaded unconditionally, each from an in-bounds address (the
-// part's weights stand in for the one not needed), and selected: a branch
-// around a load would make the compiler wait for every load in flight at
-// the join.
-__device__ __forceinline__ float q4_res1(const Q4Parts& parts, int p, size_t i) {
-    const bool has = parts.res[p] != nullptr, bf = parts.ybf16[p] != 0;
-    const uint16_t* r16 = has && bf ? static_cast<const uint16_t*>(parts.res[p]) + i
-                                    : reinterpret_cast<const uint16_t*>(parts.w[p]);
-    const uint32_t* r32 = has && !bf ? static_cast<const uint32_t*>(parts.res[p]) + i : parts.w[p];
-    const uint32_t h = *r16, f = *r32;
-    return has ? __uint_as_float(bf ? h << 16 : f) : 0.0f;
+// The part of workgroup blk with its fields, read at kernel start in two
+// scalar-memory round trips (the block boundaries, then the part's fields);
+// the integer fields are pinned in registers: left to itself the compiler
+// re-reads kernel arguments at a later use, and every such read is another
+// round trip on the critical path of a launch that lasts a few microseconds.
+struct Q4Part1 {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    void* y;
+    const void* res;
+    int rows, ybf16, blk0;
+};
+__device__ __forceinline__ Q4Part1 q4_part_of(const Q4Parts& parts, int blk) {
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < QFF_Q4_MAX_PARTS; ++i) p += blk >= parts.blk0[i];   // unused entries hold INT_MAX
+    Q4Part1 r{parts.w[p], parts.s[p], parts.b[p], parts.y[p], parts.res[p], parts.rows[p], parts.ybf16[p], parts.blk0[p]};
+    // (the pointers stay as read: through an asm operand they would lose
+    // their global address space and every access would become a flat one)
+    asm volatile("" : "+s"(r.rows), "+s"(r.ybf16), "+s"(r.blk0));
+    return r;
 }
-// ... of elements i .. i+3, when ok (i a multiple of 4, so the loads are
-// aligned): one 8-B (bf16) and one 16-B (fp32) load
+
+// The residual of elements i .. i+3 of part p (0 without one), read early,
+// when ok (i a multiple of 4, so the loads are aligned): one 8-B (bf16) and
+// one 16-B (fp32) load. Both dtypes are loaded unconditionally, each from an
+// in-bounds address (the part's weights stand in for the one not needed),
+// and selected: a branch around a load would make the compiler wait for
+// every load in flight at the join.
 __device__ __forceinline__ f32x4_t q4_res4(const Q4Parts& parts, int p, size_t i, bool ok) {
     const bool has = ok && parts.res[p] != nullptr, bf = parts.ybf16[p] != 0;
     const u32x2_t* r16 = has && bf ? reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(parts.res[p]) + i)
@@ -139,21 +154,29 @@ __device__ __forceinline__ void q4_store(const Q4Parts& parts, int p, size_t i, 
 // f32 or bf16 without a branch on the dtype (a branch around loads makes the
 // compiler wait for every load in flight at the join): per 8 weights two
 // 16-B loads, the second a repeat of the first for bf16, and selects.
-template <int N>
-__device__ __forceinline__ void q4_norm_weights(const Q4Norm& nrm, int c, float (&wn)[N]) {
+// The two halves: the raw 16-B pieces of 8 weights at column c, and their
+// values (so callers can issue other loads before any of these is used).
+struct Q4NormRaw {
+    u32x4_t lo, hi;
+};
+__device__ __forceinline__ Q4NormRaw q4_norm_weights_raw(const Q4Norm& nrm, int c) {
+    const bool bf = nrm.wbf16;
+    const char* base = static_cast<const char*>(nrm.w) + static_cast<size_t>(c) * (bf ? 2 : 4);
+    return Q4NormRaw{*reinterpret_cast<const u32x4_t*>(base), *reinterpret_cast<const u32x4_t*>(base + (bf ? 0 : 16))};
+}
+__device__ __forceinline__ void q4_norm_weights_finish(const Q4Norm& nrm, const Q4NormRaw& r, float* wn) {
     const bool bf = nrm.wbf16;
 #pragma unroll
-    for (int q = 0; q < N / 8; ++q) {
-        const char* base = static_cast<const char*>(nrm.w) + static_cast<size_t>(c + 8 * q) * (bf ? 2 : 4);
-        const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(base);
-        const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(base + (bf ? 0 : 16));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t f = e < 4 ? lo[e] : hi[e - 4];
-            const uint32_t h = (e & 1) ? (lo[e >> 1] & 0xffff0000u) : (lo[e >> 1] << 16);
-            wn[8 * q + e] = __uint_as_float(bf ? h : f);
-        }
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t f = e < 4 ? r.lo[e] : r.hi[e - 4];
+        const uint32_t h = (e & 1) ? (r.lo[e >> 1] & 0xffff0000u) : (r.lo[e >> 1] << 16);
+        wn[e] = __uint_as_float(bf ? h : f);
     }
+}
+template <int N>
+__device__ __forceinline__ void q4_norm_weights(const Q4Norm& nrm, int c, float (&wn)[N]) {
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) q4_norm_weights_finish(nrm, q4_norm_weights_raw(nrm, c + 8 * q), wn + 8 * q);
 }
 
 // Groups per wave: 2 up to 2048 columns, 4 up to 4096 (at most 16 waves).
@@ -500,44 +523,40 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
                                                                     int cols, Q4Norm nrm) {
     constexpr bool HILO = X_DT == 0 || NORM;   // x is not exactly bf16: hi + lo
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    int p = 0;
-#pragma unroll
-    for (int i = 1; i < QFF_Q4_MAX_PARTS; ++i) p += (i < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[i]);
-    const uint32_t* __restrict__ w = parts.w[p];
-    const uint16_t* __restrict__ scales = parts.s[p];
-    const uint16_t* __restrict__ biases = parts.b[p];
-    const int rows = parts.rows[p];
-    const int R0 = ((blockIdx.x - parts.blk0[p]) * kQ4VecWaves + wave) * kQ4VecRows;
+    const Q4Part1 P = q4_part_of(parts, static_cast<int>(blockIdx.x));
+    const uint32_t* __restrict__ w = P.w;
+    const uint16_t* __restrict__ scales = P.s;
+    const uint16_t* __restrict__ biases = P.b;
+    const int rows = P.rows;
+    const int R0 = ((static_cast<int>(blockIdx.x) - P.blk0) * kQ4VecWaves + wave) * kQ4VecRows;
     const int G = cols / 64, W8 = cols / 8, npc = cols / 32;   // 32-column pieces per row
 
-    // x (and the norm weights) first: the workgroup's preparation below waits
-    // for these loads only, while the weight rows are still arriving.
-    // Slice i = columns 8i .. 8i+7 of x.
+    // Every load of the workgroup is issued before any loaded value is used:
+    // x (and the norm weights) first, the residual, then the weight rows, so
+    // the preparation of x below waits for its own loads only while the
+    // weight rows are still arriving. Slice i = columns 8i .. 8i+7 of x.
     constexpr int NS = KW * 256 / (64 * kQ4VecWaves);   // slices per thread
-    float v[NS][8], wn[NS][8];
+    u32x4_t xr[NS][2];
+    Q4NormRaw nr[NS];
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         const int ic = min(t + 64 * kQ4VecWaves * k, W8 - 1);
         if (X_DT == 1) {
-            const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + 8 * ic);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[k][2 * e] = __uint_as_float(u[e] << 16);
-                v[k][2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
-            }
+            xr[k][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + 8 * ic);
         } else {
-            const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 8 * ic);
-            const float4 f0 = f[0], f1 = f[1];
-            v[k][0] = f0.x; v[k][1] = f0.y; v[k][2] = f0.z; v[k][3] = f0.w;
-            v[k][4] = f1.x; v[k][5] = f1.y; v[k][6] = f1.z; v[k][7] = f1.w;
+            const u32x4_t* f = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + 8 * ic);
+            xr[k][0] = f[0];
+            xr[k][1] = f[1];
         }
-        if (NORM) q4_norm_weights<8>(nrm, 8 * ic, wn[k]);
+        if (NORM) nr[k] = q4_norm_weights_raw(nrm, 8 * ic);
     }
-
-    // the residual of the row this lane stores at the end (lanes 16 j store
-    // row R0 + j), requested now
-    const float resv = q4_res1(parts, p, static_cast<size_t>(min(R0 + (lane >> 4), rows - 1)));
-    // weights and group constants of this wave's rows, all in flight
+    // the residual of the row this lane stores at the end (lanes
+    // 64 j / kQ4VecRows store row R0 + j)
+    const size_t ri = static_cast<size_t>(min(R0 + lane / (64 / kQ4VecRows), rows - 1));
+    const bool has_res = P.res != nullptr, ybf = P.ybf16 != 0;
+    const uint32_t rh = *(has_res && ybf ? static_cast<const uint16_t*>(P.res) + ri : reinterpret_cast<const uint16_t*>(w));
+    const uint32_t rf = *(has_res && !ybf ? static_cast<const uint32_t*>(P.res) + ri : w);
+    // weights and group constants of this wave's rows
     u32x4_t wq[kQ4VecRows][KW];
     float sv[kQ4VecRows][KW], bv[kQ4VecRows][KW];
 #pragma unroll
@@ -550,6 +569,25 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
             sv[r][k] = elem<SB_DT>::load(scales, row * G + pc / 2);
             bv[r][k] = elem<SB_DT>::load(biases, row * G + pc / 2);
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float v[NS][8], wn[NS][8];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        if (X_DT == 1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[k][2 * e] = __uint_as_float(xr[k][0][e] << 16);
+                v[k][2 * e + 1] = __uint_as_float(xr[k][0][e] & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[k][e] = __uint_as_float(xr[k][0][e]);
+                v[k][4 + e] = __uint_as_float(xr[k][1][e]);
+            }
+        }
+        if (NORM) q4_norm_weights_finish(nrm, nr[k], wn[k]);
     }
 
     // x once per workgroup: slice i -> xl[i] as the four bf16 pairs
@@ -590,8 +628,7 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
 #pragma unroll
             for (int e = 0; e < 4; ++e) sum += __uint_as_float(xb[e] << 16) + __uint_as_float(xb[e] & 0xffff0000u);
         }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
+        sum = group_sum<4>(sum);
         if (live) {
             xl[i] = xb;
             if (HILO) xll[i] = xlb;
@@ -599,8 +636,7 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
         }
     }
     if (NORM) {
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = group_sum<64>(ss);
         if (lane == 0) ssl[wave] = ss;
     }
     __syncthreads();
@@ -639,29 +675,44 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
             part[r] = fmaf(sk, dq, fmaf(fmaf(-128.0f, sk, bk), xs, part[r]));
         }
     }
-    // reduce-scatter: lane ^ 32 and ^ 16 halve the four rows, then ^ 8 .. ^ 1
+    // reduce-scatter over the wave: with four rows the 32-lane halves swap
+    // (permlane32) and lane ^ 16 (swizzle) halve them, with two rows the
+    // swap alone; then the 16-lane groups sum on DPP moves. Lane
+    // 64 j / kQ4VecRows ends with row j.
     const bool b5 = lane & 32, b4 = lane & 16;
-    float q2[2];
+    auto other_half = [&](float v) {
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(b5 ? h[0] : h[1]);
+    };
+    float q1;
+    if (kQ4VecRows == 4) {
+        float q2[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const float keep = b5 ? part[2 + j] : part[j], give = b5 ? part[j] : part[2 + j];
-        q2[j] = keep + __shfl_xor(give, 32, 64);
+        for (int j = 0; j < 2; ++j) q2[j] = (b5 ? part[2 + j] : part[j]) + other_half(b5 ? part[j] : part[2 + j]);
+        q1 = (b4 ? q2[1] : q2[0]) + swizzle_xor16(b4 ? q2[0] : q2[1]);
+    } else if (kQ4VecRows == 2) {
+        q1 = (b5 ? part[kQ4VecRows - 1] : part[0]) + other_half(b5 ? part[0] : part[kQ4VecRows - 1]);
+        q1 += swizzle_xor16(q1);
+    } else {
+        q1 = part[0] + other_half(part[0]);
+        q1 += swizzle_xor16(q1);
     }
-    float q1 = (b4 ? q2[1] : q2[0]) + __shfl_xor(b4 ? q2[0] : q2[1], 16, 64);
-    q1 += __shfl_xor(q1, 8, 64);
-    q1 += __shfl_xor(q1, 4, 64);
-    q1 += __shfl_xor(q1, 2, 64);
-    q1 += __shfl_xor(q1, 1, 64);
+    q1 = group_sum<16>(q1);
     if (NORM) {
         float sq = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kQ4VecWaves; ++ww) sq += ssl[ww];
         q1 *= rsqrtf(sq / static_cast<float>(cols) + nrm.eps);
     }
-    // lane 16 * (2 b5 + b4) holds row 2 b5 + b4
-    if ((lane & 15) == 0) {
-        const int r = R0 + (lane >> 4);
-        if (r < rows) q4_put(parts, p, r, q1 + resv);
+    if ((lane & (64 / kQ4VecRows - 1)) == 0) {
+        const int r = R0 + lane / (64 / kQ4VecRows);
+        uint32_t mask = has_res ? ~0u : 0u;   // opaque: no branch around the residual loads
+        asm volatile("" : "+v"(mask));
+        const float y = q1 + __uint_as_float((ybf ? rh << 16 : rf) & mask);
+        if (r < rows) {
+            if (ybf) elem<1>::store(P.y, r, y);
+            else elem<0>::store(P.y, r, y);
+        }
     }
 }
 
@@ -1031,6 +1082,7 @@ static Q4Parts q4_pack_parts(const qff_q4_part* parts, int nparts, int rpb, int&
         blocks += (parts[i].rows + rpb - 1) / rpb;
     }
     P.blk0[nparts] = blocks;
+    for (int i = nparts + 1; i <= QFF_Q4_MAX_PARTS; ++i) P.blk0[i] = INT_MAX;   // past the last part
     P.n = nparts;
     return P;
 }
