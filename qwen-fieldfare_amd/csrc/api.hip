@@ -38,6 +38,7 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_o = take(S * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
     L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * (64 + 1) * sizeof(float));   // 64 group sums + inverse RMS
+    L.q4_sk_part = take(static_cast<size_t>(kQ4SkSlots) * 16 * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(uint16_t));   // pre-norm DeltaNet prefill output, fp16
     L.sched = take(2 * kSchedSlots * sizeof(unsigned));
@@ -161,6 +162,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_qb = u16(L.gqa_qb);
     c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
+    c->q4_sk_part = reinterpret_cast<float*>(base + L.q4_sk_part);
     c->pf_o = u16(L.pf_o);
     c->sched = reinterpret_cast<unsigned*>(base + L.sched);
     c->num_cu = prop.multiProcessorCount;

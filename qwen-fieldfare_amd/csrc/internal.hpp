@@ -42,6 +42,9 @@ struct qff_ctx {
     // (row G after the groups: the inverse RMS of a normed product).
     float* q4_xs = nullptr;
     int q4_xs_tokens = 0;
+    // Decode-batch Q4 products split over 512-column slices: per (row tile,
+    // slice) the partial [16 tokens][64 rows], kQ4SkSlots of them.
+    float* q4_sk_part = nullptr;
     // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
     // chunk intermediates.
     uint16_t* pf_o = nullptr;
@@ -67,11 +70,12 @@ constexpr int kGqaSeqChunks = 128;     // partial slots per (sequence, kv head) 
 // smaller batch spreads them over more chunks per sequence.
 inline int gqa_slots(const qff_ctx_cfg& cfg) { return 2 * (cfg.max_batch > 4 ? cfg.max_batch : 4) * kGqaSeqChunks; }
 constexpr int kSchedSlots = 8;         // work-queue counter pairs in the context
+constexpr int kQ4SkSlots = 4096;       // (row tile, slice) partials of the split decode-batch Q4 product
 constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
+    size_t gqa_qb, q4_xs, q4_sk_part, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

@@ -93,10 +93,12 @@ struct Q4Parts {
 };
 
 // The part of workgroup blk with its fields, read at kernel start in two
-// scalar-memory round trips (the block boundaries, then the part's fields);
-// the integer fields are pinned in registers: left to itself the compiler
-// re-reads kernel arguments at a later use, and every such read is another
-// round trip on the critical path of a launch that lasts a few microseconds.
+// scalar-memory round trips (the block boundaries, then the part's fields;
+// selecting among all parts' fields read at once needs ~100 SGPRs and the
+// compiler splits it into two batches anyway); the integer fields are
+// pinned in registers: left to itself the compiler re-reads kernel
+// arguments at a later use, and every such read is another round trip on
+// the critical path of a launch that lasts a few microseconds.
 struct Q4Part1 {
     const uint32_t* w;
     const uint16_t* s;
@@ -481,6 +483,194 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
                     else q4_store(parts, p, i, v[j]);
                 }
             }
+        }
+    }
+}
+
+// ---- decode batches of 2-16 tokens, 4096 columns: split over 512-column slices
+//
+// The out-projection shape (2048 rows x 4096 columns, no norm) has too few
+// rows for the decode-batch kernel above to amortise x: 128 workgroups of 16
+// rows each read all 256 KB of fp32 x. Here one workgroup takes (64 rows,
+// one 512-column slice): four waves of 16 rows, 32 KB of x, and the grid is
+// tiles x 8 slices wide. The workgroup stages its slice of x once in LDS as
+// bf16 operands (lane l of wave w takes word l of the slice for tokens w,
+// w + 4, ..: hi, + lo when x is fp32, in the nibble conversion's pair order),
+// the per-(group, token) sums of the staged values and the rows' (s, b - 128
+// s). The weights go straight to registers: lane (row n, kb) loads the 16 B
+// at words 4 kb .. 4 kb + 3 of each 128-column span (one access per row and
+// 4 lanes), and one permlane32 swap of words 2, 3 between lanes kb and kb ^ 2
+// leaves every lane two words of each of the span's two groups: with group
+// parity h, lane kb holds words base(kb ^ 2h) + {0, 1} of the group,
+// base(k) = 4 (k & 1) + 2 (k >> 1), and the B operand reads x for the same
+// words, so each 16x16x32 MFMA stays inside one group and the group's scale
+// applies to its result: y = sum_g s_g P_g + (b_g - 128 s_g) X_g as in the
+// other paths. Each workgroup writes its (64 rows x 16 tokens) partial to the
+// workspace; q4_sk_reduce_kernel, the next launch, adds each tile's partials
+// in slice order and the residual and stores the rows. (Handing the partials
+// to the tile's last workgroup inside one launch needs an agent-scope
+// release per workgroup, which writes back the L2: measured 9x slower.
+// Measured against the kernel above: 8.6-9.2 vs 10.1-12.3 us at 2048 x 4096,
+// batch 4-16; the normed 2048-column in-projections ran slower split, 772
+// small workgroups, and stay there.)
+constexpr int kQ4SkCols = 512;     // columns per slice (8 groups)
+constexpr int kQ4SkSplit = 8;      // slices per row (cols = 4096)
+constexpr int kQ4SkRows = 64;      // rows per workgroup (four waves of 16)
+constexpr int kQ4SkXStride = 17;   // LDS entries (16 B) per staged word: 16 tokens + 1 pad
+
+__device__ __forceinline__ int q4_sk_word(int kb, int h, int s) {
+    const int k = kb ^ (2 * h);
+    return 4 * (k & 1) + 2 * (k >> 1) + s;
+}
+
+template <int SB_DT, int X_DT>
+__global__ __launch_bounds__(256) void q4_gemv_sk_kernel(Q4Parts parts, const void* __restrict__ x, int batch,
+                                                         float* __restrict__ wpart) {
+    constexpr bool HILO = X_DT == 0;   // fp32 x: hi + lo operands
+    constexpr int cols = kQ4SkCols * kQ4SkSplit, G = cols / 64, W8 = cols / 8;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = lane & 15, kb = lane >> 4;
+    const int tile = static_cast<int>(blockIdx.x), split = static_cast<int>(blockIdx.y);
+    const Q4Part1 P = q4_part_of(parts, tile);
+    const int rows = P.rows;
+    const int R0 = (tile - P.blk0) * kQ4SkRows;
+    const int k0 = split * kQ4SkCols, gs = k0 / 64;
+
+    __shared__ u32x4_t xh[64 * kQ4SkXStride];
+    __shared__ u32x4_t xlo[HILO ? 64 * kQ4SkXStride : 1];
+    __shared__ float xsum[8][16];
+    __shared__ float2 sbl[kQ4SkRows * 8];
+
+    // ---- requests: this wave's weight rows, the slice's x, the workgroup's
+    // scales and biases; nothing is used before all are issued
+    const size_t wrow = static_cast<size_t>(min(R0 + 16 * wave + n, rows - 1));
+    u32x4_t wq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        wq[j] = *reinterpret_cast<const u32x4_t*>(P.w + wrow * W8 + k0 / 8 + 16 * j + 4 * kb);
+    // x: token 4 i + wave, columns k0 + 8 lane .. +7
+    u32x4_t xr[4][HILO ? 2 : 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t xo = static_cast<size_t>(min(4 * i + wave, batch - 1)) * cols + k0 + 8 * lane;
+        if (HILO) {
+            xr[i][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + xo);
+            xr[i][HILO ? 1 : 0] = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + xo + 4);
+        } else {
+            xr[i][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo);
+        }
+    }
+    float sreg[2], breg[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int e = t + 256 * j, r = e >> 3, g = e & 7;
+        const size_t gi = static_cast<size_t>(min(R0 + r, rows - 1)) * G + gs + g;
+        sreg[j] = elem<SB_DT>::load(P.s, gi);
+        breg[j] = elem<SB_DT>::load(P.b, gi);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x operands and group sums into LDS
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * i + wave;
+        u32x4_t hv, lv;
+        float sum = 0.0f;
+        if (HILO) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t hh, ll;
+                split_bf16x2(__uint_as_float(xr[i][0][e]), __uint_as_float(xr[i][HILO ? 1 : 0][e]), hh, ll);
+                hv[e] = hh;
+                lv[e] = ll;
+                sum += (__uint_as_float(hh << 16) + __uint_as_float(ll << 16)) +
+                       (__uint_as_float(hh & 0xffff0000u) + __uint_as_float(ll & 0xffff0000u));
+            }
+        } else {
+            hv = interleave8(xr[i][0]);   // exact bf16 x, reordered to the pair order
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum += __uint_as_float(hv[e] << 16) + __uint_as_float(hv[e] & 0xffff0000u);
+        }
+        xh[lane * kQ4SkXStride + m] = hv;
+        if (HILO) xlo[lane * kQ4SkXStride + m] = lv;
+        sum = group_sum<8>(sum);   // the 8 words of group lane / 8
+        if ((lane & 7) == 0) xsum[lane >> 3][m] = sum;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sbl[t + 256 * j] = make_float2(sreg[j], breg[j] - 128.0f * sreg[j]);
+    __syncthreads();
+
+    // ---- products: per 128-column span j, words 2, 3 swap with lane ^ 32
+    const bool b5 = lane & 32;
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto s2 = __builtin_amdgcn_permlane32_swap(wq[j][2], wq[j][2], false, false);
+        const auto s3 = __builtin_amdgcn_permlane32_swap(wq[j][3], wq[j][3], false, false);
+        const uint32_t p2 = b5 ? s2[0] : s2[1], p3 = b5 ? s3[0] : s3[1];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int g = 2 * j + h;
+            const bool own = (kb < 2) == (h == 0);
+            const uint32_t w0 = own ? wq[j][0] : p2, w1 = own ? wq[j][1] : p3;
+            const int e0 = (8 * g + q4_sk_word(kb, h, 0)) * kQ4SkXStride + n;
+            const int e1 = (8 * g + q4_sk_word(kb, h, 1)) * kQ4SkXStride + n;
+            const u32x4_t a0 = q4_to_bf16_interleaved(w0), a1 = q4_to_bf16_interleaved(w1);
+            f32x4_t pr = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            pr = mfma_16x16x32_bf16(a0, xh[e0], pr);
+            pr = mfma_16x16x32_bf16(a1, xh[e1], pr);
+            if (HILO) {
+                pr = mfma_16x16x32_bf16(a0, xlo[e0], pr);
+                pr = mfma_16x16x32_bf16(a1, xlo[e1], pr);
+            }
+            const float xs = xsum[g][n];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 sb = sbl[(16 * wave + 4 * kb + i) * 8 + g];
+                acc[i] = fmaf(sb.x, pr[i], fmaf(sb.y, xs, acc[i]));
+            }
+        }
+    }
+    // this slice's partial: rows 16 wave + 4 kb .. +3 of token n
+    const size_t slot = static_cast<size_t>(tile) * kQ4SkSplit + split;
+    *reinterpret_cast<f32x4_t*>(wpart + slot * 16 * kQ4SkRows + n * kQ4SkRows + 16 * wave + 4 * kb) = acc;
+}
+
+// One workgroup per row tile: thread t -> token t % 16, rows 4 (t / 16) .. +3
+// of the tile, the slices' partials and the residuals requested at once, the
+// partials added in slice order.
+__global__ __launch_bounds__(256) void q4_sk_reduce_kernel(Q4Parts parts, int batch, const float* __restrict__ wpart) {
+    const int t = threadIdx.x, tile = static_cast<int>(blockIdx.x);
+    const Q4Part1 P = q4_part_of(parts, tile);
+    const int rows = P.rows, R0 = (tile - P.blk0) * kQ4SkRows;
+    const int m = t & 15, r4 = 4 * (t >> 4);
+    f32x4_t pv[kQ4SkSplit];
+#pragma unroll
+    for (int sp = 0; sp < kQ4SkSplit; ++sp)
+        pv[sp] = *reinterpret_cast<const f32x4_t*>(wpart + (static_cast<size_t>(tile) * kQ4SkSplit + sp) * 16 *
+                                                               kQ4SkRows + m * kQ4SkRows + r4);
+    const size_t o0 = static_cast<size_t>(min(m, batch - 1)) * rows;
+    const bool has_res = P.res != nullptr, ybf = P.ybf16 != 0;
+    uint32_t rh[4], rf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t oi = o0 + min(R0 + r4 + i, rows - 1);
+        rh[i] = *(has_res && ybf ? static_cast<const uint16_t*>(P.res) + oi : reinterpret_cast<const uint16_t*>(P.w));
+        rf[i] = *(has_res && !ybf ? static_cast<const uint32_t*>(P.res) + oi : P.w);
+    }
+    f32x4_t y = pv[0];
+#pragma unroll
+    for (int sp = 1; sp < kQ4SkSplit; ++sp) y += pv[sp];
+    if (m >= batch) return;
+    uint32_t mask = has_res ? ~0u : 0u;   // opaque: no branch around the residual loads
+    asm volatile("" : "+v"(mask));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = R0 + r4 + i;
+        if (r < rows) {
+            const float v = y[i] + __uint_as_float((ybf ? rh[i] << 16 : rf[i]) & mask);
+            if (ybf) elem<1>::store(P.y, o0 + r, v);
+            else elem<0>::store(P.y, o0 + r, v);
         }
     }
 }
@@ -1149,6 +1339,23 @@ static hipError_t q4_gemv_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
 #undef QFF_Q4S_X
 #undef QFF_Q4S
         return hipGetLastError();
+    }
+    if (!NORM && batch <= 16 && cols == kQ4SkCols * kQ4SkSplit) {
+        // 2-16 tokens at 4096 columns: the split-slice kernel and its
+        // reduction launch, when the tiles fit the workspace's partials
+        const Q4Parts P = q4_pack_parts(parts, nparts, kQ4SkRows, blocks);
+        if (static_cast<size_t>(blocks) * kQ4SkSplit * 16 * kQ4SkRows <= static_cast<size_t>(kQ4SkSlots) * 1024) {
+            ProfScope prof(ctx, stream, "q4_matmul");
+            const dim3 grid(blocks, kQ4SkSplit);
+#define QFF_Q4K(S, X) q4_gemv_sk_kernel<S, X><<<grid, 256, 0, stream>>>(P, x, batch, ctx->q4_sk_part)
+#define QFF_Q4K_X(S) \
+    if (x_dtype == QFF_BF16) { QFF_Q4K(S, 1); } else { QFF_Q4K(S, 0); }
+            if (sb_dtype == QFF_BF16) { QFF_Q4K_X(1); } else { QFF_Q4K_X(2); }
+#undef QFF_Q4K_X
+#undef QFF_Q4K
+            q4_sk_reduce_kernel<<<blocks, 256, 0, stream>>>(P, batch, ctx->q4_sk_part);
+            return hipGetLastError();
+        }
     }
     if (NORM && batch > 16) {
         // the normed product keeps one 16-token tile per launch (two tiles

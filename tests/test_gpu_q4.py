@@ -60,6 +60,8 @@ def _rel(a, b):
                                              # many-token GEMM path (batch >= 64), ragged tiles included
                                              (512, 2048, 64), (100, 2048, 300), (8192, 2048, 256),
                                              (2048, 4096, 130), (512, 2048, 8192),
+                                             # 4096 columns, 2-16 tokens: the split-slice kernel
+                                             (2048, 4096, 16), (100, 4096, 3), (2048, 4096, 2),
                                              # column counts that are not a multiple of 512
                                              (300, 576, 5), (200, 3136, 17), (64, 1088, 2),
                                              (8192, 1088, 4), (40, 192, 1), (40, 3136, 1)])
@@ -248,6 +250,35 @@ def test_q4_matmul_parts_residual(hip, batch):
     ref = to_np(res_bf).astype(np.float64) + O.bf16_to_f32(xb).astype(np.float64) @ \
         O.q4_dequant(w, s, b, O.BF16).astype(np.float64).T
     assert _rel(to_np(out_bf), ref) <= 4e-3
+
+
+@pytest.mark.parametrize("batch", [2, 9, 16])
+def test_q4_matmul_parts_4096_cols_f32_x_residual(hip, batch):
+    """The out-projection shape (4096 columns, 2-16 tokens, fp32 x, a residual
+    added in place) through the split-slice kernel and its reduction launch:
+    two parts with a ragged row tile, fp32 and bf16 outputs, against fp64
+    products of the fp32 x; called twice so the second call reuses the
+    workspace the first one filled."""
+    import qff
+    print(f"q4_matmul_parts 4096 cols batch={batch}", flush=True)
+    cols = 4096
+    shapes = [(2048, torch.float32), (100, torch.bfloat16)]
+    ws = [synth.q4_weight(r, cols, seed=r + 11 * batch) for r, _ in shapes]
+    parts = [_w_gpu(w, s, b, "f16") for w, s, b in ws]
+    rng = np.random.default_rng(40 + batch)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    res0 = (rng.standard_normal((batch, 2048)) * 30).astype(np.float32)
+    ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=64)
+    for _ in range(2):
+        y0 = f32_tensor(res0)
+        y1 = torch.empty(batch, 100, dtype=torch.bfloat16, device=DEV)
+        outs = qff.q4_matmul_parts(ctx, parts, f32_tensor(x), outs=[y0, y1], residuals=[y0, None])
+        torch.cuda.synchronize()
+        for i, ((w, s, b), (_, dt)) in enumerate(zip(ws, shapes)):
+            ref = x.astype(np.float64) @ O.q4_dequant(w, s, b, O.F16).astype(np.float64).T
+            if i == 0:
+                ref = ref + res0.astype(np.float64)
+            assert _rel(to_np(outs[i]), ref) <= (1e-5 if dt == torch.float32 else 4e-3)
 
 
 def test_q4_norm_matmul_parts_rejects_bad_calls(hip):
