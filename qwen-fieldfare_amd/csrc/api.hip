@@ -23,7 +23,7 @@ static qff_ctx_cfg resolve(const qff_ctx_cfg* cfg) {
     return c;
 }
 
-// Tokens per slice of a many-token Q4 product (group sums in workspace).
+// Tokens per slice of a many-token Q4 product (fp16 activations in workspace).
 int q4_xs_tokens(const qff_ctx_cfg& cfg) { return std::max(std::max(cfg.max_batch, cfg.max_prefill_tokens), 1024); }
 
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
@@ -37,7 +37,8 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_d = take(S * 8 * sizeof(float));
     L.gqa_o = take(S * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
-    L.q4_xs = take(static_cast<size_t>(q4_xs_tokens(cfg)) * (64 + 1) * sizeof(float));   // 64 group sums + inverse RMS
+    L.q4_x16 = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 4096 * sizeof(uint16_t));
+    L.q4_fm = take(static_cast<size_t>(q4_xs_tokens(cfg)) * sizeof(float));
     L.q4_sk_part = take(static_cast<size_t>(kQ4SkSlots) * 16 * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
     L.pf_o = take(TC * 4096 * sizeof(uint16_t));   // pre-norm DeltaNet prefill output, fp16
@@ -160,7 +161,8 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->gqa_o = reinterpret_cast<float*>(base + L.gqa_o);
     auto u16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
     c->gqa_qb = u16(L.gqa_qb);
-    c->q4_xs = reinterpret_cast<float*>(base + L.q4_xs);
+    c->q4_x16 = reinterpret_cast<uint16_t*>(base + L.q4_x16);
+    c->q4_fm = reinterpret_cast<float*>(base + L.q4_fm);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
     c->q4_sk_part = reinterpret_cast<float*>(base + L.q4_sk_part);
     c->pf_o = u16(L.pf_o);

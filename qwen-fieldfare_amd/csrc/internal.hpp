@@ -38,9 +38,10 @@ struct qff_ctx {
     float* gqa_o = nullptr;       // [gqa_slots(cfg) * 8 * 256]
     // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
     uint16_t* gqa_qb = nullptr;
-    // Many-token Q4 products: per-token group sums [64 + 1][q4_xs_tokens] fp32
-    // (row G after the groups: the inverse RMS of a normed product).
-    float* q4_xs = nullptr;
+    // Many-token Q4 products, per slice of q4_xs_tokens tokens: the fp16
+    // activations x16 [q4_xs_tokens][<= 4096] and each token's output factor.
+    uint16_t* q4_x16 = nullptr;
+    float* q4_fm = nullptr;
     int q4_xs_tokens = 0;
     // Decode-batch Q4 products split over 512-column slices: per (row tile,
     // slice) the partial [16 tokens][64 rows], kQ4SkSlots of them.
@@ -75,7 +76,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, q4_xs, q4_sk_part, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
+    size_t gqa_qb, q4_x16, q4_fm, q4_sk_part, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

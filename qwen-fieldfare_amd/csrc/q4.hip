@@ -908,94 +908,125 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
 
 // ---- many-token GEMM (prefill projections) -----------------------------------
 //
-// y[m, r] for batch >= kQ4GemmMinBatch, as
-//   y = sum_g s_g P_g + sum_g b_g X_g,
-//   P_g[r, m] = sum_{c in g} (128 + q[r, c]) x[m, c] - 128 X_g[m],
-//   X_g[m] = sum_{c in g} x[m, c]
-// with x rounded to bf16 (exactly the operands the matrix cores see).
-// q4_xsum_kernel forms X_g first (group-major). q4_gemm_kernel: one workgroup
-// per 128 rows x 128 tokens, four waves of 64 x 64 (4 x 4 MFMA tiles, C rows =
-// weight rows so each lane's four outputs are adjacent in y). Per 64-column
-// group the workgroup stages the group's weight words, converted once, the
-// bf16 activations and -128 X_g in LDS while the next group's loads are in
-// flight; the MFMAs start from -128 X_g, so P_g is the small sum q x and the
-// large 128 X_g cancels inside the fp32 accumulator, and s_g P_g is added on
-// the vector units. The bias sums are one small product at the end, on
-// bf16x3 MFMAs over the groups.
+// y[m, r] = sum_c W[r, c] x[m, c] for batch >= kQ4GemmMinBatch, on fp16 matrix
+// cores with fp32 accumulation:
+//   W16[r, c] = fp16(2^8 (s q + b))     one fused fp16 FMA per element,
+//                                      rounded once from the exact value
+//   x16[m, c] = fp16(x'[m, c] 2^-e_m)  x' = x (or x w_norm), e_m the token's
+//                                      binary exponent that puts max |x'| in
+//                                      [2^13, 2^14)
+//   y[m, r]   = f_m sum_c W16 x16,     f_m = 2^(e_m - 8) (times the token's
+//                                      inverse RMS with the norm)
+// The power-of-two shifts are exact and keep both operands inside fp16's
+// normal range: x' of any fp32 magnitude, W of magnitude 2^-22 .. 255. Both
+// operands carry 11 significant bits (the bf16 activations of the factored
+// form carried 8), so the product is the fp32 dot product to a few 2^-12
+// relative; the bias is part of every W16 element, so no group sums are
+// needed and the accumulators stay in the matrix cores for the whole K loop.
+//
+// q4_x16_kernel forms x16 and f_m (one wave per token). q4_gemm_kernel: one
+// workgroup per 256 rows x 128 tokens, four waves of 64 rows x 128 tokens
+// (4 x 8 MFMA tiles, C rows = weight rows so each lane's four outputs are
+// adjacent in y). A wave loads its own rows' nibbles straight into registers
+// (8 B per lane and row tile per group: it alone uses them) and converts them
+// there; the token tile's x16 group goes through LDS, double-buffered, one
+// barrier per group, loaded straight from global memory into LDS. The packed fp16 (256 s, 256 b) of the tile's rows sit in
+// LDS for the whole K loop.
 //
 // Within each 8-column word the matrix-core k order is (c0, c4, c1, c5, c2,
-// c6, c3, c7): dword j of the converted word is then
-// ((w >> 4j) & 0x000F000F) | 0x43004300 (two instructions), and the
-// activations are staged in the same order.
-constexpr int kQ4LD = 72;   // bf16 row stride of the [128][64] LDS tiles
+// c6, c3, c7): dword j of the converted word is then the fp16 pair
+// ((w >> 4j) & 0x000F000F) | 0x64006400 = (1024 + q_j, 1024 + q_j+4), exact,
+// minus 1024 (exact), then the FMA; x16 is stored in the same order. A lane
+// with k-block kb of a 32-wide MFMA step ks takes word 2 kb + ks of the group,
+// so its two words of a group are one 8-byte load.
+constexpr int kQ4GemmRows = 256;   // weight rows per workgroup
+constexpr int kQ4GemmToks = 128;   // tokens per workgroup
 
-// X_g[m] = sum of the bf16-rounded x[m, 64g .. 64g+63]: one wave per token;
-// lane l sums half-groups l, l + 64 (32 columns each), pairs of lanes combine.
-// With NORM the summed values are bf16(x w_norm) and row G of xs takes the
-// token's inverse RMS, rsqrt(mean(x^2) + eps), from the same pass.
+// x16 and f_m of one token per wave: lane l holds 8-column blocks l, l + 64, ...
 template <int X_DT, bool NORM>
-__global__ __launch_bounds__(256) void q4_xsum_kernel(const void* __restrict__ x, float* __restrict__ xs, int cols,
-                                                      int batch, int xs_stride, Q4Norm nrm) {
+__global__ __launch_bounds__(256) void q4_x16_kernel(const void* __restrict__ x, uint16_t* __restrict__ x16,
+                                                     float* __restrict__ fm, int cols, int batch, Q4Norm nrm) {
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int G = cols / 64;
     if (m >= batch) return;
-    float ss = 0.0f;
-    for (int hg0 = 0; hg0 < 2 * G; hg0 += 64) {
-        const int hg = hg0 + lane;
-        float acc = 0.0f;
-        if (hg < 2 * G) {
-            const size_t o = static_cast<size_t>(m) * cols + 32 * hg;
-            float v[32];
+    const int nb = cols / 8;
+    constexpr int kMaxB = 4096 / 8 / 64;
+    float v[kMaxB][8];
+    float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxB; ++i) {
+        const int b = lane + 64 * i;
+        if (b < nb) {
+            const size_t o = static_cast<size_t>(m) * cols + 8 * b;
             if (X_DT == 1) {
+                const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + o);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + o + 8 * i);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        v[8 * i + 2 * j] = __uint_as_float(u[j] << 16);
-                        v[8 * i + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    v[i][2 * j] = __uint_as_float(u[j] << 16);
+                    v[i][2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
                 }
             } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + o)[i];
-                    v[4 * i] = f.x;
-                    v[4 * i + 1] = f.y;
-                    v[4 * i + 2] = f.z;
-                    v[4 * i + 3] = f.w;
-                }
+                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + o);
+                const float4 a = p[0], c = p[1];
+                v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+                v[i][4] = c.x; v[i][5] = c.y; v[i][6] = c.z; v[i][7] = c.w;
             }
             if (NORM) {
-                float wn[32];
-                q4_norm_weights<32>(nrm, 32 * hg, wn);
+                float wn[8];
+                q4_norm_weights<8>(nrm, 8 * b, wn);
 #pragma unroll
-                for (int c = 0; c < 32; ++c) {
-                    ss = fmaf(v[c], v[c], ss);
-                    v[c] *= wn[c];
+                for (int e = 0; e < 8; ++e) {
+                    ss = fmaf(v[i][e], v[i][e], ss);
+                    v[i][e] *= wn[e];
                 }
             }
-            if (NORM || X_DT == 0) {
 #pragma unroll
-                for (int c = 0; c < 32; ++c) v[c] = bf16_to_f32(f32_to_bf16(v[c]));
-            }
-#pragma unroll
-            for (int c = 0; c < 32; ++c) acc += v[c];
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[i][e]));
         }
-        acc += __shfl_xor(acc, 1, 64);
-        if ((lane & 1) == 0 && hg < 2 * G) xs[static_cast<size_t>(hg >> 1) * xs_stride + m] = acc;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    // max |x'| in [2^(E-1), 2^E): x' 2^-(E-14) stays below 2^14
+    const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 14 : 0;
+    const float p = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int i = 0; i < kMaxB; ++i) {
+        const int b = lane + 64 * i;
+        if (b < nb) {
+            const u32x4_t h{pack_f16x2(v[i][0] * p, v[i][4] * p), pack_f16x2(v[i][1] * p, v[i][5] * p),
+                            pack_f16x2(v[i][2] * p, v[i][6] * p), pack_f16x2(v[i][3] * p, v[i][7] * p)};
+            *reinterpret_cast<u32x4_t*>(x16 + static_cast<size_t>(m) * cols + 8 * b) = h;
+        }
     }
     if (NORM) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if (lane == 0) xs[static_cast<size_t>(G) * xs_stride + m] = rsqrtf(ss / static_cast<float>(cols) + nrm.eps);
+    }
+    if (lane == 0) {
+        const float rs = NORM ? rsqrtf(ss / static_cast<float>(cols) + nrm.eps) : 1.0f;
+        fm[m] = ldexpf(rs, e - 8);
     }
 }
 
-template <int SB_DT, int X_DT, bool NORM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q4_gemm_kernel(Q4Parts parts, const void* __restrict__ x,
-                                                      const float* __restrict__ xs, int xs_stride, int cols,
-                                                      int batch, Q4Norm nrm) {
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// One nibble word -> four fp16 pairs 256 (s q + b) in the k order above;
+// sb = packed fp16 (256 s, 256 b).
+__device__ __forceinline__ u32x4_t q4_to_f16_scaled(uint32_t w, uint32_t sb) {
+    const f16x2_t sbv = __builtin_bit_cast(f16x2_t, sb);
+    const f16x2_t s2 = {sbv[0], sbv[0]}, b2 = {sbv[1], sbv[1]};
+    const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f16x2_t q = __builtin_bit_cast(f16x2_t, ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - k1024;
+        r[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
+    }
+    return r;
+}
+
+template <int SB_DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q4_gemm_kernel(
+    Q4Parts parts, const uint16_t* __restrict__ x16, const float* __restrict__ fm, int cols, int batch) {
     // the part of this workgroup's row tile (parts' tiles are consecutive in x)
     int pp = 0;
     while (pp + 1 < parts.n && static_cast<int>(blockIdx.x) >= parts.blk0[pp + 1]) ++pp;
@@ -1009,217 +1040,134 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const int G = cols / 64;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const int wr = wave & 1, wm = wave >> 1;
-    const int R0 = (blockIdx.x - parts.blk0[pp]) * 128, M0 = blockIdx.y * 128;
+    const int R0 = (blockIdx.x - parts.blk0[pp]) * kQ4GemmRows, M0 = blockIdx.y * kQ4GemmToks;
 
-    __shared__ __attribute__((aligned(16))) uint16_t Wl[128 * kQ4LD];
-    __shared__ __attribute__((aligned(16))) uint16_t Xl[128 * kQ4LD];
-    __shared__ __attribute__((aligned(16))) float sl[kQ4MaxGroups][128];
-    __shared__ float xsl[128];
+    __shared__ __attribute__((aligned(16))) uint16_t Xl[2][kQ4GemmToks * 64];
+    extern __shared__ __attribute__((aligned(16))) uint32_t sbl[];   // [G][256] packed fp16 (256 s, 256 b)
 
-    // scales of rows R0 .. R0+127, all groups
-    for (int idx = t; idx < 128 * G; idx += 256) {
+    for (int idx = t; idx < kQ4GemmRows * G; idx += 256) {
         const int r = idx / G, g = idx % G;
-        sl[g][r] = elem<SB_DT>::load(scales, static_cast<size_t>(min(R0 + r, rows - 1)) * G + g);
+        const size_t gi = static_cast<size_t>(min(R0 + r, rows - 1)) * G + g;
+        sbl[g * kQ4GemmRows + r] = pack_f16x2(256.0f * elem<SB_DT>::load(scales, gi), 256.0f * elem<SB_DT>::load(biases, gi));
     }
 
-    // staging: thread -> weight row t/2, words 4(t%2) .. +3 of the group;
-    // token t/2, columns 32(t%2) .. +31 of the group
-    const int srow = t >> 1, shalf = t & 1;
-    const uint32_t* wsrc = w + static_cast<size_t>(min(R0 + srow, rows - 1)) * (cols / 8) + 4 * shalf;
-    const int xm = min(M0 + srow, batch - 1);
-    const int xsm = min(M0 + (t & 127), batch - 1);
-    // one group's staging registers; two stages (raw x) keep groups g+1 and
-    // g+2 in flight while group g computes
-    struct Stage {
-        u32x4_t w, x[4];
-        float xs;
+    // x16 staging straight from global memory into LDS: wave w's load i fills
+    // tokens 8 (4w + i) .. +7 of the [128][64] tile, lane l the 16-byte
+    // piece l & 7 of token l >> 3, which holds the token's 8-column block
+    // (l & 7) ^ ((token >> 1) & 7) of the group (the swizzle puts the 16 rows
+    // of an operand read on different banks)
+    const uint16_t* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = 8 * (4 * wave + i) + (lane >> 3);
+        xsrc[i] = x16 + static_cast<size_t>(min(M0 + tok, batch - 1)) * cols + 8 * ((lane & 7) ^ ((tok >> 1) & 7));
+    }
+    // weight words: lane -> rows 64 wave + 16 rt + n, words 2 kb, 2 kb + 1 of each group
+    // (rows past the part's end read its last row; their outputs are not stored)
+    const int wrow = R0 + 64 * wave + n;
+    const uint32_t* wsrc = w + static_cast<size_t>(min(wrow, rows - 1)) * (cols / 8) + 2 * kb;
+    int wstep[4];   // word offset of row tile rt from row tile 0
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) wstep[rt] = (min(wrow + 16 * rt, rows - 1) - min(wrow, rows - 1)) * (cols / 8);
+
+    u32x2_t wa[2][4];
+    auto stage_x = [&](int buf, int g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(xsrc[i] + 64 * g),
+                                             (__attribute__((address_space(3))) void*)&Xl[buf][8 * (4 * wave + i) * 64],
+                                             16, 0, 0);
     };
-    auto fetch = [&](Stage& st, int g) {
-        u32x4_t& wreg = st.w;
-        u32x4_t (&xreg)[4] = st.x;
-        wreg = *reinterpret_cast<const u32x4_t*>(wsrc + 8 * g);
-        st.xs = xs[static_cast<size_t>(g) * xs_stride + xsm];
-        const size_t xo = static_cast<size_t>(xm) * cols + 64 * g + 32 * shalf;
-        if (NORM) {
-            // bf16(x w_norm); the token's inverse RMS scales the result
-            float wn[32];
-            q4_norm_weights<32>(nrm, 64 * g + 32 * shalf, wn);
+    auto fetch_w = [&](u32x2_t (&dst)[4], int g) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v[8];
-                if (X_DT == 1) {
-                    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * i);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        v[2 * j] = __uint_as_float(u[j] << 16);
-                        v[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
-                    }
-                } else {
-                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo + 8 * i);
-                    const float4 a = p[0], b = p[1];
-                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-                    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-                }
-                xreg[i] = u32x4_t{pack_bf16x2(v[0] * wn[8 * i], v[1] * wn[8 * i + 1]),
-                                  pack_bf16x2(v[2] * wn[8 * i + 2], v[3] * wn[8 * i + 3]),
-                                  pack_bf16x2(v[4] * wn[8 * i + 4], v[5] * wn[8 * i + 5]),
-                                  pack_bf16x2(v[6] * wn[8 * i + 6], v[7] * wn[8 * i + 7])};
-            }
-        } else if (X_DT == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                xreg[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + xo + 8 * i);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo + 8 * i);
-                const float4 a = p[0], b = p[1];
-                xreg[i] = u32x4_t{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y),
-                                  pack_bf16x2(b.z, b.w)};
-            }
-        }
+        for (int rt = 0; rt < 4; ++rt) dst[rt] = *reinterpret_cast<const u32x2_t*>(wsrc + wstep[rt] + 8 * g);
     };
 
-    f32x4_t acc[4][4];
+    f32x4_t acc[4][8];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < 8; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // group g from stage st, then st refilled with group gn (clamped, so the
-    // loads are unconditional and the compiler's vmcnt bookkeeping exact)
-    auto step = [&](Stage& st, int g, int gn) {
-        // (the two stages' steps are kept apart: interleaved by the scheduler
-        // they would not fit the registers)
+    // group g: x16 in LDS buffer g & 1, its weight words in wa[s]; on the
+    // way, group g + 1's x16 is requested into the other buffer and its
+    // weight words into wa[s ^ 1] (clamped, so every load is unconditional)
+    const int sw = (n >> 1) & 7;
+    auto step = [&](int s, int g) {
+        // (the two unrolled steps are kept apart: interleaved by the
+        // scheduler they would not fit the registers)
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<u32x4_t*>(&Wl[srow * kQ4LD + 32 * shalf + 8 * i]) = q4_to_bf16_interleaved(st.w[i]);
-            *reinterpret_cast<u32x4_t*>(&Xl[srow * kQ4LD + 32 * shalf + 8 * i]) = interleave8(st.x[i]);
-        }
-        if (t < 128) xsl[t] = -128.0f * st.xs;
+        // every wave's pieces of group g have landed, and every wave is done
+        // with group g - 1's buffer
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        fetch(st, gn);
-        f32x4_t P[4][4];
+        stage_x((g + 1) & 1, min(g + 1, G - 1));
+        const u32x2_t (&cur)[4] = wa[s];
+        fetch_w(wa[s ^ 1], min(g + 1, G - 1));
+        // the loads stay at the top of the step, a whole group's work ahead
+        // of their use (the scheduler would sink them next to it)
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t sb[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float x0 = xsl[64 * wm + 16 * b + n];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) P[a][b] = f32x4_t{x0, x0, x0, x0};
-        }
+        for (int rt = 0; rt < 4; ++rt) sb[rt] = sbl[g * kQ4GemmRows + 64 * wave + 16 * rt + n];
+        const uint16_t* xb = &Xl[g & 1][n * 64];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            u32x4_t A[4], B[4];
+            u32x4_t A[4];
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
-                A[rt] = *reinterpret_cast<const u32x4_t*>(&Wl[(64 * wr + 16 * rt + n) * kQ4LD + 32 * ks + 8 * kb]);
+            for (int rt = 0; rt < 4; ++rt) A[rt] = q4_to_f16_scaled(cur[rt][ks], sb[rt]);
+            const int off = 8 * ((2 * kb + ks) ^ sw);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                B[mt] = *reinterpret_cast<const u32x4_t*>(&Xl[(64 * wm + 16 * mt + n) * kQ4LD + 32 * ks + 8 * kb]);
+            for (int mh = 0; mh < 2; ++mh) {
+                u32x4_t B[4];
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
+                for (int mi = 0; mi < 4; ++mi)
+                    B[mi] = *reinterpret_cast<const u32x4_t*>(xb + 16 * (4 * mh + mi) * 64 + off);
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) P[rt][mt] = mfma_16x16x32_bf16(A[rt], B[mt], P[rt][mt]);
+                for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi)
+                        acc[rt][4 * mh + mi] = mfma_16x16x32_f16(A[rt], B[mi], acc[rt][4 * mh + mi]);
+            }
         }
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(&sl[g][64 * wr + 16 * rt + 4 * kb]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[rt][mt][i] = fmaf(sv[i], P[rt][mt][i], acc[rt][mt][i]);
-        }
-        __syncthreads();
     };
-    Stage s0;
-    fetch(s0, 0);
-    if constexpr (NORM) {
-        // the normed x is formed as it is fetched, so its loads complete in
-        // the fetch: one stage (a second would not fit the registers)
-        for (int g = 0; g < G; ++g) step(s0, g, min(g + 1, G - 1));
-    } else {
-        Stage s1;
-        fetch(s1, min(1, G - 1));
-        int g = 0;
-        for (; g + 1 < G; g += 2) {
-            step(s0, g, min(g + 2, G - 1));
-            step(s1, g + 1, min(g + 3, G - 1));
-        }
-        if (g < G) step(s0, g, g);
+    stage_x(0, 0);
+    fetch_w(wa[0], 0);
+    int g = 0;
+    for (; g + 1 < G; g += 2) {
+        step(0, g);
+        step(1, g + 1);
     }
-    // bias sums: acc += B X^T over the groups (k = g), bf16x3. A lane holds
-    // B[row][8kb .. 8kb+7] and X[token][8kb .. 8kb+7] of a 32-group step;
-    // groups past G are zero.
-    for (int g0 = 0; g0 < G; g0 += 32) {
-        u32x4_t bh[4], bl[4], xh[4], xl[4];
+    if (g < G) step(0, g);
+
+    // lane: token 16mt + n, rows 64 wave + 16 rt + 4 kb .. +3 (adjacent in y)
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const size_t gi = static_cast<size_t>(min(R0 + 64 * wr + 16 * rt + n, rows - 1)) * G + g0 + 8 * kb;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                v[e] = g0 + 8 * kb + e < G ? elem<SB_DT>::load(biases, gi + e) : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                uint32_t hh, ll;
-                split_bf16x2(v[2 * e], v[2 * e + 1], hh, ll);
-                bh[rt][e] = hh;
-                bl[rt][e] = ll;
-            }
-        }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const float* xp = xs + static_cast<size_t>(g0 + 8 * kb) * xs_stride +
-                              min(M0 + 64 * wm + 16 * mt + n, batch - 1);
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = g0 + 8 * kb + e < G ? xp[static_cast<size_t>(e) * xs_stride] : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                uint32_t hh, ll;
-                split_bf16x2(v[2 * e], v[2 * e + 1], hh, ll);
-                xh[mt][e] = hh;
-                xl[mt][e] = ll;
-            }
-        }
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                acc[rt][mt] = mfma_16x16x32_bf16(bl[rt], xh[mt], acc[rt][mt]);
-                acc[rt][mt] = mfma_16x16x32_bf16(bh[rt], xl[mt], acc[rt][mt]);
-                acc[rt][mt] = mfma_16x16x32_bf16(bh[rt], xh[mt], acc[rt][mt]);
-            }
-    }
-    // lane: token 64wm + 16mt + n, rows 64wr + 16rt + 4kb .. +3 (adjacent in y)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int m = M0 + 64 * wm + 16 * mt + n;
+    for (int mt = 0; mt < 8; ++mt) {
+        const int m = M0 + 16 * mt + n;
         if (m >= batch) continue;
-        const float rs = NORM ? xs[static_cast<size_t>(G) * xs_stride + m] : 1.0f;
+        const float f = fm[m];
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-            const int r = R0 + 64 * wr + 16 * rt + 4 * kb;
+            const int r = R0 + 64 * wave + 16 * rt + 4 * kb;
             const size_t o = static_cast<size_t>(m) * rows + r;
+            f32x4_t v = acc[rt][mt];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (NORM) acc[rt][mt][i] *= rs;
-                if (res && r + i < rows)
-                    acc[rt][mt][i] += ybf ? elem<1>::load(res, o + i) : elem<0>::load(res, o + i);
+                v[i] *= f;
+                if (res && r + i < rows) v[i] += ybf ? elem<1>::load(res, o + i) : elem<0>::load(res, o + i);
             }
             if (r + 3 < rows && (rows & 3) == 0) {
                 if (ybf)
                     *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
-                        u32x2_t{pack_bf16x2(acc[rt][mt][0], acc[rt][mt][1]), pack_bf16x2(acc[rt][mt][2], acc[rt][mt][3])};
+                        u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 else
-                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = acc[rt][mt];
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = v;
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (r + i >= rows) continue;
-                    if (ybf) elem<1>::store(y, o + i, acc[rt][mt][i]);
-                    else elem<0>::store(y, o + i, acc[rt][mt][i]);
+                    if (ybf) elem<1>::store(y, o + i, v[i]);
+                    else elem<0>::store(y, o + i, v[i]);
                 }
             }
         }
@@ -1277,24 +1225,26 @@ static Q4Parts q4_pack_parts(const qff_q4_part* parts, int nparts, int rpb, int&
     return P;
 }
 
-// Many tokens: group sums (and inverse RMS) once per token slice, then one
+// Many tokens: x16 and the per-token factors once per token slice, then one
 // tiled launch over all parts (the small parts' tiles fill the chip beside the
 // large one's).
 template <bool NORM>
 static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_part* parts, int nparts,
                                 qff_dtype sb_dtype, const void* x, qff_dtype x_dtype, const Q4Norm& norm,
                                 int cols, int batch) {
+    const int G = cols / 64;
+    const int lds = G * kQ4GemmRows * 4;   // packed (s, b) of the row tile
+    QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemm_kernel<1>>(lds)));
+    QFF_CHECK_HIP_RET((q4_allow_lds<q4_gemm_kernel<2>>(lds)));
     for (int m0 = 0; m0 < batch; m0 += ctx->q4_xs_tokens) {
         const int mb = min(ctx->q4_xs_tokens, batch - m0);
         const void* xm = static_cast<const char*>(x) + static_cast<size_t>(m0) * cols * (x_dtype == QFF_BF16 ? 2 : 4);
         {
-            ProfScope prof(ctx, stream, "q4_xsum");
+            ProfScope prof(ctx, stream, "q4_x16");
             if (x_dtype == QFF_BF16)
-                q4_xsum_kernel<1, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
-                                                                        ctx->q4_xs_tokens, norm);
+                q4_x16_kernel<1, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_x16, ctx->q4_fm, cols, mb, norm);
             else
-                q4_xsum_kernel<0, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_xs, cols, mb,
-                                                                        ctx->q4_xs_tokens, norm);
+                q4_x16_kernel<0, NORM><<<(mb + 3) / 4, 256, 0, stream>>>(xm, ctx->q4_x16, ctx->q4_fm, cols, mb, norm);
         }
         // one launch over every part's row tiles, outputs offset to this slice
         qff_q4_part sl[QFF_Q4_MAX_PARTS];
@@ -1305,16 +1255,13 @@ static hipError_t q4_gemm_parts(qff_ctx* ctx, hipStream_t stream, const qff_q4_p
             if (parts[i].residual) sl[i].residual = static_cast<const char*>(parts[i].residual) + yoff;
         }
         int tiles = 0;
-        const Q4Parts P = q4_pack_parts(sl, nparts, 128, tiles);
-        const dim3 grid(tiles, (mb + 127) / 128);
+        const Q4Parts P = q4_pack_parts(sl, nparts, kQ4GemmRows, tiles);
+        const dim3 grid(tiles, (mb + kQ4GemmToks - 1) / kQ4GemmToks);
         ProfScope prof(ctx, stream, "q4_gemm");
-#define QFF_Q4G(S, X) \
-    q4_gemm_kernel<S, X, NORM><<<grid, 256, 0, stream>>>(P, xm, ctx->q4_xs, ctx->q4_xs_tokens, cols, mb, norm)
-#define QFF_Q4G_X(S) \
-    if (x_dtype == QFF_BF16) { QFF_Q4G(S, 1); } else { QFF_Q4G(S, 0); }
-        if (sb_dtype == QFF_BF16) { QFF_Q4G_X(1); } else { QFF_Q4G_X(2); }
-#undef QFF_Q4G_X
-#undef QFF_Q4G
+        if (sb_dtype == QFF_BF16)
+            q4_gemm_kernel<1><<<grid, 256, lds, stream>>>(P, ctx->q4_x16, ctx->q4_fm, cols, mb);
+        else
+            q4_gemm_kernel<2><<<grid, 256, lds, stream>>>(P, ctx->q4_x16, ctx->q4_fm, cols, mb);
     }
     return hipGetLastError();
 }

@@ -349,7 +349,8 @@ def test_gqa_prefill_config3_exact_call(hip):
     k 512, v 512 rows from hidden 2048, fp16 scales) over T = 8192 tokens in
     one call, then qff_gqa_prefill on its bf16 outputs from position 0.
     Projections: 64 sampled tokens of every part against the fp64 product of
-    the dequantized weights, each bf16 output within one bf16 ulp. Attention:
+    the dequantized weights, each bf16 output within one bf16 ulp plus
+    2.5e-3 of its row's RMS (fp16 operands). Attention:
     all 8192 output rows against a vectorised fp32 restatement of the
     oracle's arithmetic, itself checked against the oracle on 8 rows."""
     import qff
@@ -371,16 +372,17 @@ def test_gqa_prefill_config3_exact_call(hip):
     out = qff.gqa_prefill(ctx, {kk: f32_tensor(vv) for kk, vv in p.items()}, qg.view(T, 16, 512),
                           k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
-    # projections on sampled tokens: the fp32 accumulation over 2048 columns
-    # is off by ~1e-6 of the terms' magnitudes (absolute, so it dominates
-    # near zero), then rounded once to bf16
+    # projections on sampled tokens: the GEMM's fp16 operands (W rounded once
+    # to 11 significant bits) put ~3e-4 of each row's RMS of noise on every
+    # output (absolute, so it dominates near zero), then rounded once to bf16
     toks = sorted({0, 1, 127, 128, 4095, 4096, 8191} | set(rng.integers(0, T, 57).tolist()))
     xs = O.bf16_to_f32(xb[toks]).astype(np.float64)
     for (w, s, b), y in zip(ws, (qg, k, v)):
         ref = xs @ O.q4_dequant(w, s, b, O.F16).astype(np.float64).T
         got = to_np(y)[toks]
-        err = np.abs(got - ref) - bf16_ulp(ref)
-        assert np.all(err <= 1e-4), f"Q4 GEMM output beyond one bf16 ulp + 1e-4: worst excess {err.max():.3g}"
+        rms = np.sqrt((ref * ref).mean(axis=1, keepdims=True))
+        err = (np.abs(got - ref) - bf16_ulp(ref)) / rms
+        assert np.all(err <= 2.5e-3), f"Q4 GEMM output beyond one bf16 ulp + 2.5e-3 RMS: worst {err.max():.3g}"
     print("  projections ok", flush=True)
     qg_f = to_np(qg).reshape(T, 16, 512)
     kref = np.zeros((T, 2, 256), np.uint16)

@@ -2,22 +2,25 @@
 
 qff_q4_dequant must be bit-exact with the closed form
 (QwenQ4ActiveExpertStreamingRunner.swift:899-922) for f16 and bf16 scales.
-qff_q4_matmul is checked against an fp64 product of the dequantized matrix:
-with bf16 activations (exact MFMA operands) the relative Frobenius error must
-stay <= 1e-5 (fp32 accumulation order only). Decode batches (<= 32 tokens)
-with fp32 activations take them as bf16 hi + lo pairs, so they meet the same
-1e-5 against the exact fp32 x and against the reference's own fp32 factored
-order (deltanet.metal:816-861); the many-token GEMM takes fp32 x rounded to
-bf16 and matches the fp64 product of the rounded x to 1e-5.
+qff_q4_matmul is checked against an fp64 product of the dequantized matrix.
+Decode batches (<= 32 tokens) take the nibbles exactly and bf16 x exactly
+(fp32 x as bf16 hi + lo pairs), so the relative Frobenius error must stay
+<= 1e-5 (fp32 accumulation order only), against the exact fp32 x and against
+the reference's own fp32 factored order (deltanet.metal:816-861). The
+many-token GEMM (>= 33 tokens) runs on fp16 operands, W rounded once to
+fp16 (2^8 (s q + b)) and x to fp16 after a per-token power-of-two shift:
+each operand carries 11 significant bits, so its bar against the exact
+product is rel <= 1e-3 (measured ~3e-4), for bf16 and fp32 x alike, and for
+tokens whose magnitudes span 2^-40 .. 2^40 (dequantized weights keep 11 bits
+for magnitudes 2^-22 .. 255, the range of real Q4 checkpoints).
 
 qff_q4_norm_matmul_parts (RMSNorm, deltanet.metal:18-53, feeding the
 products) is checked against a mirror of its arithmetic (inverse RMS in
-fp64 applied to the row sums; x w_norm exact in fp32 for decode batches, as
-bf16 for the GEMM), rel <= 1e-5 for fp32 outputs, and against the oracle's
-RMSNorm (pinned by the reference's KAT) followed by an fp64 product: rel <=
-1e-5 for decode batches, <= 1e-2 for the GEMM (bf16 rounding of the normed
-activations). Tokens carry different scales so a norm taken from the wrong
-token shows. The residual store (y = residual + x W^T) must equal the
+fp64 applied to the row sums, x w_norm exact in fp32), rel <= 1e-5 for fp32
+outputs of decode batches, and against the oracle's RMSNorm (pinned by the
+reference's KAT) followed by an fp64 product: rel <= 1e-5 for decode
+batches, <= 1e-3 for the GEMM (fp16 operands). Tokens carry different
+scales so a norm taken from the wrong token shows. The residual store (y = residual + x W^T) must equal the
 product plus the residual bit for bit with fp32 outputs, in place too."""
 import numpy as np
 import pytest
@@ -53,6 +56,9 @@ def _rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
+GEMM_MIN_BATCH = 33   # batches from here on take the fp16-operand GEMM
+
+
 @pytest.mark.parametrize("rows,cols,batch", [(8192, 2048, 1), (512, 2048, 5), (4096, 2048, 16),
                                              (2048, 4096, 32), (100, 2048, 33), (32, 2048, 1),
                                              # 64-row workgroups (batch >= 2, >= 8192 rows), ragged end
@@ -76,7 +82,7 @@ def test_q4_matmul_bf16_activations(hip, rows, cols, batch):
     torch.cuda.synchronize()
     dense = O.q4_dequant(w, s, b, O.F16).astype(np.float64)
     ref = O.bf16_to_f32(xb).astype(np.float64) @ dense.T
-    assert _rel(to_np(y), ref) <= 1e-5
+    assert _rel(to_np(y), ref) <= (1e-3 if batch >= GEMM_MIN_BATCH else 1e-5)
 
 
 def test_q4_matmul_f32_activations_vs_reference_order(hip):
@@ -112,9 +118,10 @@ def test_q4_gemv_f32_activations_64_row_workgroups(hip):
     assert _rel(to_np(y), ref) <= 1e-5
 
 
-def test_q4_gemm_f32_activations_round_like_bf16(hip):
-    """Many-token path with fp32 activations: the matrix cores take x rounded
-    to bf16, so the product matches the fp64 product with bf16-rounded x."""
+def test_q4_gemm_f32_activations(hip):
+    """Many-token path with fp32 activations: the matrix cores take x as fp16
+    after the per-token shift, so the product is the fp64 product of the
+    exact fp32 x to the GEMM's fp16-operand bar."""
     import qff
     rows, cols, batch = 640, 2048, 96
     w, s, b = synth.q4_weight(rows, cols, seed=7)
@@ -123,8 +130,36 @@ def test_q4_gemm_f32_activations_round_like_bf16(hip):
     y = qff.q4_matmul(ctx, *_w_gpu(w, s, b, "f16"), f32_tensor(x))
     torch.cuda.synchronize()
     dense = O.q4_dequant(w, s, b, O.F16).astype(np.float64)
-    ref = O.round_bf16(x).astype(np.float64) @ dense.T
-    assert _rel(to_np(y), ref) <= 1e-5
+    ref = x.astype(np.float64) @ dense.T
+    assert _rel(to_np(y), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_q4_gemm_token_magnitudes(hip, xdt):
+    """Tokens scaled by 2^-40 .. 2^40 (beyond fp16's range both ways, and an
+    all-zero token): the per-token power-of-two shift keeps every token's x16
+    in fp16's normal range, so each token's row of outputs meets the bar on
+    its own, with no overflow and no flush to zero."""
+    import qff
+    rows, cols, batch = 300, 1024, 48
+    w, s, b = synth.q4_weight(rows, cols, seed=21, sb_dtype="bf16")
+    rng = np.random.default_rng(22)
+    scale = 2.0 ** np.linspace(-40, 40, batch)
+    x = (rng.standard_normal((batch, cols)) * scale[:, None]).astype(np.float32)
+    x[5] = 0.0
+    x[7, ::3] *= 1e-4   # a wide spread inside one token
+    if xdt == "bf16":
+        x = O.round_bf16(x)
+    xt = bf16_tensor(O.f32_to_bf16(x)) if xdt == "bf16" else f32_tensor(x)
+    ctx = qff.Context(max_batch=1, max_ctx=64, max_prefill_tokens=64)
+    y = to_np(qff.q4_matmul(ctx, *_w_gpu(w, s, b, "bf16"), xt))
+    torch.cuda.synchronize()
+    ref = x.astype(np.float64) @ O.q4_dequant(w, s, b, O.BF16).astype(np.float64).T
+    assert np.all(np.isfinite(y))
+    assert np.all(y[5] == 0.0)
+    for m in range(batch):
+        if m != 5:
+            assert _rel(y[m], ref[m]) <= 1e-3, f"token {m} (scale 2^{np.log2(scale[m]):.1f})"
 
 
 def test_q4_rejects_bad_shapes(hip):
@@ -161,7 +196,7 @@ def test_q4_matmul_parts_match_single_products(hip, batch):
                                                     s1.view(torch.int16) if s1.dtype == torch.bfloat16 else s1)
     w, s, b = ws[2]
     ref = O.bf16_to_f32(xb).astype(np.float64) @ O.q4_dequant(w, s, b, O.F16).astype(np.float64).T
-    assert _rel(to_np(outs[2]), ref) <= 1e-5
+    assert _rel(to_np(outs[2]), ref) <= (1e-3 if batch >= GEMM_MIN_BATCH else 1e-5)
 
 
 def test_q4_matmul_parts_rejects_bad_calls(hip):
@@ -179,14 +214,13 @@ def test_q4_matmul_parts_rejects_bad_calls(hip):
     assert lib().qff_q4_matmul_parts(ctx.handle, None, arr, 1, 2, x.data_ptr(), 1, 128, 1) == -1
 
 
-def _norm_mirror(x, wn, eps, gemm):
-    """x w_norm as the product takes it (fp32 multiply; rounded to bf16 by
-    the many-token GEMM, exact as hi + lo in the decode kernels) and the
-    inverse RMS of each token in fp64."""
+def _norm_mirror(x, wn, eps):
+    """x w_norm as the product takes it (fp32 multiply) and the inverse RMS
+    of each token in fp64."""
     x64 = x.astype(np.float64)
     r = 1.0 / np.sqrt((x64 * x64).mean(axis=1) + eps)
     xw = (x.astype(np.float32) * wn.astype(np.float32)).astype(np.float32)
-    return (O.round_bf16(xw) if gemm else xw).astype(np.float64), r
+    return xw.astype(np.float64), r
 
 
 @pytest.mark.parametrize("batch,cols,xdt,ndt", [(1, 2048, "bf16", "f32"), (1, 4096, "f32", "bf16"),
@@ -213,14 +247,15 @@ def test_q4_norm_matmul_parts(hip, batch, cols, xdt, ndt):
     ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=512)
     outs = qff.q4_norm_matmul_parts(ctx, parts, xt, nt, eps, out_dtypes=[dt for _, dt in shapes])
     torch.cuda.synchronize()
-    gemm = batch >= 33
-    xq, r = _norm_mirror(x, wn, eps, gemm)
+    gemm = batch >= GEMM_MIN_BATCH
+    xq, r = _norm_mirror(x, wn, eps)
     xn = np.stack([O.rmsnorm(x[m], wn, eps, prec=64) for m in range(batch)]).astype(np.float64)
+    bar = 1e-3 if gemm else 1e-5
     for o, (w, s, b), (_, dt) in zip(outs, ws, shapes):
         dense = O.q4_dequant(w, s, b, O.F16).astype(np.float64)
         got = to_np(o)
-        assert _rel(got, r[:, None] * (xq @ dense.T)) <= (1e-5 if dt == torch.float32 else 4e-3)
-        assert _rel(got, xn @ dense.T) <= (1e-2 if gemm else 1e-5 if dt == torch.float32 else 4e-3)
+        assert _rel(got, r[:, None] * (xq @ dense.T)) <= (bar if dt == torch.float32 else 4e-3)
+        assert _rel(got, xn @ dense.T) <= (bar if dt == torch.float32 else 4e-3)
 
 
 @pytest.mark.parametrize("batch", [1, 7, 33])
@@ -231,7 +266,7 @@ def test_q4_matmul_parts_residual(hip, batch):
     import qff
     print(f"q4_matmul_parts residual batch={batch}", flush=True)
     cols, rows = 2048, 640
-    w, s, b = synth.q4_weight(rows, cols, seed=5 + batch)
+    w, s, b = synth.q4_weight(rows, cols, seed=5 + batch, sb_dtype="bf16")
     part = _w_gpu(w, s, b, "bf16")
     rng = np.random.default_rng(batch)
     xb = O.f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32))
