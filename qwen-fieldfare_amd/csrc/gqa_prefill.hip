@@ -10,9 +10,11 @@
 //          reference also rounds q to half, Runner:1119-1126) and of the 2 k
 //          heads (appended to the bf16 cache together with v).
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
-//          of one kv head (128 rows; eight waves of 16 rows = 2 tokens x 8
-//          heads, so accumulators and q stay in VGPRs and two waves share
-//          each SIMD) and walks 64-position K/V tiles staged in LDS
+//          of one kv head (128 rows; four wave pairs of 32 rows = 4 tokens
+//          x 8 heads, each wave scoring half of a tile's positions and
+//          accumulating half of the output dims, so accumulators and q stay
+//          in VGPRs and two waves share each SIMD) and walks 64-position
+//          K/V tiles staged in LDS
 //          row-major (double-buffered; the next tile's global loads are in
 //          flight while the current one computes), converted from the bf16
 //          cache to fp16 as they are staged (exact for the cache's values),
@@ -168,41 +170,56 @@ __device__ __forceinline__ void tile_store(const TileRegs& r, uint16_t* __restri
     }
 }
 
-// grid (ceil(T/16), 2 kv heads), 512 threads.
+// grid (ceil(T/16), 2 kv heads), 512 threads: four wave pairs, pair pr
+// owning the 32 rows of tokens t0 + 4 pr .. t0 + 4 pr + 3 (x the 8 q heads)
+// as two 16-row tiles. Wave e of a pair scores positions 32e .. 32e + 31 of
+// each K tile for both row tiles (each K operand read from LDS feeds two
+// MFMAs), the pair meets once for the row maxima and once for the P
+// operands (through LDS), and wave e accumulates output dims
+// 128e .. 128e + 127 over all 64 positions (each V operand feeds two MFMAs):
+// 34 KB of LDS reads per wave and tile instead of the 64 KB a wave of 16
+// rows scoring every position and accumulating every dim would need.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const uint16_t* __restrict__ qb, const void* __restrict__ q_gate, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int start, int T, void* __restrict__ out) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kPfKT * kKStride];
     __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kPfKT * kKStride];
+    __shared__ float xrow[kPfThreads / 64][2][16];                              // per wave, row tile, row
+    __shared__ __attribute__((aligned(16))) u32x4_t xp[kPfThreads / 64][2][64];  // per wave, row tile, lane
     const int nqb = (T + kPfQB - 1) / kPfQB;
     const int q_blk = nqb - 1 - static_cast<int>(blockIdx.x);
     const int kvh = blockIdx.y;
     const int t0 = q_blk * kPfQB;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = lane & 15, kb = lane >> 4;
+    const int pr = wave >> 1, e = wave & 1, partner = wave ^ 1;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
 
-    // this lane's q row: token t0 + 2w + n/8, head n%8
-    u32x4_t qreg[8];
-    const int tok_q = min(t0 + 2 * wave + (n >> 3), T - 1);
-    const int lim = start + tok_q;
-    {
+    // this lane's q rows: row tile rt = token t0 + 4 pr + 2 rt + n/8, head n%8
+    u32x4_t qreg[2][8];
+    int lim[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int tok_q = min(t0 + 4 * pr + 2 * rt + (n >> 3), T - 1);
+        lim[rt] = start + tok_q;
         const uint16_t* qrow = qb + (static_cast<size_t>(tok_q) * 16 + kvh * 8 + (n & 7)) * 256;
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) qreg[jj] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj + 8 * kb);
+        for (int jj = 0; jj < 8; ++jj) qreg[rt][jj] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj + 8 * kb);
         // consumed here (no instruction) so the loads are not sunk into the loop
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) asm volatile("" ::"v"(qreg[jj]));
+        for (int jj = 0; jj < 8; ++jj) asm volatile("" ::"v"(qreg[rt][jj]));
     }
     const int kv_end = start + min(T, t0 + kPfQB);
     const int ntiles = (kv_end + kPfKT - 1) / kPfKT;
     const int first_masked = (start + t0) / kPfKT;   // tiles before this need no causal mask
 
-    float m_run = -INFINITY, d_run = 0.0f;
-    f32x4_t oacc[16];
+    float m_run[2] = {-INFINITY, -INFINITY}, d_run[2] = {0.0f, 0.0f};
+    f32x4_t oacc[2][8];
 #pragma unroll
-    for (int jd = 0; jd < 16; ++jd) oacc[jd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int jd = 0; jd < 8; ++jd) oacc[rt][jd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     TileRegs regs;
     tile_load(regs, k_cache, v_cache, kvh, 0, kv_end, t);
@@ -211,113 +228,153 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     // loop's waits would also cover the next tile's loads each iteration
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    const int kp = 32 * e;   // the wave's first scored position in a tile
     for (int kt = 0; kt < ntiles; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < ntiles;
         if (more) tile_load(regs, k_cache, v_cache, kvh, (kt + 1) * kPfKT, kv_end, t);
         const int p0 = kt * kPfKT;
-        // S^T = K Q^T for kPfKT/16 position tiles, 32 dims at a time: the K
-        // operands of the next 32 dims are read while the four independent
-        // MFMAs of these run
-        constexpr int NPT = kPfKT / 16;
-        f32x4_t s[NPT];
+        // S^T = K Q^T for the wave's two 16-position tiles x both row tiles,
+        // 32 dims at a time: the K operands of the next 32 dims are read
+        // while the four independent MFMAs of these run
+        f32x4_t s[2][2];
 #pragma unroll
-        for (int pt = 0; pt < NPT; ++pt) s[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        u32x4_t ka[2][NPT];
+        for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int pt = 0; pt < NPT; ++pt)
-            ka[0][pt] = *reinterpret_cast<const u32x4_t*>(&Ks[cur][(16 * pt + n) * kKStride + 8 * kb]);
+            for (int pt = 0; pt < 2; ++pt) s[rt][pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        u32x4_t ka[2][2];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+            ka[0][pt] = *reinterpret_cast<const u32x4_t*>(&Ks[cur][(kp + 16 * pt + n) * kKStride + 8 * kb]);
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
             if (jj + 1 < 8) {
 #pragma unroll
-                for (int pt = 0; pt < NPT; ++pt)
+                for (int pt = 0; pt < 2; ++pt)
                     ka[(jj + 1) & 1][pt] = *reinterpret_cast<const u32x4_t*>(
-                        &Ks[cur][(16 * pt + n) * kKStride + 32 * (jj + 1) + 8 * kb]);
+                        &Ks[cur][(kp + 16 * pt + n) * kKStride + 32 * (jj + 1) + 8 * kb]);
             }
 #pragma unroll
-            for (int pt = 0; pt < NPT; ++pt) s[pt] = mfma_16x16x32_f16(ka[jj & 1][pt], qreg[jj], s[pt]);
+            for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) s[rt][pt] = mfma_16x16x32_f16(ka[jj & 1][pt], qreg[rt][jj], s[rt][pt]);
         }
-        // softmax (base 2); lane holds q row n, positions p0 + 16pt + 4kb + i
-        float tmax = -INFINITY;
+        // softmax (base 2); lane holds q row n of each row tile, positions
+        // p0 + kp + 16pt + 4kb + i; the pair's maxima over all 64 positions
         const bool masked = kt >= first_masked;
+        float tm[2];
 #pragma unroll
-        for (int pt = 0; pt < NPT; ++pt)
+        for (int rt = 0; rt < 2; ++rt) {
+            tm[rt] = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (masked && p0 + 16 * pt + 4 * kb + i > lim) s[pt][i] = -INFINITY;
-                tmax = fmaxf(tmax, s[pt][i]);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        if (__any(tmax > m_run + kLazy)) {
-            const float m_new = tmax > m_run + kLazy ? tmax : m_run;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            d_run *= alpha;
-            float al[4];
+            for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * kb + i, 64);
-#pragma unroll
-            for (int jd = 0; jd < 16; ++jd)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) oacc[jd][i] *= al[i];
+                for (int i = 0; i < 4; ++i) {
+                    if (masked && p0 + kp + 16 * pt + 4 * kb + i > lim[rt]) s[rt][pt][i] = -INFINITY;
+                    tm[rt] = fmaxf(tm[rt], s[rt][pt][i]);
+                }
+            tm[rt] = fmaxf(tm[rt], __shfl_xor(tm[rt], 16, 64));
+            tm[rt] = fmaxf(tm[rt], __shfl_xor(tm[rt], 32, 64));
+            if (kb == 0) xrow[wave][rt][n] = tm[rt];
         }
-        // A operands of O += P V, one per 32 positions: k = 8kb + j <->
-        // position 32c + 16(j/4) + 4kb + j%4
-        u32x4_t pa[NPT / 2];
+        __syncthreads();
+        // both waves of the pair take the same maxima and so keep the same
+        // running max (the lazy rule sees the same values in both)
 #pragma unroll
-        for (int c = 0; c < NPT / 2; ++c) {
+        for (int rt = 0; rt < 2; ++rt) {
+            tm[rt] = fmaxf(tm[rt], xrow[partner][rt][n]);
+            if (__any(tm[rt] > m_run[rt] + kLazy)) {
+                const float m_new = tm[rt] > m_run[rt] + kLazy ? tm[rt] : m_run[rt];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+                m_run[rt] = m_new;
+                d_run[rt] *= alpha;
+                float al[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * kb + i, 64);
+#pragma unroll
+                for (int jd = 0; jd < 8; ++jd)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) oacc[rt][jd][i] *= al[i];
+            }
+        }
+        // P of the wave's 32 positions: the A operand of O += P V for that
+        // 32-position chunk, k = 8kb + j <-> position kp + 16(j/4) + 4kb + j%4
+        u32x4_t pa[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
             float pe[2][4];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pe[h][i] = __builtin_amdgcn_exp2f(s[2 * c + h][i] - m_run);
-                    d_run += pe[h][i];
+                    pe[h][i] = __builtin_amdgcn_exp2f(s[rt][h][i] - m_run[rt]);
+                    d_run[rt] += pe[h][i];
                 }
-            pa[c] = u32x4_t{pack_f16x2(pe[0][0], pe[0][1]), pack_f16x2(pe[0][2], pe[0][3]),
-                            pack_f16x2(pe[1][0], pe[1][1]), pack_f16x2(pe[1][2], pe[1][3])};
+            pa[rt] = u32x4_t{pack_f16x2(pe[0][0], pe[0][1]), pack_f16x2(pe[0][2], pe[0][3]),
+                             pack_f16x2(pe[1][0], pe[1][1]), pack_f16x2(pe[1][2], pe[1][3])};
+            xp[wave][rt][lane] = pa[rt];
         }
-        // O += P V; B operand through the LDS transpose read: lane s of group
-        // kb points at position 32c + 16h + 4kb + s/4, dims 16jd + 4(s%4)
-        const uint16_t* vbase = &Vs[cur][(4 * kb + (n >> 2)) * kKStride + 4 * (n & 3)];
+        __syncthreads();
+        // O += P V for dims 128e .. 128e + 127: the wave's own chunk (pa),
+        // then the partner's (its P operands, read back lane for lane); B
+        // operand through the LDS transpose read: lane s of group kb points at
+        // position 32c + 16h + 4kb + s/4, dims 128e + 16jd + 4(s%4)
+        const uint16_t* vbase = &Vs[cur][(4 * kb + (n >> 2)) * kKStride + 4 * (n & 3) + 128 * e];
 #pragma unroll
-        for (int c = 0; c < NPT / 2; ++c)
+        for (int cc = 0; cc < 2; ++cc) {
+            u32x4_t A[2];
 #pragma unroll
-            for (int j0 = 0; j0 < 16; j0 += 8) {
-                u32x2_t v0[8], v1[8];
+            for (int rt = 0; rt < 2; ++rt) A[rt] = cc == 0 ? pa[rt] : xp[partner][rt][lane];
+            const uint16_t* vb = vbase + 32 * (cc == 0 ? e : 1 - e) * kKStride;
 #pragma unroll
-                for (int jd = 0; jd < 8; ++jd) {
-                    v0[jd] = lds_read_tr16(vbase + 32 * c * kKStride + 16 * (j0 + jd));
-                    v1[jd] = lds_read_tr16(vbase + (32 * c + 16) * kKStride + 16 * (j0 + jd));
+            for (int j0 = 0; j0 < 8; j0 += 4) {
+                u32x2_t v0[4], v1[4];
+#pragma unroll
+                for (int jd = 0; jd < 4; ++jd) {
+                    v0[jd] = lds_read_tr16(vb + 16 * (j0 + jd));
+                    v1[jd] = lds_read_tr16(vb + 16 * kKStride + 16 * (j0 + jd));
                 }
 #pragma unroll
-                for (int jd = 0; jd < 8; ++jd)
-                    oacc[j0 + jd] =
-                        mfma_16x16x32_f16(pa[c], u32x4_t{v0[jd][0], v0[jd][1], v1[jd][0], v1[jd][1]}, oacc[j0 + jd]);
+                for (int jd = 0; jd < 4; ++jd) {
+                    const u32x4_t B = u32x4_t{v0[jd][0], v0[jd][1], v1[jd][0], v1[jd][1]};
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) oacc[rt][j0 + jd] = mfma_16x16x32_f16(A[rt], B, oacc[rt][j0 + jd]);
+                }
             }
+        }
         if (more) tile_store(regs, Ks[cur ^ 1], Vs[cur ^ 1], t);
         __syncthreads();
     }
 
-    // epilogue: O / d * sigmoid(gate); oacc[jd][i] = O[row 4kb+i][dim 16jd+n]
-    float d = d_run;
-    d += __shfl_xor(d, 16, 64);
-    d += __shfl_xor(d, 32, 64);
+    // epilogue: O / d * sigmoid(gate), d the pair's row sums;
+    // oacc[rt][jd][i] = O[row 4kb+i of row tile rt][dim 128e + 16jd + n]
+    float dt[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = 4 * kb + i;
-        const float inv_d = 1.0f / __shfl(d, row, 64);
-        const int tok = t0 + 2 * wave + (row >> 3);
-        if (tok >= T) continue;
-        const int h = kvh * 8 + (row & 7);
-        const size_t qi = static_cast<size_t>(tok) * 16 + h;
+    for (int rt = 0; rt < 2; ++rt) {
+        float d = d_run[rt];
+        d += __shfl_xor(d, 16, 64);
+        d += __shfl_xor(d, 32, 64);
+        dt[rt] = d;
+        if (kb == 0) xrow[wave][rt][n] = d;
+    }
+    __syncthreads();
 #pragma unroll
-        for (int jd = 0; jd < 16; ++jd) {
-            const int dim = 16 * jd + n;
-            const float g = elem<IN_DT>::load(q_gate, qi * 512 + 256 + dim);
-            elem<OUT_DT>::store(out, qi * 256 + dim, oacc[jd][i] * inv_d * sigmoid(g));
+    for (int rt = 0; rt < 2; ++rt) {
+        const float d = dt[rt] + xrow[partner][rt][n];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * kb + i;
+            const float inv_d = 1.0f / __shfl(d, row, 64);
+            const int tok = t0 + 4 * pr + 2 * rt + (row >> 3);
+            if (tok >= T) continue;
+            const int h = kvh * 8 + (row & 7);
+            const size_t qi = static_cast<size_t>(tok) * 16 + h;
+#pragma unroll
+            for (int jd = 0; jd < 8; ++jd) {
+                const int dim = 128 * e + 16 * jd + n;
+                const float g = elem<IN_DT>::load(q_gate, qi * 512 + 256 + dim);
+                elem<OUT_DT>::store(out, qi * 256 + dim, oacc[rt][jd][i] * inv_d * sigmoid(g));
+            }
         }
     }
 }
