@@ -108,7 +108,12 @@ int qff_q4_dequant(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
  * (deltanet.metal:1897-1919) and qwen_gemv_q4_affine (deltanet.metal:816-861)
  * as dispatched for the q/k/v and out projections
  * (QwenQ4ActiveExpertStreamingRunner.swift:1024-1032, 1051-1074, 1152-1160);
- * batch > 1 covers batched decode and prefill projections. */
+ * batch > 1 covers batched decode and prefill projections. Up to 32 tokens
+ * the nibbles and x enter exactly (fp32 x as a bf16 hi + lo pair: fp32-class
+ * products); from 33 tokens the product runs on fp16 operands, W rounded
+ * once to fp16 and x to fp16 after a per-token power-of-two shift (relative
+ * error ~3e-4 of the exact product; x of any fp32 magnitude, dequantized
+ * weights of magnitude 2^-22 .. 255). */
 int qff_q4_matmul(qff_ctx* ctx, qff_stream_t stream, const uint32_t* w,
                   const void* scales, const void* biases, qff_dtype sb_dtype,
                   const void* x, qff_dtype x_dtype, void* y, qff_dtype y_dtype,
@@ -152,12 +157,13 @@ int qff_q4_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* pa
  *   y_p = xn W_p^T (+ residual_p),
  * without writing a normalised copy of x: in one pass over the weights up
  * to 16 tokens (two for 17-32, one per 16-token half; many-token batches
- * fold the norm into the group-sum pass their product already makes).
+ * fold the norm into the pass that forms their fp16 activations).
  * Replaces qwen_rmsnorm_f32 (deltanet.metal:18-53, weight used as is, mean
  * over the row) followed by the in-projections, as dispatched at
  * QwenQ4ActiveExpertStreamingRunner.swift:973-997 (DeltaNet layer) and
  * 1043-1074 (full-attention layer). norm_w [cols] of norm_dtype (F32 or
- * BF16). The product rounds x[m, c] * norm_w[c] to bf16 and applies the
+ * BF16). The product takes x[m, c] * norm_w[c] (exact as a bf16 hi + lo
+ * pair up to 32 tokens, as fp16 from 33 as in qff_q4_matmul) and applies the
  * per-token inverse RMS to the fp32 row sums. */
 int qff_q4_norm_matmul_parts(qff_ctx* ctx, qff_stream_t stream, const qff_q4_part* parts,
                              int nparts, qff_dtype sb_dtype, const void* x, qff_dtype x_dtype,
