@@ -290,14 +290,14 @@ def bench_c3(ctx, steps, warmup):
     out = torch.empty(T, 16, 256, dtype=torch.bfloat16, device="cuda")
 
     def step(i):
-        # q|gate, k and v share X: one multi-part product (one group-sum pass,
-        # one tiled launch over the three parts' row tiles)
+        # q|gate, k and v share X: one multi-part product (one x16 pass, one
+        # tiled launch over the three parts' row tiles)
         qff.q4_matmul_parts(ctx, wts, X, outs=(qg, k, v))
         qff.gqa_prefill(ctx, p, qg.view(T, 16, 512), k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out=out)
 
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
     kt, cnt = kernel_times(ctx, step, max(2, min(steps, 5)))
-    # one group-sum pass and one GEMM launch per step
+    # one x16 pass and one GEMM launch per step
     proj_ms = sum(v for k_, v in kt.items() if k_.startswith("q4_"))
     attn_ms = sum(v for k_, v in kt.items() if k_.startswith("gqa_prefill"))
     return {"ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "kernels_ms": kt,
