@@ -286,8 +286,10 @@ int qff_gqa_decode(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
  * current device; the split-KV partials live in a fixed device array of the
  * library (4096 slots, 33.8 MB, one per GPU, held until the process ends),
  * so batch is limited to 64 (QFF_ERR_WORKSPACE above). The first call on a
- * device looks up that array's address; no call allocates or frees. Calls
- * that overlap on one GPU (other streams or threads) race on the array. */
+ * device looks up that array's address (make it before a capture that must
+ * not see runtime queries; a failed look-up returns its status and is tried
+ * again by the next call); no call allocates or frees. Calls that overlap on
+ * one GPU (other streams or threads) race on the array. */
 int qff_gqa_decode_static(qff_stream_t stream, const qff_gqa_params* p, const void* q_gate,
                           const void* k_new, const void* v_new, qff_dtype in_dtype, void* k_cache,
                           void* v_cache, const int32_t* positions, void* out, qff_dtype out_dtype,

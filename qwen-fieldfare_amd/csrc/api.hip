@@ -41,17 +41,17 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.q4_fm = take(static_cast<size_t>(q4_xs_tokens(cfg)) * sizeof(float));
     L.q4_sk_part = take(static_cast<size_t>(kQ4SkSlots) * 16 * 64 * sizeof(float));
     const size_t TC = (T + 63) / 64 * 64;   // tokens rounded up to whole chunks
-    L.pf_o = take(TC * 4096 * sizeof(uint16_t));   // pre-norm DeltaNet prefill output, fp16
+    L.pf_o = take(TC * 4096 * sizeof(float));   // pre-norm DeltaNet prefill output, fp32
     L.sched = take(2 * kSchedSlots * sizeof(unsigned));
     L.dn_arrive = take(B * 16 * sizeof(unsigned));
     // DeltaNet prefill chunk records (deltanet_chunked.hip): per chunk and key
-    // head the K image (hi, lo) and Q blocks, per chunk and value head the T
-    // blocks (hi, lo), P blocks, gate factors and beta V
+    // head the K image and Q blocks (hi, lo), per chunk and value head the T
+    // and P blocks (hi, lo), gate factors and beta V
     const size_t NC = TC / 64;
     L.kimg = take(NC * 16 * 2 * 64 * 128 * sizeof(uint16_t));
-    L.qop = take(NC * 16 * 16 * 512 * sizeof(uint16_t));
+    L.qop = take(NC * 16 * 2 * 16 * 512 * sizeof(uint16_t));
     L.top = take(NC * 32 * 2 * 6 * 512 * sizeof(uint16_t));
-    L.pop = take(NC * 32 * 6 * 512 * sizeof(uint16_t));
+    L.pop = take(NC * 32 * 2 * 6 * 512 * sizeof(uint16_t));
     L.gates = take(NC * 32 * 4 * 64 * sizeof(float));
     L.bv = take(NC * 32 * 64 * 128 * sizeof(float));
     L.total = off;
@@ -165,7 +165,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     c->q4_fm = reinterpret_cast<float*>(base + L.q4_fm);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
     c->q4_sk_part = reinterpret_cast<float*>(base + L.q4_sk_part);
-    c->pf_o = u16(L.pf_o);
+    c->pf_o = reinterpret_cast<float*>(base + L.pf_o);
     c->sched = reinterpret_cast<unsigned*>(base + L.sched);
     c->num_cu = prop.multiProcessorCount;
     c->dn_arrive = reinterpret_cast<unsigned*>(base + L.dn_arrive);
@@ -360,18 +360,13 @@ int qff_deltanet_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_deltanet_p
     return QFF_OK;
 }
 
-static bool gqa_params_ok(const qff_gqa_params* p) {
-    return p && p->q_norm_w && p->k_norm_w && p->rotary_dim == 64 && p->rope_theta > 0.0f && p->eps >= 0.0f;
-}
-
 int qff_gqa_decode(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p, const void* q_gate,
                    const void* k_new, const void* v_new, qff_dtype in_dtype, void* k_cache,
                    void* v_cache, const int32_t* positions, void* out, qff_dtype out_dtype, int batch,
                    int max_ctx) {
     if (!ctx || !q_gate || !k_new || !v_new || !k_cache || !v_cache || !positions || !out)
         return QFF_ERR_INVALID_ARG;
-    if (!p || !p->q_norm_w || !p->k_norm_w) return QFF_ERR_INVALID_ARG;
-    if (!gqa_params_ok(p)) return QFF_ERR_UNSUPPORTED;
+    if (const int st = gqa_params_status(p)) return st;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return QFF_ERR_INVALID_ARG;
     if (batch <= 0 || max_ctx <= 0) return QFF_ERR_INVALID_ARG;
     if (batch > ctx->cfg.max_batch || max_ctx > ctx->cfg.max_ctx) return QFF_ERR_WORKSPACE;
@@ -384,8 +379,7 @@ int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p, 
                     const void* k, const void* v, qff_dtype in_dtype, void* k_cache, void* v_cache,
                     int start_pos, void* out, qff_dtype out_dtype, int T, int max_ctx) {
     if (!ctx || !q_gate || !k || !v || !k_cache || !v_cache || !out) return QFF_ERR_INVALID_ARG;
-    if (!p || !p->q_norm_w || !p->k_norm_w) return QFF_ERR_INVALID_ARG;
-    if (!gqa_params_ok(p)) return QFF_ERR_UNSUPPORTED;
+    if (const int st = gqa_params_status(p)) return st;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return QFF_ERR_INVALID_ARG;
     if (T <= 0 || start_pos < 0 || max_ctx <= 0) return QFF_ERR_INVALID_ARG;
     if (static_cast<long long>(start_pos) + T > max_ctx) return QFF_ERR_INVALID_ARG;

@@ -46,12 +46,14 @@
 // the A operand walks k in the same order; every operand block below is
 // written in it.
 //
-// Precision: the chain's products (X, U and the state update) run as bf16x3
-// on v_mfma_f32_16x16x32_bf16 (a b ~ a_hi b_hi + a_hi b_lo + a_lo b_hi,
-// ~2^-16 relative per product), which keeps the fp32 state within 1e-4 of
-// the sequential fp32 recurrence; the Gram products likewise. The output
-// products (Q S^T, P U) take fp16 operands (11 significant bits): they feed
-// only the bf16/fp32 outputs, through the gated RMSNorm.
+// Precision: every product runs as bf16x3 on v_mfma_f32_16x16x32_bf16
+// (a b ~ a_hi b_hi + a_hi b_lo + a_lo b_hi, ~2^-16 relative per product):
+// the chain's (X, U and the state update), which keeps the fp32 state within
+// 1e-4 of the sequential fp32 recurrence, the Gram products, and the output
+// products Q S^T and P U, whose fp32 result is the pre-norm output. Their
+// error is relative to the operands whatever their scale (bf16 has fp32's
+// exponent range), so tiny and huge value heads keep their precision
+// through the gated RMSNorm.
 #include <algorithm>
 
 #include "common.hpp"
@@ -69,9 +71,9 @@ constexpr float kLog2e = 1.44269504088896341f;
 
 // Workspace records (16-bit elements unless noted), per chunk c:
 constexpr int kKImg = 2 * kC * 128;   // per key head: K hi, lo, each [64][128] in the LDS image order
-constexpr int kQOp = 16 * kBlk;       // per key head: Q fp16, blocks (token tile tt, k step j), tt * 4 + j
+constexpr int kQOp = 2 * 16 * kBlk;   // per key head: Q hi, lo, blocks (token tile tt, k step j), tt * 4 + j
 constexpr int kTOp = 2 * 6 * kBlk;    // per value head: T hi, lo, blocks tblk(tt, j)
-constexpr int kPOp = 6 * kBlk;        // per value head: P fp16, blocks tblk(tt, j)
+constexpr int kPOp = 2 * 6 * kBlk;    // per value head: P hi, lo, blocks tblk(tt, j)
 constexpr int kGates = 4 * kC;        // per value head (floats): beta, beta e^G, e^{G_C - G}, e^G
 constexpr int kBV = kC * 128;         // per value head (floats): beta V, [16-channel block][token tile][lane][4]
 
@@ -234,8 +236,8 @@ constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
 constexpr int kOffK = 0;                          // K hi, lo
 constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T fp32 [2][64][65]
 constexpr int kOffA = 4 * kTile128;               // A fp32 [2][64][65]
-constexpr int kOffP = kOffA + 2 * kC * 65 * 4;    // P fp16 [2][64][72]
-constexpr int kOffS = kOffP + 2 * kC * kLP * 2;   // off-diagonal solve scratch [6][16][17] fp32
+constexpr int kOffP = kOffA + 2 * kC * 65 * 4;    // P hi, lo: bf16 [2][2][64][72]
+constexpr int kOffS = kOffP + 4 * kC * kLP * 2;   // off-diagonal solve scratch [6][16][17] fp32
 constexpr int kOffG = kOffS + 6 * 16 * 17 * 4;    // G [2][64], beta [2][64]
 constexpr int kLocalSmem = kOffG + 4 * kC * 4;
 static_assert(2 * kC * 65 * 4 <= 2 * kTile128, "T must fit the Q region");
@@ -276,7 +278,8 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     uint16_t* Ql = Qh + kC * kLD;
     float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [2][64][65]
     float* Am = reinterpret_cast<float*>(smem + kOffA);   // [2][64][65]
-    uint16_t* Pf = reinterpret_cast<uint16_t*>(smem + kOffP);   // [2][64][72]
+    uint16_t* Pfh = reinterpret_cast<uint16_t*>(smem + kOffP);   // [2][64][72]
+    uint16_t* Pfl = Pfh + 2 * kC * kLP;
     float* Scr = reinterpret_cast<float*>(smem + kOffS);
     float* Gs = reinterpret_cast<float*>(smem + kOffG);   // [hh][64]
     float* Bs = Gs + 2 * kC;                              // [hh][64]
@@ -432,16 +435,20 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
                     const int i = 16 * rt + 4 * kb + ii;
                     // e^{G_i - G_j}; for j > i the product is discarded by the select
                     const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * acc[0][cj][ii];
-                    if (role == 0)
+                    if (role == 0) {
                         Am[hh * kC * 65 + i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
-                    else
-                        Pf[hh * kC * kLP + i * kLP + j] = f32_to_f16(j <= i ? v : 0.0f);
+                    } else {
+                        uint16_t ph, pl;
+                        split_bf16(j <= i ? v : 0.0f, ph, pl);
+                        Pfh[hh * kC * kLP + i * kLP + j] = ph;
+                        Pfl[hh * kC * kLP + i * kLP + j] = pl;
+                    }
                 }
             }
         }
     }
     __syncthreads();
-    // ---- K image, Q blocks (fp16) and P blocks (fp16) out -----------------------
+    // ---- K image, Q blocks and P blocks (bf16 hi, lo) out ----------------------
     {
         uint16_t* ko = out.kimg + (static_cast<size_t>(c) * 16 + kh) * kKImg;
 #pragma unroll
@@ -461,28 +468,25 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             const int pc = t + kLocalThreads * i;   // [block tt * 4 + j][lane]
             const int blk = pc >> 6, l = pc & 63;
             const int row = 16 * (blk >> 2) + (l & 15), k0 = 32 * (blk & 3) + 4 * (l >> 4);
-            uint32_t w[4];
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const u32x2_t h2 = *reinterpret_cast<const u32x2_t*>(Qh + row * kLD + k0 + 16 * hf);
-                const u32x2_t l2 = *reinterpret_cast<const u32x2_t*>(Ql + row * kLD + k0 + 16 * hf);
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    w[2 * hf + e] = pack_f16x2(__uint_as_float(h2[e] << 16) + __uint_as_float(l2[e] << 16),
-                                               __uint_as_float(h2[e] & 0xffff0000u) +
-                                                   __uint_as_float(l2[e] & 0xffff0000u));
-            }
-            *reinterpret_cast<u32x4_t*>(qo + 8 * pc) = u32x4_t{w[0], w[1], w[2], w[3]};
+            const u32x2_t h0 = *reinterpret_cast<const u32x2_t*>(Qh + row * kLD + k0);
+            const u32x2_t h1 = *reinterpret_cast<const u32x2_t*>(Qh + row * kLD + k0 + 16);
+            const u32x2_t l0 = *reinterpret_cast<const u32x2_t*>(Ql + row * kLD + k0);
+            const u32x2_t l1 = *reinterpret_cast<const u32x2_t*>(Ql + row * kLD + k0 + 16);
+            *reinterpret_cast<u32x4_t*>(qo + 8 * pc) = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+            *reinterpret_cast<u32x4_t*>(qo + 16 * kBlk + 8 * pc) = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
         }
         for (int pc = t; pc < 2 * 6 * 64; pc += kLocalThreads) {   // [hh][block][lane]
             const int hh = pc / 384, blk = (pc >> 6) % 6, l = pc & 63;
             const int tt = blk < 2 ? blk : 2 + ((blk - 2) >> 1), j = blk < 2 ? 0 : (blk - 2) & 1;
             const int row = 16 * tt + (l & 15), k0 = 32 * j + 4 * (l >> 4);
-            const uint16_t* src = Pf + hh * kC * kLP + row * kLP + k0;
-            const u32x2_t x0 = *reinterpret_cast<const u32x2_t*>(src);
-            const u32x2_t x1 = *reinterpret_cast<const u32x2_t*>(src + 16);
-            uint16_t* po = out.pop + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kPOp;
-            *reinterpret_cast<u32x4_t*>(po + 8 * (pc % 384)) = u32x4_t{x0[0], x0[1], x1[0], x1[1]};
+            const int so = hh * kC * kLP + row * kLP + k0;
+            const u32x2_t h0 = *reinterpret_cast<const u32x2_t*>(Pfh + so);
+            const u32x2_t h1 = *reinterpret_cast<const u32x2_t*>(Pfh + so + 16);
+            const u32x2_t l0 = *reinterpret_cast<const u32x2_t*>(Pfl + so);
+            const u32x2_t l1 = *reinterpret_cast<const u32x2_t*>(Pfl + so + 16);
+            uint16_t* po = out.pop + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kPOp + 8 * (pc % 384);
+            *reinterpret_cast<u32x4_t*>(po) = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+            *reinterpret_cast<u32x4_t*>(po + 6 * kBlk) = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
         }
     }
     __syncthreads();   // Q consumed: its region holds T from here on
@@ -587,11 +591,10 @@ __device__ __forceinline__ f32x4_t mma_x3(u32x4_t ah, u32x4_t al, u32x4_t bh, u3
 // waves one chunk ahead) and the pieces the chain waves exchange.
 struct StateSmem {
     uint16_t kimg[2][kKImg];        // [stage] K hi | lo image
-    u32x4_t sop[4][2][64];          // [k step][hi, lo][lane] S^T bf16 B operands
-    u32x4_t sf[3][4][64];           // [chunk % 3][k step][lane] S^T fp16 B operands
+    u32x4_t st[3][4][2][64];        // [chunk % 3][k step][hi, lo][lane] S^T bf16 B operands
     uint32_t yop[2][2][64][4];      // [k step][hi, lo][lane][tile parity x 2] Y bf16 B operands
     uint32_t uop[2][2][64][4];      // [k step][hi, lo][lane][...] e^{G_C - G} U bf16 B operands
-    uint32_t uf[2][2][64][4];       // [chunk parity][k step][lane][...] U fp16 B operands
+    uint32_t uf[2][2][2][64][4];    // [chunk parity][k step][hi, lo][lane][...] U bf16 B operands
     unsigned sync;                  // arrivals of the chain waves at their own barriers
 };
 
@@ -620,29 +623,30 @@ __device__ __forceinline__ void chain_sync(unsigned* cnt, unsigned target, int l
 // beta V, gate factors) come from L2 into registers a chunk ahead, so only
 // the K image, which all four read, goes through LDS. Per chunk c:
 //   (a) X_w = K[tokens of tile w, :] S^T over all four k steps: A = K image
-//       rows from LDS, B = S^T operands (its own k step from registers, the
-//       others as published by their waves); Y_w = beta V - D X_w, split
-//       bf16 hi / lo and published as its half of Y's k-step operand;
+//       rows from LDS, B = the S^T operands the four waves published at the
+//       end of chunk c - 1; Y_w = beta V - D X_w, split bf16 hi / lo and
+//       published as its half of Y's k-step operand;
 //   [C1: the chain waves only]
-//   (b) U_w = T[tile w, :] Y (k steps j <= w / 2); U_w published as fp16 (for
-//       the output) and e^{G_C - G} U_w as bf16 hi / lo operand halves;
+//   (b) U_w = T[tile w, :] Y (k steps j <= w / 2); U_w and e^{G_C - G} U_w
+//       published as bf16 hi / lo operand halves (for the output and for
+//       (c));
 //   [C2: the chain waves only]
 //   (c) S^T[keys of w] = e^{G_C} S^T + K^T diag(e^{G_C - G}) U: A = K^T through
 //       the LDS transpose read of the image, B = the scaled U operands; the
-//       new S^T published as bf16 (next step) and fp16 (output) operands.
+//       new S^T published as bf16 hi / lo operands (slot (c + 1) % 3).
 //   [B0 of chunk c + 1: the whole workgroup]
 // Helper waves 4-7 (hw, token tile hw) meet the chain only at B0. Between
 // B0(c) and B0(c + 1): the output rows of chunk c - 1, O = diag(e^G) Q S^T +
-// P U on fp16 MFMAs (Q, P blocks in registers, loaded a chunk earlier; S^T
-// of chunk c - 1 stays published until the end of step c + 1, hence three
-// buffers) to the pre-norm output (fp16: it only feeds the gated RMSNorm);
-// a quarter of chunk c + 1's K image into the free stage from registers
-// loaded a chunk earlier; the loads of chunk c + 2.
+// P U, as bf16x3 products like the chain's (Q, P blocks in registers, loaded
+// a chunk earlier; S^T of chunk c - 1 stays published until the end of step
+// c + 1, hence three slots), stored as the fp32 pre-norm output that the
+// gated RMSNorm pass reads; a quarter of chunk c + 1's K image into the free
+// stage from registers loaded a chunk earlier; the loads of chunk c + 2.
 constexpr int kStateThreads = 512;
 
 __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qff_dn_bufs in,
                                                                       float* __restrict__ ssm_state,
-                                                                      uint16_t* __restrict__ po) {
+                                                                      float* __restrict__ po) {
     const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
     const int kh = 2 * xcd + (slot >> 4), h = 2 * kh + ((slot >> 3) & 1), cb = slot & 7;
     const int t = threadIdx.x, lane = t & 63;
@@ -660,12 +664,11 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
         f32x4_t sT[2];
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) sT[k2] = *reinterpret_cast<const f32x4_t*>(Sg + 16 * k2);
-        u32x4_t bh, bl;   // this wave's k step of the S^T operands
-        auto publish_state = [&](int par) {
+        auto publish_state = [&](int slot3) {
+            u32x4_t bh, bl;
             split8(sT[0], sT[1], bh, bl);
-            sm.sop[w][0][lane] = bh;
-            sm.sop[w][1][lane] = bl;
-            sm.sf[par][w][lane] = pack_f16x8(sT[0], sT[1]);
+            sm.st[slot3][w][0][lane] = bh;
+            sm.st[slot3][w][1][lane] = bl;
         };
         publish_state(0);
         // this wave's own chunk operands, loaded from L2 a chunk ahead: T
@@ -691,7 +694,7 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             r.gam = gg[3 * kC + kC - 1];
         };
         auto step = [&](int c, const ChainIn& ci, ChainIn& next) {
-            const int s = c & 1;
+            const int s = c & 1, s3 = c % 3;
             __syncthreads();   // B0(c): stage s holds chunk c; S_c published
             load_in(next, min(c + 1, nch - 1));
             const uint16_t* kh_ = sm.kimg[s];
@@ -703,8 +706,8 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
                 const int o = kimg_off(16 * w + n, 4 * j + g);
                 ka[j][0] = *reinterpret_cast<const u32x4_t*>(kh_ + o);
                 ka[j][1] = *reinterpret_cast<const u32x4_t*>(kl_ + o);
-                sb[j][0] = sm.sop[j][0][lane];
-                sb[j][1] = sm.sop[j][1][lane];
+                sb[j][0] = sm.st[s3][j][0][lane];
+                sb[j][1] = sm.st[s3][j][1][lane];
             }
             f32x4_t xa = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -729,11 +732,12 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
                                 *reinterpret_cast<const u32x4_t*>(sm.yop[j][1][lane]), ua);
             }
             {
-                const f32x4_t e4 = ci.e4;
-                *reinterpret_cast<u32x2_t*>(sm.uf[s][w >> 1][lane] + 2 * (w & 1)) =
-                    u32x2_t{pack_f16x2(ua[0], ua[1]), pack_f16x2(ua[2], ua[3])};
-                const f32x4_t us = ua * e4;
                 uint32_t h0, l0, h1, l1;
+                split_bf16x2(ua[0], ua[1], h0, l0);
+                split_bf16x2(ua[2], ua[3], h1, l1);
+                *reinterpret_cast<u32x2_t*>(sm.uf[s][w >> 1][0][lane] + 2 * (w & 1)) = u32x2_t{h0, h1};
+                *reinterpret_cast<u32x2_t*>(sm.uf[s][w >> 1][1][lane] + 2 * (w & 1)) = u32x2_t{l0, l1};
+                const f32x4_t us = ua * ci.e4;
                 split_bf16x2(us[0], us[1], h0, l0);
                 split_bf16x2(us[2], us[3], h1, l1);
                 *reinterpret_cast<u32x2_t*>(sm.uop[w >> 1][0][lane] + 2 * (w & 1)) = u32x2_t{h0, h1};
@@ -792,9 +796,9 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             u32x4_t k[8];
         } hs;
         struct Out {
-            u32x4_t q[4];   // Q blocks (hw, j)
-            u32x4_t p[2];   // P blocks pb, pb + 1
-            f32x4_t eg;     // e^G of the tile's tokens
+            u32x4_t q[4][2];   // Q blocks (hw, j), hi / lo
+            u32x4_t p[2][2];   // P blocks pb, pb + 1, hi / lo
+            f32x4_t eg;        // e^G of the tile's tokens
         } ho;
         // every helper load is unconditional (a load under a divergent branch
         // makes the compiler wait for all outstanding loads at the join)
@@ -809,27 +813,40 @@ __global__ __launch_bounds__(kStateThreads) void dn_chunk_state_kernel(int T, qf
             for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4_t*>(kd + i * kBlk + 8 * lane) = hs.k[i];
         };
         auto load_out = [&](int cc) {
-            const uint16_t* qg = in.qop + (static_cast<size_t>(cc) * 16 + kh) * kQOp + 4 * hw * kBlk;
+            const uint16_t* qg = in.qop + (static_cast<size_t>(cc) * 16 + kh) * kQOp + 4 * hw * kBlk + 8 * lane;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ho.q[i] = *reinterpret_cast<const u32x4_t*>(qg + i * kBlk + 8 * lane);
-            const uint16_t* pg = in.pop + (static_cast<size_t>(cc) * 32 + h) * kPOp + pb * kBlk;
+            for (int i = 0; i < 4; ++i) {
+                ho.q[i][0] = *reinterpret_cast<const u32x4_t*>(qg + i * kBlk);
+                ho.q[i][1] = *reinterpret_cast<const u32x4_t*>(qg + 16 * kBlk + i * kBlk);
+            }
+            const uint16_t* pg = in.pop + (static_cast<size_t>(cc) * 32 + h) * kPOp + pb * kBlk + 8 * lane;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) ho.p[i] = *reinterpret_cast<const u32x4_t*>(pg + i * kBlk + 8 * lane);
+            for (int i = 0; i < 2; ++i) {
+                ho.p[i][0] = *reinterpret_cast<const u32x4_t*>(pg + i * kBlk);
+                ho.p[i][1] = *reinterpret_cast<const u32x4_t*>(pg + 6 * kBlk + i * kBlk);
+            }
             ho.eg = *reinterpret_cast<const f32x4_t*>(in.gates + (static_cast<size_t>(cc) * 32 + h) * kGates + 3 * kC +
                                                       16 * hw + 4 * g);
         };
+        // the output rows of chunk cc: lane (n, g) holds state row 16 cb + n of
+        // tokens cc * 64 + 16 hw + 4 g + i
         auto output = [&](int cc) {
-            const int par = cc & 1;
+            const int par = cc & 1, s3 = cc % 3;
             f32x4_t o = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o = mfma_16x16x32_f16(ho.q[j], sm.sf[cc % 3][j][lane], o);
+            for (int j = 0; j < 4; ++j)
+                o = mma_x3(ho.q[j][0], ho.q[j][1], sm.st[s3][j][0][lane], sm.st[s3][j][1][lane], o);
             o *= ho.eg;
-            o = mfma_16x16x32_f16(ho.p[0], *reinterpret_cast<const u32x4_t*>(sm.uf[par][0][lane]), o);
-            if (hw >= 2) o = mfma_16x16x32_f16(ho.p[1], *reinterpret_cast<const u32x4_t*>(sm.uf[par][1][lane]), o);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (j == 0 || hw >= 2)
+                    o = mma_x3(ho.p[j][0], ho.p[j][1], *reinterpret_cast<const u32x4_t*>(sm.uf[par][j][0][lane]),
+                               *reinterpret_cast<const u32x4_t*>(sm.uf[par][j][1][lane]), o);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tok = cc * kC + 16 * hw + 4 * g + i;
-                if (tok < T) po[static_cast<size_t>(tok) * 4096 + 128 * h + 16 * cb + n] = f32_to_f16(o[i]);
+                if (tok < T) po[static_cast<size_t>(tok) * 4096 + 128 * h + 16 * cb + n] = o[i];
             }
         };
         load_stage(0);

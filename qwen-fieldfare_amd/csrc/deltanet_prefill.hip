@@ -6,7 +6,7 @@
 // computes the same result for a whole sequence:
 //   chunked    conv1d + SiLU, L2 norms, gates and the chunked WY form of the
 //              gated delta rule (deltanet_chunked.hip), pre-norm outputs to
-//              workspace (fp16);
+//              workspace (fp32);
 //   norm       gated RMSNorm of every (token, value head) output row, and
 //              (32 extra workgroups of the same launch) the conv state after
 //              the last token.
@@ -60,11 +60,11 @@ template <int DT> __device__ __forceinline__ void store8(void* p, size_t i, cons
 }
 
 // Gated RMSNorm (QwenDeltaNetKernel.swift:127-151: o * rsqrt(mean(o^2) + eps)
-// * w * silu(z)) of the pre-norm outputs the state pass wrote.
+// * w * silu(z)) of the fp32 pre-norm outputs the state pass wrote.
 // grid (T + 32), 256 threads: thread -> value head t/8, rows 16*(t%8) .. +15;
 // the 32 workgroups past the tokens write the conv state after the last token.
 template <int IN_DT, int OUT_DT>
-__global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const uint16_t* __restrict__ po,
+__global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const float* __restrict__ po,
                                                               const void* __restrict__ z,
                                                               const float* __restrict__ norm_w, float eps,
                                                               void* __restrict__ out, int T,
@@ -86,8 +86,8 @@ __global__ __launch_bounds__(256) void dn_prefill_norm_kernel(const uint16_t* __
     const int r0 = 16 * (t & 7);
     const size_t base = static_cast<size_t>(tok) * 4096 + (t >> 3) * 128 + r0;
     float o[2][8], zz[2][8], ss = 0.0f;
-    load8<2>(po, base, o[0]);
-    load8<2>(po, base + 8, o[1]);
+    load8<0>(po, base, o[0]);
+    load8<0>(po, base + 8, o[1]);
     load8<IN_DT>(z, base, zz[0]);
     load8<IN_DT>(z, base + 8, zz[1]);
 #pragma unroll

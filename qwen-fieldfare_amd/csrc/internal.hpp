@@ -19,9 +19,9 @@ struct qff_prof_record {
 // each array split into bf16 hi / lo halves.
 struct qff_dn_bufs {
     uint16_t* kimg;   // per (chunk, key head): K hi, lo [64][128] in the state pass's LDS image order
-    uint16_t* qop;    // per (chunk, key head): Q fp16, 16 MFMA operand blocks
+    uint16_t* qop;    // per (chunk, key head): Q hi, lo, 16 MFMA operand blocks each
     uint16_t* top;    // per (chunk, value head): T = (I + A)^-1 hi, lo, 6 operand blocks each
-    uint16_t* pop;    // per (chunk, value head): P fp16, 6 operand blocks
+    uint16_t* pop;    // per (chunk, value head): P hi, lo, 6 operand blocks each
     float* gates;     // per (chunk, value head): beta, beta e^G, e^{G_C - G}, e^G [4][64]
     float* bv;        // per (chunk, value head): beta V [64][128] in the state pass's lane order
 };
@@ -46,9 +46,9 @@ struct qff_ctx {
     // Decode-batch Q4 products split over 512-column slices: per (row tile,
     // slice) the partial [16 tokens][64 rows], kQ4SkSlots of them.
     float* q4_sk_part = nullptr;
-    // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] and
-    // chunk intermediates.
-    uint16_t* pf_o = nullptr;
+    // DeltaNet prefill: pre-norm outputs [T rounded up to 64][32][128] fp32
+    // and chunk intermediates.
+    float* pf_o = nullptr;
     qff_dn_bufs dn{};
     // DeltaNet decode: per (sequence, key head) arrival counters [max_batch][16],
     // zero between launches (the second arrival resets its counter).
@@ -108,6 +108,18 @@ struct RopeFreqs {
     float f[32];
 };
 RopeFreqs rope_freqs(float theta);
+
+// Status of a full-attention parameter block: the norm weights present, a
+// finite positive softmax scale, RoPE theta and eps (invalid argument
+// otherwise); rotary_dim 64 is the only rotation built (unsupported otherwise).
+inline int gqa_params_status(const qff_gqa_params* p) {
+    if (!p || !p->q_norm_w || !p->k_norm_w) return QFF_ERR_INVALID_ARG;
+    if (!(p->scale > 0.0f) || !(p->scale < __builtin_huge_valf())) return QFF_ERR_INVALID_ARG;
+    if (!(p->rope_theta > 0.0f) || !(p->rope_theta < __builtin_huge_valf()) || !(p->eps >= 0.0f))
+        return QFF_ERR_INVALID_ARG;
+    if (p->rotary_dim != 64) return QFF_ERR_UNSUPPORTED;
+    return QFF_OK;
+}
 
 inline bool dtype_ok(qff_dtype d, bool allow_f16 = false) {
     return d == QFF_F32 || d == QFF_BF16 || (allow_f16 && d == QFF_F16);

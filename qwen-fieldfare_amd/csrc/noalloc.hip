@@ -6,9 +6,9 @@
 // qff_gqa_decode keeps in its context's workspace live here in one
 // file-scope device array, `scratch`, of kSlots slots. Each GPU the library
 // runs on holds its own copy of it until the process ends. Its device
-// address on the current device is looked up once per device with
-// hipGetSymbolAddress on the first call there and cached; kernels only ever
-// see that address. Nothing here calls hipMalloc, hipFree or any allocating
+// address on the current device is looked up with hipGetSymbolAddress on
+// the first call there that succeeds in doing so, and cached; kernels only
+// ever see that address. Nothing here calls hipMalloc, hipFree or any allocating
 // routine.
 //
 // Every call on one GPU shares that GPU's array and it keeps the last
@@ -36,32 +36,29 @@ namespace {
 std::mutex g_mu;
 float* g_ptr[kMaxDevices];      // scratch's device address, per device (null until looked up)
 int g_num_cu[kMaxDevices];
-int g_status[kMaxDevices];      // 0: not looked up; 1: ready; < 0: qff_status of a failed set-up
 }  // namespace
 
-// scratch's address and CU count on the current device, set up on the
-// first call there.
+// scratch's address and CU count on the current device. Only a successful
+// set-up is cached: a failed one (a transient runtime error, a call refused
+// while the stream is being captured) returns its status and is tried again
+// on the next call.
 static int static_scratch(float** ptr, int* num_cu) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return QFF_ERR_HIP;
     if (dev < 0 || dev >= kMaxDevices) return QFF_ERR_UNSUPPORTED;
     std::lock_guard<std::mutex> lock(g_mu);
-    if (g_status[dev] == 0) {
+    if (!g_ptr[dev]) {
         hipDeviceProp_t prop;
         void* p = nullptr;
-        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
-            g_status[dev] = QFF_ERR_HIP;
-        } else if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-            g_status[dev] = QFF_ERR_UNSUPPORTED;
-        } else if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
-            g_status[dev] = QFF_ERR_HIP;
-        } else {
-            g_ptr[dev] = static_cast<float*>(p);
-            g_num_cu[dev] = prop.multiProcessorCount;
-            g_status[dev] = 1;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QFF_ERR_HIP;
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return QFF_ERR_UNSUPPORTED;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();   // leave no sticky error for the caller's next call
+            return QFF_ERR_HIP;
         }
+        g_num_cu[dev] = prop.multiProcessorCount;
+        g_ptr[dev] = static_cast<float*>(p);
     }
-    if (g_status[dev] != 1) return g_status[dev];
     *ptr = g_ptr[dev];
     *num_cu = g_num_cu[dev];
     return QFF_OK;
@@ -76,8 +73,7 @@ extern "C" int qff_gqa_decode_static(qff_stream_t stream, const qff_gqa_params* 
                                      void* v_cache, const int32_t* positions, void* out, qff_dtype out_dtype,
                                      int batch, int max_ctx) {
     if (!q_gate || !k_new || !v_new || !k_cache || !v_cache || !positions || !out) return QFF_ERR_INVALID_ARG;
-    if (!p || !p->q_norm_w || !p->k_norm_w) return QFF_ERR_INVALID_ARG;
-    if (p->rotary_dim != 64 || !(p->rope_theta > 0.0f) || !(p->eps >= 0.0f)) return QFF_ERR_UNSUPPORTED;
+    if (const int st = gqa_params_status(p)) return st;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return QFF_ERR_INVALID_ARG;
     if (batch <= 0 || max_ctx <= 0) return QFF_ERR_INVALID_ARG;
     if (batch > kStaticMaxBatch) return QFF_ERR_WORKSPACE;

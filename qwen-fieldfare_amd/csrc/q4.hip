@@ -918,7 +918,8 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
 //   y[m, r]   = f_m sum_c W16 x16,     f_m = 2^(e_m - 8) (times the token's
 //                                      inverse RMS with the norm)
 // The power-of-two shifts are exact and keep both operands inside fp16's
-// normal range: x' of any fp32 magnitude, W of magnitude 2^-22 .. 255. Both
+// normal range: x' of any fp32 magnitude down to 2^-141 (the shift is at
+// most 2^127), W of magnitude 2^-22 .. 255. Both
 // operands carry 11 significant bits (the bf16 activations of the factored
 // form carried 8), so the product is the fp32 dot product to a few 2^-12
 // relative; the bias is part of every W16 element, so no group sums are
@@ -985,8 +986,11 @@ __global__ __launch_bounds__(256) void q4_x16_kernel(const void* __restrict__ x,
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    // max |x'| in [2^(E-1), 2^E): x' 2^-(E-14) stays below 2^14
-    const int e = mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 14 : 0;
+    // max |x'| in [2^(E-1), 2^E): x' 2^-(E-14) stays below 2^14. e >= -127
+    // keeps 2^-e a finite fp32 for the smallest tokens (fp32 subnormals
+    // included): their x16 then sits below 2^14 but stays in fp16's normal
+    // range down to |x'| = 2^-141, and f_m >= 2^-135 keeps 14 bits.
+    const int e = mx > 0.0f ? max(__builtin_amdgcn_frexp_expf(mx) - 14, -127) : 0;
     const float p = ldexpf(1.0f, -e);
 #pragma unroll
     for (int i = 0; i < kMaxB; ++i) {

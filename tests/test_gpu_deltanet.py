@@ -111,6 +111,82 @@ def test_deltanet_prefill_matches_sequential_oracle(hip, T):
     assert state_rel_err(to_np(ssm), ref_s) <= 1e-4
 
 
+def _prefill_vs_oracle(p, inp, T, max_tokens=256):
+    import qff
+    ref_o, ref_c, ref_s = O.deltanet_sequence(O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"]),
+                                              inp["a"], inp["b"], p["a_log"], p["dt_bias"],
+                                              p["conv_w"], p["norm_w"], inp["conv_state"],
+                                              inp["ssm_state"])
+    ctx = qff.Context(max_batch=1, max_prefill_tokens=max_tokens)
+    conv = f32_tensor(inp["conv_state"])
+    ssm = f32_tensor(inp["ssm_state"])
+    out = qff.deltanet_prefill(ctx, _params_gpu(p), bf16_tensor(inp["qkv"]), bf16_tensor(inp["z"]),
+                               f32_tensor(inp["a"]), f32_tensor(inp["b"]), conv, ssm,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    return to_np(out), ref_o, to_np(conv), ref_c, to_np(ssm), ref_s
+
+
+def _row_rel_err(got, ref, T):
+    """Error of every (token, value head) row over that row's RMS."""
+    g3, r3 = got.reshape(T, 32, 128).astype(np.float64), ref.reshape(T, 32, 128).astype(np.float64)
+    rms = np.sqrt(np.mean(r3 ** 2, axis=2))
+    return np.max(np.abs(g3 - r3), axis=2) / (rms + 1e-300)
+
+
+@pytest.mark.parametrize("vscale", [2.0 ** -12, 2.0 ** 20])
+def test_deltanet_prefill_value_scales(hip, vscale):
+    """v channels scaled by 2^-12 and by 2^20 (q, k and the gates unchanged),
+    from zero state, against the same inputs at scale 1: the output rows are
+    formed and normalised in fp32-class arithmetic whose error is relative to
+    the operands, so each row's error over its own RMS is no worse at either
+    scale than at scale 1 (an fp16 intermediate would lose relative precision
+    among its subnormals at 2^-12 and overflow at 2^20). The worst rows at
+    every scale are those whose size comes from a nearly cancelled q.k (the
+    Gram product's error is relative to |q||k|, ~1e-3 of the row there)."""
+    T = 200
+    print(f"deltanet_prefill v scale {vscale}", flush=True)
+    p = synth.deltanet_params()
+    base = synth.deltanet_prefill_inputs(T, seed=777)
+    got1, ref1, _, _, _, _ = _prefill_vs_oracle(p, base, T)
+    inp = {k: v.copy() for k, v in base.items()}
+    v = O.bf16_to_f32(inp["qkv"][:, 4096:]) * np.float32(vscale)
+    inp["qkv"][:, 4096:] = O.f32_to_bf16(v)
+    got, ref, conv, ref_c, ssm, ref_s = _prefill_vs_oracle(p, inp, T)
+    assert np.all(np.isfinite(got))
+    assert_f32_output_close(got, ref)
+    e1, es = _row_rel_err(got1, ref1, T), _row_rel_err(got, ref, T)
+    print(f"row errors / RMS: scale 1 median {np.median(e1):.3g} max {e1.max():.3g}; "
+          f"scale {vscale} median {np.median(es):.3g} max {es.max():.3g}", flush=True)
+    assert np.median(es) <= 2 * np.median(e1) + 1e-6
+    assert es.max() <= 2 * e1.max() + 1e-5
+    assert np.array_equal(conv, ref_c)
+    assert state_rel_err(ssm, ref_s) <= 1e-4
+
+
+def test_deltanet_prefill_first_token_q_nearly_orthogonal_to_k(hip):
+    """T = 1 from zero state with q nearly orthogonal to k in every key head:
+    the output is beta (q.k) v / sqrt(128), with q.k ~ 1e-4 of |q||k|, so the
+    pre-norm rows are four orders of magnitude below their usual size."""
+    T = 1
+    p = synth.deltanet_params()
+    inp = synth.deltanet_prefill_inputs(T, seed=778)
+    x = O.bf16_to_f32(inp["qkv"]).copy()
+    w3 = p["conv_w"][:, 3]
+    for kh in range(16):
+        q0, k0 = kh * 128, 2048 + kh * 128
+        # k = silu(w3 x) along key 127 only; q has a tiny component there
+        x[0, k0:k0 + 127] = 0.0
+        x[0, k0 + 127] = 2.0 / w3[k0 + 127]
+        x[0, q0 + 127] = 1e-3 / w3[q0 + 127]
+    inp["qkv"] = O.f32_to_bf16(x)
+    got, ref, conv, ref_c, ssm, ref_s = _prefill_vs_oracle(p, inp, T)
+    assert np.all(np.isfinite(got))
+    assert_f32_output_close(got, ref)
+    assert np.array_equal(conv, ref_c)
+    assert state_rel_err(ssm, ref_s) <= 1e-4
+
+
 def test_deltanet_prefill_config1_full_length(hip):
     """Config 1 at its full size: T = 4096 from zero state, against the
     4096-step sequential fp32 oracle (a few seconds of CPU)."""

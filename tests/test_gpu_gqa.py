@@ -85,18 +85,26 @@ def test_gqa_decode_config4_shape(hip):
     _run_case(hip, lengths, 32768, out_dtype=torch.bfloat16, seed=16)
 
 
-@pytest.mark.parametrize("B", [3, 10])
+@pytest.mark.parametrize("B", [3, 10, 65, 130])
 def test_gqa_decode_position_outside_cache(hip, B):
     """A sequence whose position lies outside the cache (negative or >=
     max_ctx) gets NaN outputs and leaves its cache rows untouched; the other
     sequences of the batch are unaffected (both combine shapes: B <= 8 and
-    B > 8)."""
+    B > 8). Batches above 64 take the split's multi-pass path (the
+    per-64 sums and the prefix carried across blocks of 64 sequences), with
+    such zero-work sequences on both sides of the block boundaries."""
     import qff
     max_ctx = 512
     print(f"gqa_decode invalid positions B={B}", flush=True)
     p = synth.gqa_params()
-    inp = synth.gqa_decode_inputs(B, max_ctx, seed=70 + B, lengths=[200 + 30 * i for i in range(B)])
+    if B <= 10:
+        lengths = [200 + 30 * i for i in range(B)]
+    else:
+        lengths = list(np.random.default_rng(B).integers(1, max_ctx + 1, B))
+    inp = synth.gqa_decode_inputs(B, max_ctx, seed=70 + B, lengths=lengths)
     bad = {1: -1, B - 1: max_ctx}
+    if B > 64:
+        bad.update({63: -5, 64: max_ctx + 7, 65 % B: 1 << 30, B // 2: -1})
     positions = inp["positions"].copy()
     for s_, v in bad.items():
         positions[s_] = v
@@ -249,6 +257,18 @@ def test_gqa_rejects_bad_calls(hip):
     with pytest.raises(qff.QffError) as e:       # batch above max_batch
         qff.gqa_decode(ctx, pg, qg, kn, kn, kc3, kc3.clone(), pos)
     assert e.value.status == -4
+    # softmax scale and RoPE theta must be finite and positive
+    kc2 = torch.zeros(2, max_ctx, 2, 256, dtype=torch.bfloat16, device=DEV)
+    for bad in (0.0, -1.0 / 16, float("nan"), float("inf")):
+        with pytest.raises(qff.QffError) as e:
+            qff.gqa_decode(ctx, pg, qg[:2], kn[:2], kn[:2], kc2, kc2.clone(), pos[:2], scale=bad)
+        assert e.value.status == -1
+        with pytest.raises(qff.QffError) as e:
+            qff.gqa_prefill(ctx, pg, qg[:2], kn[:2], kn[:2], kc, vc, 0, scale=bad)
+        assert e.value.status == -1
+    with pytest.raises(qff.QffError) as e:
+        qff.gqa_decode(ctx, pg, qg[:2], kn[:2], kn[:2], kc2, kc2.clone(), pos[:2], theta=float("inf"))
+    assert e.value.status == -1
 
 
 def test_gqa_decode_f32_inputs(hip):

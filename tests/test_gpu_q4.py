@@ -148,6 +148,10 @@ def test_q4_gemm_token_magnitudes(hip, xdt):
     x = (rng.standard_normal((batch, cols)) * scale[:, None]).astype(np.float32)
     x[5] = 0.0
     x[7, ::3] *= 1e-4   # a wide spread inside one token
+    # the smallest tokens: 2^-120, and one made of fp32 subnormals (2^-136)
+    scale[9], scale[11] = 2.0 ** -120, 2.0 ** -136
+    x[9] = (rng.standard_normal(cols) * scale[9]).astype(np.float32)
+    x[11] = (rng.standard_normal(cols) * scale[11]).astype(np.float32)
     if xdt == "bf16":
         x = O.round_bf16(x)
     xt = bf16_tensor(O.f32_to_bf16(x)) if xdt == "bf16" else f32_tensor(x)
@@ -159,7 +163,11 @@ def test_q4_gemm_token_magnitudes(hip, xdt):
     assert np.all(y[5] == 0.0)
     for m in range(batch):
         if m != 5:
-            assert _rel(y[m], ref[m]) <= 1e-3, f"token {m} (scale 2^{np.log2(scale[m]):.1f})"
+            # compared at unit scale, so the smallest tokens' errors are not
+            # lost below the helper's 1e-30 floor
+            u = 1.0 / scale[m]
+            assert _rel(y[m].astype(np.float64) * u, ref[m] * u) <= 1e-3, \
+                f"token {m} (scale 2^{np.log2(scale[m]):.1f})"
 
 
 def test_q4_rejects_bad_shapes(hip):

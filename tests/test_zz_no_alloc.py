@@ -63,3 +63,46 @@ def test_gqa_decode_static_rejects_oversized_batch(hip):
     out = torch.zeros(B, 16, 256, device=DEV)
     assert _call_static(prm, qg, kn, kn, kc, kc.clone(), pos, out, B, max_ctx) == -4
     assert _call_static(prm, qg, kn, kn, kc, kc.clone(), pos, out, 0, max_ctx) == -1
+
+
+def test_gqa_decode_static_graph_replay(hip):
+    """The static entry point captured in a HIP graph (after one eager call,
+    which resolves the array's address) and replayed three times, with eager
+    work and synchronisations between the replays: every replay equals the
+    context entry point's result bit for bit, and the appended cache rows too."""
+    import qff
+    from qff._lib import GqaParams
+    p = {k: f32_tensor(v) for k, v in synth.gqa_params().items()}
+    prm = GqaParams(p["q_norm_w"].data_ptr(), p["k_norm_w"].data_ptr(), 1e7, 64, 1.0 / 16, 1e-6)
+    B, max_ctx = 4, 4096
+    print(f"gqa_decode_static graph replay B={B} max_ctx={max_ctx}", flush=True)
+    # 32 x 2 x 64 = 4096 slots: the same chunk cap as the static array
+    ctx = qff.Context(max_batch=32, max_ctx=max_ctx, max_prefill_tokens=1)
+    inp = synth.gqa_decode_inputs(B, max_ctx, seed=31, lengths=[4096, 1, 777, 3000])
+    qg, kn, vn = (bf16_tensor(inp[k]) for k in ("q_gate", "k_new", "v_new"))
+    pos = torch.from_numpy(inp["positions"]).to(DEV)
+    kc_a, vc_a = bf16_tensor(inp["k_cache"]), bf16_tensor(inp["v_cache"])
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    ref = qff.gqa_decode(ctx, p, qg, kn, vn, kc_a, vc_a, pos, out_dtype=torch.float32)
+    out = torch.full((B, 16, 256), float("nan"), device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert _call_static(prm, qg, kn, vn, kc_b, vc_b, pos, out, B, max_ctx) == 0   # eager, sets up
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        assert _call_static(prm, qg, kn, vn, kc_b, vc_b, pos, out, B, max_ctx) == 0
+    for r in range(3):
+        out.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device=DEV).sum()   # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        assert torch.equal(out, ref), f"replay {r}"
+        assert torch.equal(kc_a.view(torch.int16), kc_b.view(torch.int16))
+        assert torch.equal(vc_a.view(torch.int16), vc_b.view(torch.int16))
+    ctx.close()
