@@ -433,15 +433,41 @@ def _host_info():
     return {"host_cores": len(os.sched_getaffinity(0)), "nproc": os.cpu_count(), "cpu_model": model}
 
 
+def _filled(shape, rng):
+    """fp32 array of `shape` filled with a repeated random block (timing data:
+    the baselines have no data-dependent control flow, and drawing GBs of
+    normals would cost more than the timed work)."""
+    import numpy as np
+    a = np.empty(shape, np.float32)
+    flat = a.reshape(-1)
+    blk = rng.standard_normal(1 << 16).astype(np.float32)
+    for o in range(0, flat.size, blk.size):
+        n = min(blk.size, flat.size - o)
+        flat[o:o + n] = blk[:n]
+    return a
+
+
 def cpu_baselines():
     """The reference's CPU algorithms (oracle/cpu_baseline.c: the oracle's
     fp32 functions in the reference's loop order with OpenMP drivers, equal
-    to the sequential oracle bit for bit), compiled here with gcc -O3
-    -march=native. Config 1: a 1024-token sample of the config-1 sequence on
-    one thread, the whole 4096-token sequence on all cores. Config 2: the
-    batch-8 decode at context 8192 with random lengths (the split-KV
-    attention of attention.metal:134-224, 342-377). 3 warm-ups, median of
-    10 runs each."""
+    to the oracle bit for bit, tests/test_oracle_deltanet.py and
+    tests/test_oracle_cpu_baseline.py), compiled here with gcc -O3
+    -march=native, one thread and all cores, 3 warm-ups then the median of
+    10 runs (3 for the multi-second samples). Per configuration:
+      c0  one DeltaNet decode step (the config-0 inputs);
+      c1  the 4096-token sequence (all cores) and its first 1024 tokens (one
+          thread), token by token;
+      c2  split-KV decode attention at batch 1, 8 and 32, context 8192 with
+          random lengths (attention.metal:134-224, 342-377);
+      c3  the reference's token-by-token prefill of the full-attention layer
+          (Q4 projections, norms, RoPE, attention over 0..t, gate) on tokens
+          4064-4095 of the 8192-token sequence, whose cost is the sequence's
+          average per token (attention grows linearly with the position);
+      c4  one DeltaNet layer and one full-attention layer of the stack
+          (input norm, Q4 in-projection, core, Q4 out-projection +
+          residual) at the step's batch and context, composed as 30 + 10
+          layers.
+    Returns {config key: baseline}."""
     import numpy as np
     from oracle import cpu_baseline as CB
     from oracle import oracle as O
@@ -452,7 +478,11 @@ def cpu_baselines():
     build = "gcc -O3 -march=native -fopenmp -ffp-contract=off" if path else "portable build (-march=x86-64-v2)"
     info = _host_info()
     threads = min(info["host_cores"], int(os.environ.get("OMP_NUM_THREADS", info["host_cores"]) or 1))
+    med = "median of 10 after 3 warm-ups"
+    out = {}
     p = synth.deltanet_params()
+
+    # config 1 and config 0
     inp = synth.deltanet_prefill_inputs(4096)
     qkv, z = O.bf16_to_f32(inp["qkv"]), O.bf16_to_f32(inp["z"])
 
@@ -461,25 +491,91 @@ def cpu_baselines():
                                            inp["ssm_state"], threads=th)
     t1 = _median_time(dn(1024, 1))
     tn = _median_time(dn(4096, threads))
-    rng = np.random.default_rng(1008)
-    B, ctxlen = 8, 8192
-    lengths = rng.integers(1, ctxlen + 1, B).astype(np.int32)
-    q = rng.standard_normal((B, 16, 256)).astype(np.float32)
-    K = rng.standard_normal((B, ctxlen, 2, 256)).astype(np.float32)
-    V = rng.standard_normal((B, ctxlen, 2, 256)).astype(np.float32)
-    a1 = _median_time(lambda: CB.attention_decode(L, q, K, V, lengths, threads=1))
-    an = _median_time(lambda: CB.attention_decode(L, q, K, V, lengths, threads=threads))
     c1 = {"value": 4096 / tn, "unit": "tokens/s", "cores": threads, "kind": "port",
           "sample": f"config 1, the 4096-token sequence from zero state through the DeltaNet layer core "
-                    f"(oracle/cpu_baseline.c, {build}), {threads} threads; median of 10 after 3 warm-ups",
+                    f"(oracle/cpu_baseline.c, {build}), {threads} threads; {med}",
           "single_thread": {"value": 1024 / t1, "unit": "tokens/s", "cores": 1,
                             "sample": "the first 1024 tokens of the same sequence, 1 thread"}}
-    c2 = {"value": B / an, "unit": "tokens/s", "cores": threads, "kind": "port",
-          "sample": f"config 2 batch 8, context 8192, lengths {lengths.tolist()}: split-KV decode "
-                    f"attention of 16 q heads per sequence, {threads} threads; median of 10 after 3 warm-ups",
-          "single_thread": {"value": B / a1, "unit": "tokens/s", "cores": 1}}
     c1.update(info)
-    return c1, c2
+    out["c1_deltanet_prefill_t4096"] = c1
+    d0 = synth.deltanet_decode_inputs(1)
+    q0, z0 = O.bf16_to_f32(d0["qkv"]), O.bf16_to_f32(d0["z"])
+
+    def dn0(th):
+        return lambda: CB.deltanet_prefill(L, q0, z0, d0["a"], d0["b"], p, d0["conv_state"][0], d0["ssm_state"][0],
+                                           threads=th)
+    out["c0_deltanet_decode_b1"] = {
+        "value": 1.0 / _median_time(dn0(threads)), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": f"config 0, one DeltaNet decode step (batch 1), {threads} threads; {med}",
+        "single_thread": {"value": 1.0 / _median_time(dn0(1)), "unit": "tokens/s", "cores": 1}}
+
+    # config 2
+    rng = np.random.default_rng(1008)
+    ctxlen = 8192
+    for B in (1, 8, 32):
+        lengths = rng.integers(1, ctxlen + 1, B).astype(np.int32)
+        q = rng.standard_normal((B, 16, 256)).astype(np.float32)
+        K = _filled((B, ctxlen, 2, 256), rng)
+        V = _filled((B, ctxlen, 2, 256), rng)
+        a1 = _median_time(lambda: CB.attention_decode(L, q, K, V, lengths, threads=1))
+        an = _median_time(lambda: CB.attention_decode(L, q, K, V, lengths, threads=threads))
+        out[f"c2_gqa_decode_b{B}"] = {
+            "value": B / an, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 batch {B}, context 8192, lengths "
+                      f"{lengths.tolist() if B <= 8 else 'U[1, 8192]'}: split-KV decode attention of 16 q heads "
+                      f"per sequence, {threads} threads; {med}",
+            "single_thread": {"value": B / a1, "unit": "tokens/s", "cores": 1}}
+        del K, V
+
+    # config 3: token-by-token prefill sample at mid-sequence
+    T, t0, t1_ = 8192, 4064, 4096
+    x = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((t1_, 2048)).astype(np.float32)))
+    parts = []
+    for i, rows in enumerate((8192, 512, 512)):
+        w, sc, bi = synth.q4_weight(rows, 2048, seed=300 + i)
+        parts.append((w, O.f16_to_f32(sc), O.f16_to_f32(bi)))
+    w, sc, bi = CB.q4_stack(parts)
+    gp = synth.gqa_params()
+    K = _filled((T, 2, 256), rng)
+    V = _filled((T, 2, 256), rng)
+    att = np.zeros((t1_, 16, 256), np.float32)
+    t3 = _median_time(lambda: CB.gqa_prefill_tokens(L, t0, t1_, x, w, sc, bi, gp["q_norm_w"], gp["k_norm_w"], K, V,
+                                                    att, threads=threads), reps=3, warm=1)
+    v3 = (t1_ - t0) / t3
+    out["c3_gqa_prefill_t8192"] = {
+        "value": v3, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": f"config 3, tokens {t0}-{t1_ - 1} of the 8192-token sequence through the full-attention layer "
+                  f"token by token as the reference prefills (Q4 q|gate/k/v projections from hidden 2048, norms, "
+                  f"RoPE, attention over positions 0..t, gate), {threads} threads; median of 3 after 1 warm-up; "
+                  f"the whole 8192-token prefill at this average rate: {T / v3:.1f} s"}
+
+    # config 4: one layer of each kind, composed as 30 DeltaNet + 10 full attention
+    dn_in = CB.q4_stack([(w_, O.f16_to_f32(s_), O.f16_to_f32(b_)) for w_, s_, b_ in
+                         (synth.q4_weight(r, 2048, seed=500 + i) for i, r in enumerate((8192, 4096, 32, 32)))])
+    outp = synth.q4_weight(2048, 4096, seed=510)
+    dn_out = CB.q4_stack([(outp[0], O.f16_to_f32(outp[1]), O.f16_to_f32(outp[2]))])
+    norm_w = np.ones(2048, np.float32)
+    g_in = CB.q4_stack(parts)
+    for B, Lc in ((16, 32768), (1, 65536)):
+        xs = rng.standard_normal((B, 2048)).astype(np.float32)
+        conv = rng.standard_normal((B, 8192, 4)).astype(np.float32)
+        ssm = (rng.standard_normal((B, 32, 128, 128)) * 0.02).astype(np.float32)
+        Kc = _filled((B, Lc, 2, 256), rng)
+        Vc = _filled((B, Lc, 2, 256), rng)
+        pos = np.full(B, Lc - 1, np.int32)
+        t_dn = _median_time(lambda: CB.dn_layer_decode(L, xs, norm_w, dn_in, dn_out, p, conv, ssm, threads=threads),
+                            reps=3, warm=1)
+        t_gq = _median_time(lambda: CB.gqa_layer_decode(L, xs, norm_w, g_in, dn_out, gp["q_norm_w"],
+                                                        gp["k_norm_w"], Kc, Vc, pos, threads=threads), reps=3, warm=1)
+        step = 30 * t_dn + 10 * t_gq
+        out[f"c4_stack_b{B}_l{Lc}"] = {
+            "value": B / step, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 4 at batch {B}, context {Lc}: one Gated DeltaNet layer ({t_dn * 1e3:.2f} ms) and one "
+                      f"full-attention layer ({t_gq * 1e3:.2f} ms) of the stack's attention blocks, {threads} "
+                      f"threads, median of 3 after 1 warm-up, composed as 30 + 10 layers: {step * 1e3:.1f} ms "
+                      f"per step"}
+        del Kc, Vc
+    return out
 
 
 def copy_probe():
@@ -682,8 +778,11 @@ def main():
     cpu = None
     if not args.skip_cpu and c1 is not None:
         log("cpu baselines (oracle/cpu_baseline.c)")
-        cpu, cpu_c2 = cpu_baselines()
-        configs.setdefault("c2_gqa_decode_b8", {})["cpu_baseline"] = cpu_c2
+        for key, base in cpu_baselines().items():
+            if key == "c1_deltanet_prefill_t4096":
+                cpu = base
+            elif key in configs:
+                configs[key]["cpu_baseline"] = base
 
     if args.copy_probe:
         log("copy probe")

@@ -422,3 +422,68 @@ def test_gqa_prefill_config3_exact_call(hip):
             f"vectorised restatement off the oracle at row {t}"
     print("  restatement pinned; checking all rows", flush=True)
     assert_bf16_output_close(to_np(out), ref_all)
+
+
+def test_gqa_prefill_config3_from_x_end_to_end(hip):
+    """Config 3 from its input X, each side on its own projections: the HIP
+    path (the three-part Q4 GEMM on fp16 operands, bf16 outputs, then
+    qff_gqa_prefill from position 0) against the oracle's own chain
+    (QwenQ4ActiveExpertStreamingRunner.swift:1041-1150): the reference's
+    fp32 factored Q4 product (deltanet.metal:1838-1895) of X for q|gate at
+    the sampled rows and for k, v at every position (the fp64 product of the
+    dequantized weights, pinned to the factored order on the sampled rows),
+    rounded to bf16 as the workload's Q/K/V are, then the oracle's
+    append and attention. First the projections: every k / v / q|gate value
+    the GEMM produced is within one bf16 ulp plus 2.5e-3 of its row's RMS of
+    the oracle's (the fp16-weight error). Then the attention outputs of the
+    sampled rows meet the 2e-2 bar (bf16 outputs: or one bf16 ulp)."""
+    import qff
+    T, H = 8192, 2048
+    print("config 3 from X: Q4 GEMM T=8192 + gqa_prefill vs the oracle's own projections", flush=True)
+    rng = np.random.default_rng(33)
+    xb = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    ws = [synth.q4_weight(rows, H, seed=330 + i) for i, rows in enumerate((8192, 512, 512))]
+    parts = [(torch.from_numpy(w.view(np.int32)).to(DEV), torch.from_numpy(s.view(np.int16)).view(torch.float16).to(DEV),
+              torch.from_numpy(b.view(np.int16)).view(torch.float16).to(DEV)) for w, s, b in ws]
+    ctx = qff.Context(max_batch=1, max_ctx=T, max_prefill_tokens=T)
+    qg = torch.empty(T, 8192, dtype=torch.bfloat16, device=DEV)
+    k = torch.empty(T, 512, dtype=torch.bfloat16, device=DEV)
+    v = torch.empty(T, 512, dtype=torch.bfloat16, device=DEV)
+    qff.q4_matmul_parts(ctx, parts, bf16_tensor(xb), outs=(qg, k, v))
+    p = synth.gqa_params()
+    kc = torch.zeros(T, 2, 256, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    out = qff.gqa_prefill(ctx, {kk: f32_tensor(vv) for kk, vv in p.items()}, qg.view(T, 16, 512),
+                          k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    x = O.bf16_to_f32(xb)
+    rows = [0, 1, 63, 64, 511, 4095, 4096, 6000, 8190, 8191]
+    # the oracle's projections: k, v of every position (fp64 dense product),
+    # the reference's fp32 factored order at the sampled rows
+    dense = [O.q4_dequant(w, s, b, O.F16).astype(np.float64) for w, s, b in ws]
+    k_ref = (x.astype(np.float64) @ dense[1].T).astype(np.float32)
+    v_ref = (x.astype(np.float64) @ dense[2].T).astype(np.float32)
+    for t in rows:
+        for part, full in ((1, k_ref), (2, v_ref)):
+            fac = O.q4_matvec(*ws[part], x[t])
+            assert np.max(np.abs(fac - full[t])) <= 1e-5 * np.max(np.abs(full[t])), "factored order vs fp64"
+    print("  oracle projections ready", flush=True)
+    for gpu, ref in ((k, k_ref), (v, v_ref)):
+        g_ = to_np(gpu)
+        rms = np.sqrt((ref.astype(np.float64) ** 2).mean(axis=1, keepdims=True))
+        err = (np.abs(g_ - ref) - bf16_ulp(ref)) / rms
+        assert np.all(err <= 2.5e-3), f"k/v projection beyond one bf16 ulp + 2.5e-3 RMS: worst {err.max():.3g}"
+    kref = np.zeros((T, 2, 256), np.uint16)
+    vref = np.zeros((T, 2, 256), np.uint16)
+    O.gqa_append_kv_seq(O.round_bf16(k_ref).reshape(T, 2, 256), O.round_bf16(v_ref).reshape(T, 2, 256),
+                        p["k_norm_w"], kref, vref, O.BF16, start_pos=0)
+    qg_g = to_np(qg)
+    for t in rows:
+        qg_ref = O.q4_matvec(*ws[0], x[t])
+        rms = np.sqrt(np.mean(qg_ref.astype(np.float64) ** 2))
+        assert np.all(np.abs(qg_g[t] - qg_ref) - bf16_ulp(qg_ref) <= 2.5e-3 * rms), f"q|gate projection row {t}"
+        ref = O.gqa_attend(O.round_bf16(qg_ref).reshape(16, 512), p["q_norm_w"], kref, vref, O.BF16, t)
+        assert_bf16_output_close(got[t], ref)
+    print(f"  {len(rows)} rows within the bar", flush=True)
+    ctx.close()

@@ -123,11 +123,28 @@ def test_stack_two_steps_short_context(hip, B):
 
 def test_stack_config4_shape_one_group(hip):
     """The bench's config-4 shapes for one group of four layers: batch 16 at
-    32K context (every sequence at position 32767, as bench.py times it)."""
+    32K context (every sequence at position 32767, as bench.py times it),
+    every sequence checked."""
     B, L = 16, 32768
     print(f"stack config-4 shape B={B} L={L}", flush=True)
     ctx, st = _make_stack(4, B, L, seed=44)
     g = torch.Generator(device=DEV).manual_seed(4)
     x = torch.randn(B, 2048, device=DEV, generator=g)
-    _check_step(st, x, np.full(B, L - 1), seqs=[0, 9, 15])
+    _check_step(st, x, np.full(B, L - 1), seqs=range(B))
+    ctx.close()
+
+
+def test_stack_config4_single_sequence_64k(hip):
+    """Config 4's single-sequence step: one group of four layers at batch 1
+    and 64K context (position 65535, as bench.py times it), two steps in a
+    row (positions 65534 and 65535, the cache's last two), the second on
+    the states and cache the first left."""
+    B, L = 1, 65536
+    print(f"stack config-4 shape B={B} L={L}", flush=True)
+    ctx, st = _make_stack(4, B, L, seed=64)
+    g = torch.Generator(device=DEV).manual_seed(64)
+    x = torch.randn(B, 2048, device=DEV, generator=g)
+    for step, pos in enumerate((L - 2, L - 1)):
+        print(f" step {step} position {pos}", flush=True)
+        _check_step(st, x, np.full(B, pos), seqs=[0])
     ctx.close()
