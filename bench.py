@@ -578,6 +578,59 @@ def cpu_baselines():
     return out
 
 
+def measured_peaks():
+    """What this MI355X delivers, measured with the probes of
+    qwen-fieldfare_amd/probe/peaks.hip (lib/libqff_probe.so): an MFMA loop
+    (eight independent v_mfma_f32_16x16x32_bf16 chains per wave, 16,384
+    waves) and a grid-stride 16-byte streaming read of 2 GiB and copy of 1
+    GiB, each timed with HIP events on the launch stream over 5 launches
+    after 2 warm-ups. Reported beside the datasheet peaks the rooflines use
+    (BASELINE: the builder re-measures them)."""
+    import ctypes
+    import torch
+    L = ctypes.CDLL(os.path.join(ROOT, "qwen-fieldfare_amd", "lib", "libqff_probe.so"))
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    L.qffp_mfma_bf16.argtypes = [vp, i32, i32, vp]
+    L.qffp_stream_read.argtypes = [vp, vp, sz, i32, vp]
+    L.qffp_stream_copy.argtypes = [vp, vp, vp, sz, i32]
+    st = torch.cuda.current_stream()
+    sv = ctypes.c_void_p(st.cuda_stream)
+
+    def time_launch(fn, reps=5, warm=2):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    blocks, iters = 4096, 2000
+    sink = torch.empty(max(blocks * 4, 8192 * 256), device="cuda")
+    t = time_launch(lambda: L.qffp_mfma_bf16(sv, blocks, iters, ctypes.c_void_p(sink.data_ptr())))
+    mfma_tf = blocks * 4 * iters * 8 * 16384 / t / 1e12
+    nbytes = 2 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
+    rd = {}
+    for nb in (2048, 8192):
+        tr = time_launch(lambda: L.qffp_stream_read(sv, ctypes.c_void_p(src.data_ptr()), nbytes, nb,
+                                                    ctypes.c_void_p(sink.data_ptr())))
+        rd[nb] = nbytes / tr / 1e9
+    tc = time_launch(lambda: L.qffp_stream_copy(sv, ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                                nbytes // 2, 8192))
+    del src, dst, sink
+    torch.cuda.empty_cache()
+    return {"mfma_bf16_TFLOPs": mfma_tf, "mfma_frac_of_datasheet": mfma_tf / BF16_PEAK_TFLOPS,
+            "hbm_read_GBps": max(rd.values()), "hbm_read_GBps_by_grid": rd,
+            "hbm_copy_GBps": nbytes / tc / 1e9, "hbm_read_frac_of_datasheet": max(rd.values()) / HBM_PEAK_GBS,
+            "basis": "probe kernels of qwen-fieldfare_amd/probe/peaks.hip, HIP events, 5 launches after 2 warm-ups; "
+                     "copy counts bytes read + written"}
+
+
 def copy_probe():
     """One elementwise pass (dst = -src, fp32) that reads and writes
     COPY_PROBE_BYTES each, for scaling the FETCH_SIZE / WRITE_SIZE counters
@@ -787,6 +840,10 @@ def main():
     if args.copy_probe:
         log("copy probe")
         copy_probe()
+    peaks = None
+    if c1 is not None:
+        log("measured peaks (MFMA loop, streaming read / copy)")
+        peaks = measured_peaks()
 
     roof = None
     if c1 is not None:
@@ -809,7 +866,7 @@ def main():
         "vs_baseline": None, "dtype": "bf16 in/out, fp32 state+accum", "data": "synthetic",
         "config": {"workload": "config 1: Gated DeltaNet chunked prefill, 1 layer, B=1, T=4096, C=64",
                    "global_batch": 1, "seq_len": 4096, "parallelism": "none (1 GPU)"},
-        "roofline": roof, "cpu_baseline": cpu, "configs": configs,
+        "roofline": roof, "cpu_baseline": cpu, "measured_peaks": peaks, "configs": configs,
     }
     # leave nothing behind on the GPU: the context's workspace and torch's
     # cached blocks are released before the line is printed and the

@@ -436,7 +436,16 @@ def test_gqa_prefill_config3_from_x_end_to_end(hip):
     append and attention. First the projections: every k / v / q|gate value
     the GEMM produced is within one bf16 ulp plus 2.5e-3 of its row's RMS of
     the oracle's (the fp16-weight error). Then the attention outputs of the
-    sampled rows meet the 2e-2 bar (bf16 outputs: or one bf16 ulp)."""
+    sampled rows, in two links: against the oracle's attention fed the
+    GPU's own bf16 projections, the plain bar (max-abs 2e-2, or one bf16 ulp
+    of the output); against the oracle's own chain, that bar plus two bf16
+    ulps of the largest |V| the output mixes (per head and dim over the
+    attended positions): the GEMM's error (~3e-4 of a row's RMS, under the
+    2^-9 of the bf16 the workload stores Q/K/V in) makes a few percent of the
+    two sides' projections round to neighbouring bf16 values, and an output
+    that few positions dominate moves with their V by up to an ulp of V, not
+    of itself. The median end-to-end error is under one bf16 ulp of the
+    output."""
     import qff
     T, H = 8192, 2048
     print("config 3 from X: Q4 GEMM T=8192 + gqa_prefill vs the oracle's own projections", flush=True)
@@ -479,11 +488,26 @@ def test_gqa_prefill_config3_from_x_end_to_end(hip):
     O.gqa_append_kv_seq(O.round_bf16(k_ref).reshape(T, 2, 256), O.round_bf16(v_ref).reshape(T, 2, 256),
                         p["k_norm_w"], kref, vref, O.BF16, start_pos=0)
     qg_g = to_np(qg)
+    kg_bits = kc.cpu().view(torch.int16).numpy().view(np.uint16)
+    vg_bits = vc.cpu().view(torch.int16).numpy().view(np.uint16)
+    errs = []
     for t in rows:
         qg_ref = O.q4_matvec(*ws[0], x[t])
         rms = np.sqrt(np.mean(qg_ref.astype(np.float64) ** 2))
         assert np.all(np.abs(qg_g[t] - qg_ref) - bf16_ulp(qg_ref) <= 2.5e-3 * rms), f"q|gate projection row {t}"
+        # link 1: the attention on the GPU's own projections
+        own = O.gqa_attend(qg_g[t].reshape(16, 512), p["q_norm_w"], kg_bits, vg_bits, O.BF16, t)
+        assert_bf16_output_close(got[t], own)
+        # link 2: end to end against the oracle's own projections
         ref = O.gqa_attend(O.round_bf16(qg_ref).reshape(16, 512), p["q_norm_w"], kref, vref, O.BF16, t)
-        assert_bf16_output_close(got[t], ref)
-    print(f"  {len(rows)} rows within the bar", flush=True)
+        err = np.abs(got[t].astype(np.float64) - ref)
+        errs.append(err / bf16_ulp(ref))
+        vmax = np.abs(O.bf16_to_f32(vref[:t + 1])).max(axis=0)          # [2, 256]
+        vmax = np.repeat(vmax, 8, axis=0)                                 # per q head
+        lim = np.maximum(2e-2, bf16_ulp(ref)) + 2 * bf16_ulp(vmax)
+        assert np.all(err <= lim), f"row {t}: {int((err > lim).sum())} outside; worst {err.max():.4g}"
+    errs = np.concatenate([e.reshape(-1) for e in errs])
+    print(f"  {len(rows)} rows within the bar: median error {np.median(errs):.3g} output ulps, "
+          f"max {errs.max():.3g}", flush=True)
+    assert np.median(errs) <= 1.0
     ctx.close()
