@@ -581,18 +581,20 @@ def cpu_baselines():
 def measured_peaks():
     """What this MI355X delivers, measured with the probes of
     qwen-fieldfare_amd/probe/peaks.hip (lib/libqff_probe.so): an MFMA loop
-    (eight independent v_mfma_f32_16x16x32_bf16 chains per wave, 16,384
-    waves) and a grid-stride 16-byte streaming read of 2 GiB and copy of 1
-    GiB, each timed with HIP events on the launch stream over 5 launches
-    after 2 warm-ups. Reported beside the datasheet peaks the rooflines use
+    (16,384 waves, each with two independent v_mfma_f32_32x32x16_bf16
+    chains, then each with sixteen v_mfma_f32_16x16x32_bf16 chains) and a grid-stride 16-byte streaming read of 2 GiB, copy of 1 GiB
+    and in-place scale of 1 GiB (read + write of the same bytes, the traffic
+    of an in-place state update), each timed with HIP events on the launch
+    stream over 5 launches after 2 warm-ups. Reported beside the datasheet peaks the rooflines use
     (BASELINE: the builder re-measures them)."""
     import ctypes
     import torch
     L = ctypes.CDLL(os.path.join(ROOT, "qwen-fieldfare_amd", "lib", "libqff_probe.so"))
     vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
-    L.qffp_mfma_bf16.argtypes = [vp, i32, i32, vp]
+    L.qffp_mfma_bf16.argtypes = [vp, i32, i32, i32, vp]
     L.qffp_stream_read.argtypes = [vp, vp, sz, i32, vp]
     L.qffp_stream_copy.argtypes = [vp, vp, vp, sz, i32]
+    L.qffp_stream_rmw.argtypes = [vp, vp, sz, i32]
     st = torch.cuda.current_stream()
     sv = ctypes.c_void_p(st.cuda_stream)
 
@@ -610,8 +612,10 @@ def measured_peaks():
 
     blocks, iters = 4096, 2000
     sink = torch.empty(max(blocks * 4, 8192 * 256), device="cuda")
-    t = time_launch(lambda: L.qffp_mfma_bf16(sv, blocks, iters, ctypes.c_void_p(sink.data_ptr())))
-    mfma_tf = blocks * 4 * iters * 8 * 16384 / t / 1e12
+    mfma_tf = {}
+    for shape, name in ((0, "32x32x16"), (1, "16x16x32")):
+        t = time_launch(lambda: L.qffp_mfma_bf16(sv, shape, blocks, iters, ctypes.c_void_p(sink.data_ptr())))
+        mfma_tf[name] = blocks * 4 * iters * 65536 / t / 1e12
     nbytes = 2 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     dst = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
@@ -622,13 +626,17 @@ def measured_peaks():
         rd[nb] = nbytes / tr / 1e9
     tc = time_launch(lambda: L.qffp_stream_copy(sv, ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
                                                 nbytes // 2, 8192))
+    tw = time_launch(lambda: L.qffp_stream_rmw(sv, ctypes.c_void_p(dst.data_ptr()), nbytes // 2, 8192))
     del src, dst, sink
     torch.cuda.empty_cache()
-    return {"mfma_bf16_TFLOPs": mfma_tf, "mfma_frac_of_datasheet": mfma_tf / BF16_PEAK_TFLOPS,
+    best = max(mfma_tf.values())
+    return {"mfma_bf16_TFLOPs": best, "mfma_bf16_TFLOPs_by_shape": mfma_tf,
+            "mfma_frac_of_datasheet": best / BF16_PEAK_TFLOPS,
             "hbm_read_GBps": max(rd.values()), "hbm_read_GBps_by_grid": rd,
-            "hbm_copy_GBps": nbytes / tc / 1e9, "hbm_read_frac_of_datasheet": max(rd.values()) / HBM_PEAK_GBS,
+            "hbm_copy_GBps": nbytes / tc / 1e9, "hbm_inplace_rmw_GBps": nbytes / tw / 1e9,
+            "hbm_read_frac_of_datasheet": max(rd.values()) / HBM_PEAK_GBS,
             "basis": "probe kernels of qwen-fieldfare_amd/probe/peaks.hip, HIP events, 5 launches after 2 warm-ups; "
-                     "copy counts bytes read + written"}
+                     "copy and in-place count bytes read + written"}
 
 
 def copy_probe():
