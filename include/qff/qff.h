@@ -255,12 +255,17 @@ typedef struct qff_gqa_params {
     int rotary_dim;         /* 64: rotate-half on pairs (i, i+32), i < 32   */
     float scale;            /* softmax scale, 1/16                          */
     float eps;              /* head RMSNorm epsilon (1e-6)                  */
+    int kv_f16;             /* KV cache element type: 0 bf16 (the default a
+                               zeroed struct gets), 1 fp16 (the runner's
+                               Float16 caches, Runner:731-732)             */
 } qff_gqa_params;
 
 /* One decode token for each of `batch` sequences: split the per-head
  * interleaved q|gate projection, RMSNorm q and k per head, partial RoPE at
- * the sequence's position, append k and v at that position of the bf16
- * token-major cache, attend over positions 0..pos with 16 q heads on 2 kv
+ * the sequence's position, append k and v at that position of the
+ * token-major cache (bf16, or fp16 with p->kv_f16; the reference's cache is
+ * fp16, written by qwen_update_kv_cache_f16), attend over positions 0..pos
+ * with 16 q heads on 2 kv
  * heads (q head h uses kv head h/8), and gate: out = attn * sigmoid(gate).
  * Replaces QwenQ4ActiveExpertStreamingRunner.swift:1076-1150, i.e.
  * qwen_split_q_gate_f32, qwen_head_rmsnorm_f32, host RoPE tables +
@@ -269,7 +274,8 @@ typedef struct qff_gqa_params {
  * (deltanet.metal:599-708; attention.metal:134-377; Attention.swift:195-299).
  *   q_gate    [batch, 16, 512]: q = [..., :256], gate = [..., 256:] (in_dtype)
  *   k_new     [batch, 2, 256], v_new [batch, 2, 256] (in_dtype)
- *   k_cache, v_cache [batch, max_ctx, 2, 256] bf16, updated at pos
+ *   k_cache, v_cache [batch, max_ctx, 2, 256] bf16 (fp16 with p->kv_f16),
+ *             updated at pos
  *   positions [batch] int32 device array, 0 <= pos < max_ctx
  *   out       [batch, 16, 256] of out_dtype (F32 or BF16) */
 int qff_gqa_decode(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
@@ -300,7 +306,8 @@ int qff_gqa_decode_static(qff_stream_t stream, const qff_gqa_params* p, const vo
  * values appended to the cache. The reference runs prompts token by token
  * through the decode path (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561).
  *   q_gate [T, 16, 512], k, v [T, 2, 256] (in_dtype);
- *   k_cache, v_cache [max_ctx, 2, 256] bf16; out [T, 16, 256] (out_dtype).
+ *   k_cache, v_cache [max_ctx, 2, 256] bf16 (fp16 with p->kv_f16);
+ *   out [T, 16, 256] (out_dtype).
  * QFF_ERR_INVALID_ARG when start_pos + T > max_ctx; QFF_ERR_WORKSPACE when T
  * exceeds the context's max_prefill_tokens. */
 int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,

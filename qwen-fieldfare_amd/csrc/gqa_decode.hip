@@ -1,5 +1,5 @@
 // gqa_decode.hip -- full-attention decode (16 q heads on 2 kv heads, head dim
-// 256, bf16 token-major KV cache) for a batch of sequences on gfx950.
+// 256, bf16 or fp16 token-major KV cache) for a batch of sequences on gfx950.
 //
 // Reference: QwenQ4ActiveExpertStreamingRunner.swift:1076-1150 runs split
 // q/gate, head RMSNorm, host RoPE tables + RoPE, the f16 KV append, a cast of
@@ -30,6 +30,10 @@
 //            (m, d, o[8][256]) partial per chunk (m in base-2 units).
 //   combine  grid (q head, sequence): merges the chunk partials and applies
 //            out = attn * sigmoid(gate).
+// With an fp16 cache (the reference's, Runner:731-732) the same kernel runs
+// its products on fp16 MFMAs (KV_F16): q and P become fp16 hi + lo pairs
+// (~22 bits) and the appended k, v are rounded to fp16; K and V are exact
+// in either MFMA type.
 // Lengths come from the device `positions` array, so no host sync is needed;
 // waves past a sequence's last chunk exit at once.
 #include "common.hpp"
@@ -48,8 +52,8 @@ struct DecTile {
 
 // Wave-local LDS of one partial unit.
 struct DecLds {
-    uint16_t qs[8][256];                      // normed, rotated, scaled q: bf16 hi part
-    uint16_t ql[8][256];                      // ... and lo part (q = hi + lo to ~2^-16)
+    uint16_t qs[8][256];                      // normed, rotated, scaled q: hi part (cache's type)
+    uint16_t ql[8][256];                      // ... and lo part (q = hi + lo to ~2^-16 / 2^-22)
     uint16_t vs[kDecTile * kVRowStride];      // the current V tile, row-major
     uint16_t knew[256], vnew[256];            // the new token's k, v
     float2 rcs[32];                           // (cos, sin) of pos * f[i]
@@ -77,7 +81,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // transpose read (ds_read_b64_tr_b16), O += P V with 16 MFMA 16x16x16 (P as
 // bf16 hi + lo in rows 0-7 / 8-15, added at the end), and writes one (m, d, o[8][256]) partial (m in base-2 units). The next
 // tile's loads are in flight while a tile computes (two register stages).
-template <int IN_DT>
+template <int IN_DT, int KV_F16>
 __device__ __forceinline__ void gqa_partial_unit(
     DecLds& L, int seq, int kvh, int c, int pos, int lane, const void* __restrict__ q_gate,
     const void* __restrict__ k_new, const void* __restrict__ v_new, const float* __restrict__ q_norm_w,
@@ -165,7 +169,8 @@ __device__ __forceinline__ void gqa_partial_unit(
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
             uint32_t hi, lo;
-            split_bf16x2(x[i] * qscale, x[i + 1] * qscale, hi, lo);
+            if (KV_F16) split_f16x2(x[i] * qscale, x[i + 1] * qscale, hi, lo);
+            else split_bf16x2(x[i] * qscale, x[i + 1] * qscale, hi, lo);
             *reinterpret_cast<uint32_t*>(&L.qs[hl][8 * j + i]) = hi;
             *reinterpret_cast<uint32_t*>(&L.ql[hl][8 * j + i]) = lo;
         }
@@ -196,8 +201,10 @@ __device__ __forceinline__ void gqa_partial_unit(
                 kx[i] = (d < 32) ? kx[i] * r.x + (-up) * r.y : kx[i] * r.x + dn * r.y;
             }
         }
-        const uint32_t k01 = pack_bf16x2(kx[0], kx[1]), k23 = pack_bf16x2(kx[2], kx[3]);
-        const uint32_t v01 = pack_bf16x2(vx[0], vx[1]), v23 = pack_bf16x2(vx[2], vx[3]);
+        const uint32_t k01 = KV_F16 ? pack_f16x2(kx[0], kx[1]) : pack_bf16x2(kx[0], kx[1]);
+        const uint32_t k23 = KV_F16 ? pack_f16x2(kx[2], kx[3]) : pack_bf16x2(kx[2], kx[3]);
+        const uint32_t v01 = KV_F16 ? pack_f16x2(vx[0], vx[1]) : pack_bf16x2(vx[0], vx[1]);
+        const uint32_t v23 = KV_F16 ? pack_f16x2(vx[2], vx[3]) : pack_bf16x2(vx[2], vx[3]);
         *reinterpret_cast<u32x2_t*>(&L.knew[4 * lane]) = u32x2_t{k01, k23};
         *reinterpret_cast<u32x2_t*>(&L.vnew[4 * lane]) = u32x2_t{v01, v23};
         const size_t off = seq_base + static_cast<size_t>(pos) * 512 + 4 * lane;
@@ -206,7 +213,7 @@ __device__ __forceinline__ void gqa_partial_unit(
     }
     wave_lds_sync();
 
-    // q^T (B of 16x16x32): col n = head n & 7, its bf16 hi part for n < 8 and
+    // q^T (B of 16x16x32): col n = head n & 7, its hi part for n < 8 and
     // lo part for n >= 8 (the columns a group of 8 heads leaves free), k =
     // dims 32jj + 8kb .. +7, read from LDS per tile (registers are kept for
     // the two tile stages)
@@ -230,15 +237,18 @@ __device__ __forceinline__ void gqa_partial_unit(
                 tl.k[jj] = kv;
             }
         }
-        // S^T = K Q^T, q as hi + lo (K is exact in bf16): the scores carry
-        // ~16 significant bits of q, finer than the reference's fp16 q.
+        // S^T = K Q^T, q as hi + lo (K is exact in the cache's type): the
+        // scores carry ~16 (bf16) or ~22 (fp16) significant bits of q, finer
+        // than the reference's fp16 q.
         // Column n scores against head n & 7's hi (n < 8) or lo (n >= 8)
         // part; lanes n and n ^ 8 (DPP row rotate by 8) add the two, so
         // both hold head n & 7's scores from here on.
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-            s = mfma_16x16x32_bf16(tl.k[jj], *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj), s);
+        for (int jj = 0; jj < 8; ++jj) {
+            const u32x4_t qop = *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj);
+            s = KV_F16 ? mfma_16x16x32_f16(tl.k[jj], qop, s) : mfma_16x16x32_bf16(tl.k[jj], qop, s);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[i] += dpp_mov<0x128>(s[i]);
         // V tile row-major into LDS (the new token's row from LDS as well)
@@ -281,11 +291,16 @@ __device__ __forceinline__ void gqa_partial_unit(
             d_run += pe[i];
         }
         // A of O += P V (16x16x16): row n = head n & 7, k = positions 4kb ..
-        // +3, P's bf16 hi part in rows 0-7 and lo part in rows 8-15 (V is
-        // exact in bf16), so rows h and h + 8 of O sum to head h's output
+        // +3, P's hi part in rows 0-7 and lo part in rows 8-15 (V is exact
+        // in the cache's type), so rows h and h + 8 of O sum to head h's output
         uint32_t ph0, pl0, ph1, pl1;
-        split_bf16x2(pe[0], pe[1], ph0, pl0);
-        split_bf16x2(pe[2], pe[3], ph1, pl1);
+        if (KV_F16) {
+            split_f16x2(pe[0], pe[1], ph0, pl0);
+            split_f16x2(pe[2], pe[3], ph1, pl1);
+        } else {
+            split_bf16x2(pe[0], pe[1], ph0, pl0);
+            split_bf16x2(pe[2], pe[3], ph1, pl1);
+        }
         const u32x2_t pa = n < 8 ? u32x2_t{ph0, ph1} : u32x2_t{pl0, pl1};
         // B = V^T block straight from the row-major tile with a transpose read:
         // source lane (group kb, s = n) points at row 4kb + n/4, dims
@@ -295,7 +310,7 @@ __device__ __forceinline__ void gqa_partial_unit(
 #pragma unroll
         for (int jd = 0; jd < 16; ++jd) {
             const u32x2_t vb = lds_read_tr16(vsrc + 16 * jd);
-            oacc[jd] = mfma_16x16x16_bf16(pa, vb, oacc[jd]);
+            oacc[jd] = KV_F16 ? mfma_16x16x16_f16(pa, vb, oacc[jd]) : mfma_16x16x16_bf16(pa, vb, oacc[jd]);
         }
         wave_lds_sync();
     };
@@ -396,7 +411,7 @@ __device__ __forceinline__ void gqa_split(const int32_t* __restrict__ positions,
 // workgroups of a chunk are dispatched together and stream the interleaved
 // halves of the same cache records at the same time. Two single-wave
 // workgroups per SIMD stay resident, each with its next tile in flight.
-template <int IN_DT>
+template <int IN_DT, int KV_F16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 void gqa_decode_partial_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k_new, const void* __restrict__ v_new,
@@ -417,8 +432,8 @@ void gqa_decode_partial_kernel(
     __shared__ float freqs[32];
     if (lane < 32) freqs[lane] = rf.f[lane];
     wave_lds_sync();
-    gqa_partial_unit<IN_DT>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
-                                   scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
+    gqa_partial_unit<IN_DT, KV_F16>(lds, seq, kvh, c, pos, lane, q_gate, k_new, v_new, q_norm_w, k_norm_w, freqs,
+                                    scale, eps, k_cache, v_cache, max_ctx, chunk_len, cstride, pm, pd, po);
 }
 
 // grid (16 q heads x DS dim blocks, batch), 512 threads: attention.metal
@@ -536,11 +551,15 @@ hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     {
         ProfScope prof(ctx, stream, "gqa_decode_partial");
-#define QFF_PART(I)                                                                                             \
-    gqa_decode_partial_kernel<I><<<units, 64, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf,   \
-                                                          p->scale, p->eps, kc, vc, positions, batch, max_ctx,  \
-                                                          target, cap, ws.m, ws.d, ws.o)
-        if (in_dtype == QFF_BF16) QFF_PART(1); else QFF_PART(0);
+#define QFF_PART(I, F)                                                                                           \
+    gqa_decode_partial_kernel<I, F><<<units, 64, 0, stream>>>(q_gate, k_new, v_new, p->q_norm_w, p->k_norm_w, rf, \
+                                                             p->scale, p->eps, kc, vc, positions, batch, max_ctx, \
+                                                             target, cap, ws.m, ws.d, ws.o)
+        if (p->kv_f16) {
+            if (in_dtype == QFF_BF16) QFF_PART(1, 1); else QFF_PART(0, 1);
+        } else {
+            if (in_dtype == QFF_BF16) QFF_PART(1, 0); else QFF_PART(0, 0);
+        }
 #undef QFF_PART
     }
     // small batches split each head's 256 dims over 4 workgroups

@@ -8,7 +8,7 @@
 //   prep   one wave per token: head RMSNorm + partial RoPE of the
 //          16 q heads (fp16, softmax scale folded in, to workspace: the
 //          reference also rounds q to half, Runner:1119-1126) and of the 2 k
-//          heads (appended to the bf16 cache together with v).
+//          heads (appended to the cache, bf16 or fp16, together with v).
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; four wave pairs of 32 rows = 4 tokens
 //          x 8 heads, each wave scoring half of a tile's positions and
@@ -16,8 +16,9 @@
 //          in VGPRs and two waves share each SIMD) and walks 64-position
 //          K/V tiles staged in LDS
 //          row-major (double-buffered; the next tile's global loads are in
-//          flight while the current one computes), converted from the bf16
-//          cache to fp16 as they are staged (exact for the cache's values),
+//          flight while the current one computes), converted from a bf16
+//          cache to fp16 as they are staged (exact for the cache's values;
+//          an fp16 cache, the reference's, is staged as it is),
 //          so both products run on fp16 operands: S^T = K Q^T on 16x16x32
 //          fp16 MFMAs (q keeps the 11-bit significand the reference gives
 //          it, where bf16 q puts rare outputs beyond the output tolerance
@@ -51,7 +52,7 @@ constexpr int kKStride = 264;   // fp16 per K row in LDS: 256 + 8 pad (528 B)
 constexpr int kPrepWaves = 8;
 constexpr int kPrepRound = 6;
 
-template <int IN_DT>
+template <int IN_DT, int KV_F16>
 __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
@@ -124,10 +125,17 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
             } else {
                 const int kvh = hs - 16;
                 const size_t off = (static_cast<size_t>(pos) * 2 + kvh) * 256 + 4 * lane;
-                *reinterpret_cast<u32x2_t*>(k_cache + off) =
-                    u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-                *reinterpret_cast<u32x2_t*>(v_cache + off) =
-                    u32x2_t{pack_bf16x2(vv[kvh][0], vv[kvh][1]), pack_bf16x2(vv[kvh][2], vv[kvh][3])};
+                if (KV_F16) {
+                    *reinterpret_cast<u32x2_t*>(k_cache + off) =
+                        u32x2_t{pack_f16x2(y[0], y[1]), pack_f16x2(y[2], y[3])};
+                    *reinterpret_cast<u32x2_t*>(v_cache + off) =
+                        u32x2_t{pack_f16x2(vv[kvh][0], vv[kvh][1]), pack_f16x2(vv[kvh][2], vv[kvh][3])};
+                } else {
+                    *reinterpret_cast<u32x2_t*>(k_cache + off) =
+                        u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                    *reinterpret_cast<u32x2_t*>(v_cache + off) =
+                        u32x2_t{pack_bf16x2(vv[kvh][0], vv[kvh][1]), pack_bf16x2(vv[kvh][2], vv[kvh][3])};
+                }
             }
         }
     }
@@ -158,15 +166,16 @@ __device__ __forceinline__ void tile_load(TileRegs& r, const uint16_t* __restric
     }
 }
 
-// ... and stores them to LDS as fp16.
+// ... and stores them to LDS as fp16 (an fp16 cache's pieces as they are).
+template <int KV_F16>
 __device__ __forceinline__ void tile_store(const TileRegs& r, uint16_t* __restrict__ ks, uint16_t* __restrict__ vs,
                                            int t) {
 #pragma unroll
     for (int i = 0; i < kPfPieces; ++i) {
         const int q = t + kPfThreads * i;
         const int o = (q >> 5) * kKStride + 8 * (q & 31);
-        *reinterpret_cast<u32x4_t*>(ks + o) = bf16x8_to_f16x8(r.k[i]);
-        *reinterpret_cast<u32x4_t*>(vs + o) = bf16x8_to_f16x8(r.v[i]);
+        *reinterpret_cast<u32x4_t*>(ks + o) = KV_F16 ? r.k[i] : bf16x8_to_f16x8(r.k[i]);
+        *reinterpret_cast<u32x4_t*>(vs + o) = KV_F16 ? r.v[i] : bf16x8_to_f16x8(r.v[i]);
     }
 }
 
@@ -179,7 +188,7 @@ __device__ __forceinline__ void tile_store(const TileRegs& r, uint16_t* __restri
 // 128e .. 128e + 127 over all 64 positions (each V operand feeds two MFMAs):
 // 34 KB of LDS reads per wave and tile instead of the 64 KB a wave of 16
 // rows scoring every position and accumulating every dim would need.
-template <int IN_DT, int OUT_DT>
+template <int IN_DT, int OUT_DT, int KV_F16>
 __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const uint16_t* __restrict__ qb, const void* __restrict__ q_gate, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int start, int T, void* __restrict__ out) {
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
 
     TileRegs regs;
     tile_load(regs, k_cache, v_cache, kvh, 0, kv_end, t);
-    tile_store(regs, Ks[0], Vs[0], t);
+    tile_store<KV_F16>(regs, Ks[0], Vs[0], t);
     // every load before the loop (q included) has landed: without this the
     // loop's waits would also cover the next tile's loads each iteration
     __builtin_amdgcn_s_waitcnt(0);
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                 }
             }
         }
-        if (more) tile_store(regs, Ks[cur ^ 1], Vs[cur ^ 1], t);
+        if (more) tile_store<KV_F16>(regs, Ks[cur ^ 1], Vs[cur ^ 1], t);
         __syncthreads();
     }
 
@@ -391,22 +400,33 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
     {
         ProfScope prof(ctx, stream, "gqa_prefill_prep");
         const int pgrid = (T + kPrepWaves - 1) / kPrepWaves;
-        if (in_dtype == QFF_BF16)
-            gqa_prefill_prep_kernel<1><<<pgrid, 64 * kPrepWaves, 0, stream>>>(
-                q_gate, k, v, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, start_pos, T, qb, kc, vc);
-        else
-            gqa_prefill_prep_kernel<0><<<pgrid, 64 * kPrepWaves, 0, stream>>>(
-                q_gate, k, v, p->q_norm_w, p->k_norm_w, rf, p->scale, p->eps, start_pos, T, qb, kc, vc);
+#define QFF_PREP(I, F)                                                                                           \
+    gqa_prefill_prep_kernel<I, F><<<pgrid, 64 * kPrepWaves, 0, stream>>>(q_gate, k, v, p->q_norm_w, p->k_norm_w, \
+                                                                        rf, p->scale, p->eps, start_pos, T, qb, \
+                                                                        kc, vc)
+        if (p->kv_f16) {
+            if (in_dtype == QFF_BF16) QFF_PREP(1, 1); else QFF_PREP(0, 1);
+        } else {
+            if (in_dtype == QFF_BF16) QFF_PREP(1, 0); else QFF_PREP(0, 0);
+        }
+#undef QFF_PREP
     }
     const dim3 grid((T + kPfQB - 1) / kPfQB, 2);
     ProfScope prof(ctx, stream, "gqa_prefill_attn");
-#define QFF_PFA(I, O) \
-    gqa_prefill_attn_kernel<I, O><<<grid, kPfThreads, 0, stream>>>(qb, q_gate, kc, vc, start_pos, T, out)
-    if (in_dtype == QFF_BF16) {
-        if (out_dtype == QFF_BF16) QFF_PFA(1, 1); else QFF_PFA(1, 0);
-    } else {
-        if (out_dtype == QFF_BF16) QFF_PFA(0, 1); else QFF_PFA(0, 0);
+#define QFF_PFA(I, O, F) \
+    gqa_prefill_attn_kernel<I, O, F><<<grid, kPfThreads, 0, stream>>>(qb, q_gate, kc, vc, start_pos, T, out)
+#define QFF_PFA_IO(F)                                                     \
+    if (in_dtype == QFF_BF16) {                                           \
+        if (out_dtype == QFF_BF16) QFF_PFA(1, 1, F); else QFF_PFA(1, 0, F); \
+    } else {                                                              \
+        if (out_dtype == QFF_BF16) QFF_PFA(0, 1, F); else QFF_PFA(0, 0, F); \
     }
+    if (p->kv_f16) {
+        QFF_PFA_IO(1)
+    } else {
+        QFF_PFA_IO(0)
+    }
+#undef QFF_PFA_IO
 #undef QFF_PFA
     return hipGetLastError();
 }

@@ -110,10 +110,12 @@ struct RopeFreqs {
 RopeFreqs rope_freqs(float theta);
 
 // Status of a full-attention parameter block: the norm weights present, a
-// finite positive softmax scale, RoPE theta and eps (invalid argument
-// otherwise); rotary_dim 64 is the only rotation built (unsupported otherwise).
+// finite positive softmax scale, RoPE theta and eps, a cache type flag of 0
+// or 1 (invalid argument otherwise); rotary_dim 64 is the only rotation
+// built (unsupported otherwise).
 inline int gqa_params_status(const qff_gqa_params* p) {
     if (!p || !p->q_norm_w || !p->k_norm_w) return QFF_ERR_INVALID_ARG;
+    if (p->kv_f16 != 0 && p->kv_f16 != 1) return QFF_ERR_INVALID_ARG;
     if (!(p->scale > 0.0f) || !(p->scale < __builtin_huge_valf())) return QFF_ERR_INVALID_ARG;
     if (!(p->rope_theta > 0.0f) || !(p->rope_theta < __builtin_huge_valf()) || !(p->eps >= 0.0f))
         return QFF_ERR_INVALID_ARG;

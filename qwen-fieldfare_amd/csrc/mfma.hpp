@@ -4,7 +4,7 @@
 // Register layouts (wave64, lane l):
 //   16x16x32 bf16 / f16: A[16 x 32]: lane l holds row l%16, k = 8*(l/16) .. +7
 //                  B[32 x 16]: lane l holds col l%16, k = 8*(l/16) .. +7
-//   16x16x16 bf16: A[16 x 16]: lane l holds row l%16, k = 4*(l/16) .. +3
+//   16x16x16 bf16 / f16: A[16 x 16]: lane l holds row l%16, k = 4*(l/16) .. +3
 //                  B[16 x 16]: lane l holds col l%16, k = 4*(l/16) .. +3
 //   C/D[16 x 16] fp32: lane l holds col l%16, rows 4*(l/16) .. +3
 #pragma once
@@ -37,11 +37,29 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32_f16(u32x4_t a, u32x4_t b, f32x4
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma_16x16x16_f16(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                 0, 0, 0);
+}
+
 // Two floats -> packed fp16 pair, round to nearest even; the low half holds lo.
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
     const f16x2_t v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
     return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two floats as fp16 hi and lo pairs: hi = fp16(x), lo = fp16(x - hi), so
+// hi + lo carries ~22 significant bits for x in fp16's normal range (the
+// remainder is exact in fp32; lo loses bits only where it falls below
+// 2^-14, an absolute error under 2^-25).
+__device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t h = {static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = pack_f16x2(x0 - static_cast<float>(h[0]), x1 - static_cast<float>(h[1]));
 }
 
 // Two packed bf16 -> two packed fp16. Exact for every bf16 value inside the

@@ -31,7 +31,7 @@ class DeltaNetParams(ctypes.Structure):
 
 class GqaParams(ctypes.Structure):
     _fields_ = [("q_norm_w", _vp), ("k_norm_w", _vp), ("rope_theta", _f), ("rotary_dim", _i),
-                ("scale", _f), ("eps", _f)]
+                ("scale", _f), ("eps", _f), ("kv_f16", _i)]
 
 
 class Q4Part(ctypes.Structure):

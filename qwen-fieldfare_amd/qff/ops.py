@@ -222,24 +222,26 @@ def deltanet_prefill(ctx: Context, params: dict, qkv, z, a, b, conv_state, ssm_s
 
 
 def _check_gqa_inputs(q_gate, k, v, k_cache, v_cache, n):
-    """The library reads q_gate, k and v with one element type and the
-    caches as bf16: reject anything else before it reaches the device."""
-    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise TypeError("KV caches must be bfloat16")
+    """The library reads q_gate, k and v with one element type and both
+    caches as bf16 or both as fp16 (the reference's cache type): reject
+    anything else before it reaches the device."""
+    if k_cache.dtype not in (torch.bfloat16, torch.float16) or v_cache.dtype != k_cache.dtype:
+        raise TypeError("KV caches must both be bfloat16 or both float16")
     if k.dtype != q_gate.dtype or v.dtype != q_gate.dtype:
         raise TypeError("k and v must share q_gate's dtype")
     if q_gate.numel() != n * 16 * 512 or k.numel() != n * 512 or v.numel() != n * 512:
         raise ValueError("q_gate must be [n, 16, 512] and k, v [n, 2, 256]")
 
 
-def _gqa_params(p: dict, theta, scale, eps):
-    return GqaParams(_ptr(p["q_norm_w"]), _ptr(p["k_norm_w"]), theta, 64, scale, eps)
+def _gqa_params(p: dict, theta, scale, eps, k_cache):
+    return GqaParams(_ptr(p["q_norm_w"]), _ptr(p["k_norm_w"]), theta, 64, scale, eps,
+                     int(k_cache.dtype == torch.float16))
 
 
 def gqa_decode(ctx: Context, params: dict, q_gate, k_new, v_new, k_cache, v_cache, positions,
                out=None, out_dtype=torch.bfloat16, theta=1e7, scale=1.0 / 16, eps=1e-6):
-    """q_gate [B,16,512], k_new/v_new [B,2,256]; caches [B,max_ctx,2,256] bf16;
-    positions int32 [B] (device) -> out [B,16,256]."""
+    """q_gate [B,16,512], k_new/v_new [B,2,256]; caches [B,max_ctx,2,256] bf16
+    or fp16; positions int32 [B] (device) -> out [B,16,256]."""
     B = q_gate.shape[0]
     max_ctx = k_cache.shape[1]
     _check_gqa_inputs(q_gate, k_new, v_new, k_cache, v_cache, B)
@@ -249,7 +251,7 @@ def gqa_decode(ctx: Context, params: dict, q_gate, k_new, v_new, k_cache, v_cach
         raise TypeError("positions must be int32 [B]")
     if out is None:
         out = torch.empty(B, 16, 256, dtype=out_dtype, device=q_gate.device)
-    prm = _gqa_params(params, theta, scale, eps)
+    prm = _gqa_params(params, theta, scale, eps, k_cache)
     check("qff_gqa_decode", lib().qff_gqa_decode(
         ctx.handle, _stream(), ctypes.byref(prm), _ptr(q_gate), _ptr(k_new), _ptr(v_new),
         _code(q_gate), _ptr(k_cache), _ptr(v_cache), _ptr(positions), _ptr(out), _code(out), B,
@@ -259,7 +261,8 @@ def gqa_decode(ctx: Context, params: dict, q_gate, k_new, v_new, k_cache, v_cach
 
 def gqa_prefill(ctx: Context, params: dict, q_gate, k, v, k_cache, v_cache, start_pos=0, out=None,
                 out_dtype=torch.bfloat16, theta=1e7, scale=1.0 / 16, eps=1e-6):
-    """q_gate [T,16,512], k/v [T,2,256]; caches [max_ctx,2,256] bf16 -> out [T,16,256]."""
+    """q_gate [T,16,512], k/v [T,2,256]; caches [max_ctx,2,256] bf16 or fp16
+    -> out [T,16,256]."""
     T = q_gate.shape[0]
     max_ctx = k_cache.shape[0]
     _check_gqa_inputs(q_gate, k, v, k_cache, v_cache, T)
@@ -267,7 +270,7 @@ def gqa_prefill(ctx: Context, params: dict, q_gate, k, v, k_cache, v_cache, star
         raise ValueError("KV caches must be [max_ctx, 2, 256]")
     if out is None:
         out = torch.empty(T, 16, 256, dtype=out_dtype, device=q_gate.device)
-    prm = _gqa_params(params, theta, scale, eps)
+    prm = _gqa_params(params, theta, scale, eps, k_cache)
     check("qff_gqa_prefill", lib().qff_gqa_prefill(
         ctx.handle, _stream(), ctypes.byref(prm), _ptr(q_gate), _ptr(k), _ptr(v), _code(q_gate),
         _ptr(k_cache), _ptr(v_cache), start_pos, _ptr(out), _code(out), T, max_ctx))

@@ -238,7 +238,7 @@ static void run_gqa(qff_ctx* ctx) {
     int32_t* d_pos = dev_copy(pos, sizeof pos);
     void* d_out = NULL;
     HIP_OK(hipMalloc(&d_out, sizeof(float) * B * 16 * 256));
-    qff_gqa_params prm = {d_qn, d_kn, 1e7f, 64, 1.0f / 16.0f, 1e-6f};
+    qff_gqa_params prm = {d_qn, d_kn, 1e7f, 64, 1.0f / 16.0f, 1e-6f, 0};   /* bf16 cache */
     QFF_OK_CALL(qff_gqa_decode(ctx, NULL, &prm, d_qg, d_knew, d_vnew, QFF_BF16, d_kc, d_vc, d_pos, d_out, QFF_F32,
                                B, L));
     HIP_OK(hipDeviceSynchronize());

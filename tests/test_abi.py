@@ -81,3 +81,36 @@ def test_product_has_no_cpu_fallback():
             if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
                 src = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"(from|import)\s+oracle|qff_oracle|libqff_oracle", src), f
+
+
+def test_parameter_structs_match_the_header(tmp_path):
+    """The ctypes mirrors of the header's parameter blocks have the C
+    layout: a C program built against include/qff/qff.h prints each
+    struct's size and every field's offset, and the ctypes classes must
+    agree field for field (a field added on one side only would shift the
+    others silently)."""
+    import subprocess
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "qwen-fieldfare_amd"))
+    from qff import _lib
+    mirrors = {"qff_ctx_cfg": _lib.CtxCfg, "qff_q4_part": _lib.Q4Part,
+               "qff_deltanet_params": _lib.DeltaNetParams, "qff_gqa_params": _lib.GqaParams}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "qff/qff.h"', "int main(void) {"]
+    for cname, py in mirrors.items():
+        lines.append(f'    printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'    printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["    return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    r = subprocess.run(["gcc", "-std=c99", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
+                        "-o", str(exe), str(src)], capture_output=True, text=True)
+    if r.returncode != 0:
+        pytest.skip("no C compiler for the layout probe: " + r.stderr[-200:])
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                              check=True).stdout.splitlines())
+    for cname, py in mirrors.items():
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert int(got[f"{cname} {fname}"]) == getattr(py, fname).offset, (cname, fname)
