@@ -613,9 +613,10 @@ def measured_peaks():
     blocks, iters = 4096, 2000
     sink = torch.empty(max(blocks * 4, 8192 * 256), device="cuda")
     mfma_tf = {}
-    for shape, name in ((0, "32x32x16"), (1, "16x16x32")):
+    # flops per wave and iteration: two 32x32x16 (32,768 each), sixteen 16x16x32 (16,384 each)
+    for shape, name, per_it in ((0, "32x32x16", 2 * 32768), (1, "16x16x32", 16 * 16384)):
         t = time_launch(lambda: L.qffp_mfma_bf16(sv, shape, blocks, iters, ctypes.c_void_p(sink.data_ptr())))
-        mfma_tf[name] = blocks * 4 * iters * 65536 / t / 1e12
+        mfma_tf[name] = blocks * 4 * iters * per_it / t / 1e12
     nbytes = 2 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     dst = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void stream_rmw_kernel(float4* __restrict__ p,
 extern "C" {
 
 // blocks workgroups of 4 waves; sink holds blocks * 4 floats. Flops:
-// blocks * 4 * iters * 65536 (either shape).
+// blocks * 4 * iters * 65536 (shape 0) or * 262144 (shape 1).
 int qffp_mfma_bf16(hipStream_t stream, int shape, int blocks, int iters, float* sink) {
     if (blocks <= 0 || iters <= 0 || !sink || (shape != 0 && shape != 1)) return -1;
     if (shape == 0)
