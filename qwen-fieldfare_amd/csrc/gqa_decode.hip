@@ -522,8 +522,14 @@ int gqa_chunk_cap(const qff_ctx_cfg& cfg, int batch) {
 // Chunks per kv head a call aims for: half a round of resident one-wave
 // workgroups (two per SIMD, 8 per CU) over both kv heads. Measured at
 // context 8192 with random lengths and config 4: 2 x CUs beat 4 x (batch 8
-// 26.6 vs 28.9 us, config 4 at batch 16 3.72 vs 3.81 ms) and 8 x.
-static int gqa_target_chunks(int num_cu) { return 2 * (num_cu > 0 ? num_cu : 256); }
+// 26.6 vs 28.9 us, config 4 at batch 16 3.72 vs 3.81 ms) and 8 x. A single
+// sequence takes 1 x CUs: half the partials for the combine to merge
+// (config 4 at batch 1 and 64K: 999-1000 against 1014-1016 us per step;
+// 0.5 x: 1099 us); at context 8192 both give 32-position chunks.
+static int gqa_target_chunks(int num_cu, int batch) {
+    const int n = num_cu > 0 ? num_cu : 256;
+    return batch == 1 ? n : 2 * n;
+}
 
 hipError_t launch_gqa_decode(qff_ctx* ctx, hipStream_t stream, const qff_gqa_params* p,
                              const void* q_gate, const void* k_new, const void* v_new,
@@ -544,7 +550,7 @@ hipError_t launch_gqa_decode_into(qff_ctx* ctx, const GqaPartials& ws, hipStream
     // the split is derived from the device positions inside the kernels; at
     // most target + batch chunks per kv head (rounding up adds at most one
     // per sequence), so the grid covers every chunk of any length mix
-    const int target = gqa_target_chunks(ws.num_cu);
+    const int target = gqa_target_chunks(ws.num_cu, batch);
     const int units = 2 * (target + batch);
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
