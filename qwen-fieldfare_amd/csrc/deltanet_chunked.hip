@@ -23,12 +23,12 @@
 //       from a work queue, all chunks independent: conv1d + SiLU of the
 //       chunk's q and k channels straight from the projection (3 tokens of
 //       history from the input or the conv state), L2 norms, both value
-//       heads' gates, the Gram products K K^T and Q K^T, then per value head
+//       heads' gates, the Gram products K K^T and K Q^T, then per value head
 //       A, P and T = (I + A)^-1 (16x16 blocks: diagonal blocks by
 //       substitution, the rest on fp32 MFMAs), and the conv1d + SiLU of both
 //       heads' v channels times beta. Writes K (bf16 hi/lo, in the state
-//       pass's LDS image), Q (fp16), T (bf16 hi/lo), P (fp16) as MFMA operand
-//       blocks, beta V and the per-token gate factors.
+//       pass's LDS image), Q, T and P (bf16 hi/lo) as MFMA operand blocks,
+//       beta V and the per-token gate factors.
 //   dn_chunk_state_kernel  one workgroup per (16 state rows, value head)
 //       walks the chunks in order: four chain waves hold the block's state
 //       (key quarters) in accumulators and form X = K S^T, U = T (beta V -
@@ -64,7 +64,6 @@ namespace qff {
 
 constexpr int kC = 64;      // chunk length
 constexpr int kLD = 136;    // bf16 row stride of [64][128] LDS tiles (128 + 8)
-constexpr int kLP = 72;     // fp16 row stride of [64][64] LDS tiles (64 + 8)
 constexpr int kBlk = 512;   // 16-bit elements of one operand block (64 lanes x 8)
 
 constexpr float kLog2e = 1.44269504088896341f;
@@ -236,8 +235,7 @@ constexpr int kTile128 = kC * kLD * 2;            // one [64][136] bf16 array
 constexpr int kOffK = 0;                          // K hi, lo
 constexpr int kOffQ = 2 * kTile128;               // Q hi, lo; then T fp32 [2][64][65]
 constexpr int kOffA = 4 * kTile128;               // A fp32 [2][64][65]
-constexpr int kOffP = kOffA + 2 * kC * 65 * 4;    // P hi, lo: bf16 [2][2][64][72]
-constexpr int kOffS = kOffP + 4 * kC * kLP * 2;   // off-diagonal solve scratch [6][16][17] fp32
+constexpr int kOffS = kOffA + 2 * kC * 65 * 4;    // off-diagonal solve scratch [6][16][17] fp32
 constexpr int kOffG = kOffS + 6 * 16 * 17 * 4;    // G [2][64], beta [2][64]
 constexpr int kLocalSmem = kOffG + 4 * kC * 4;
 static_assert(2 * kC * 65 * 4 <= 2 * kTile128, "T must fit the Q region");
@@ -250,10 +248,12 @@ static_assert(2 * kC * 65 * 4 <= 2 * kTile128, "T must fit the Q region");
 //   gates of both value heads (waves 0, 1; lane = token) -> LDS and out;
 //   conv + SiLU + L2 norm of q and k (wave = 8 tokens, lane = 2 channels)
 //       -> LDS as bf16 hi / lo;
-//   K K^T (waves 0-3) and Q K^T (waves 4-7), one 16-row tile each, then A
-//       and P of both heads from the same accumulators; the next unit's
+//   K K^T (waves 0-3), one 16-row tile each, then A of both heads into LDS;
+//       K Q^T (waves 4-7), one query tile each over every key tile, whose
+//       accumulators are P's operand blocks: P of both heads (decay and
+//       mask applied) straight from registers to global; the next unit's
 //       inputs are requested here;
-//   K image, Q and P blocks out;
+//   K image and Q blocks out;
 //   T = (I + A)^-1 of both heads: the eight diagonal blocks by forward
 //       substitution (one wave each), the off-diagonal blocks by six waves
 //       walking their column block down on fp32 MFMAs;
@@ -278,8 +278,6 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     uint16_t* Ql = Qh + kC * kLD;
     float* Tm = reinterpret_cast<float*>(smem + kOffQ);   // [2][64][65]
     float* Am = reinterpret_cast<float*>(smem + kOffA);   // [2][64][65]
-    uint16_t* Pfh = reinterpret_cast<uint16_t*>(smem + kOffP);   // [2][64][72]
-    uint16_t* Pfl = Pfh + 2 * kC * kLP;
     float* Scr = reinterpret_cast<float*>(smem + kOffS);
     float* Gs = reinterpret_cast<float*>(smem + kOffG);   // [hh][64]
     float* Bs = Gs + 2 * kC;                              // [hh][64]
@@ -402,15 +400,19 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
     if (t == 0) grabbed = atomicAdd(sched, 1u);
     int unn;
 
-    // ---- waves 0-3: K K^T -> A of both heads (strictly lower, scaled);
-    // waves 4-7: Q K^T -> P of both heads (lower incl. diagonal); row tile rt
-    {
+    // ---- waves 0-3: K K^T -> A of both heads (strictly lower, scaled), row
+    // tile rt; waves 4-7: K Q^T for query tile rt over every key tile, whose
+    // accumulators are already P's MFMA A operands (lane (n, g) of key tile
+    // kt holds P[16 rt + n][16 kt + 4g + i]: elements 4(kt & 1) + i of the
+    // block (query tile rt, k step kt / 2)), so the P blocks of both heads
+    // (lower incl. diagonal, decay applied) go out from registers
+    if (role == 0) {
         f32x4_t acc[1][4];
 #pragma unroll
         for (int cj = 0; cj < 4; ++cj) acc[0][cj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        mma_block_x3<128, 1, 4, false>(acc, role ? Qh : Kh, role ? Ql : Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
-        // the next unit's inputs (the unit index is clamped, so the loads stay
-        // in bounds when the queue has run out)
+        mma_block_x3<128, 1, 4, false>(acc, Kh, Kl, kLD, 16 * rt, Kh, Kl, kLD, 0, lane);
+        // the next unit's inputs (the unit index is clamped, so the loads
+        // stay in bounds when the queue has run out)
         unn = s_next;
         fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, wave, lane);
 #pragma unroll
@@ -426,29 +428,53 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             }
 #pragma unroll
             for (int cj = 0; cj < 4; ++cj) {
-                // A is read only on and below its diagonal blocks; P's operand
-                // blocks cover columns 0-31 for row tiles 0, 1
-                if (role == 0 ? cj > rt : (rt < 2 && cj >= 2)) continue;
+                // A is read only on and below its diagonal blocks
+                if (cj > rt) continue;
                 const int j = 16 * cj + n;
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
                     const int i = 16 * rt + 4 * kb + ii;
                     // e^{G_i - G_j}; for j > i the product is discarded by the select
                     const float v = __builtin_amdgcn_exp2f(gi[ii] - gj[cj]) * acc[0][cj][ii];
-                    if (role == 0) {
-                        Am[hh * kC * 65 + i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
-                    } else {
-                        uint16_t ph, pl;
-                        split_bf16(j <= i ? v : 0.0f, ph, pl);
-                        Pfh[hh * kC * kLP + i * kLP + j] = ph;
-                        Pfl[hh * kC * kLP + i * kLP + j] = pl;
-                    }
+                    Am[hh * kC * 65 + i * 65 + j] = j < i ? bi[ii] * v : 0.0f;
                 }
+            }
+        }
+    } else {
+        f32x4_t acc[4][1];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) acc[kt][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        mma_block_x3<128, 4, 1, false>(acc, Kh, Kl, kLD, 0, Qh, Ql, kLD, 16 * rt, lane);
+        unn = s_next;
+        fetch_unit<IN_DT>(in, un < units ? un : u, T, qkv, a, b, a_log, dt_bias, conv_w, wave, lane);
+        const int i = 16 * rt + n;   // this lane's query token
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const float* G = Gs + hh * kC;
+            const float gi = G[i] * kLog2e;
+            uint16_t* po = out.pop + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kPOp + 8 * lane;
+#pragma unroll
+            for (int sj = 0; sj < 2; ++sj) {
+                if (sj > (rt >> 1)) continue;   // blocks tblk(rt, sj), sj <= rt / 2
+                float pv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int kt = 2 * sj + (e >> 2), r = e & 3;
+                    const int j = 16 * kt + 4 * kb + r;
+                    const float v = __builtin_amdgcn_exp2f(gi - G[j] * kLog2e) * acc[kt][0][r];
+                    pv[e] = j <= i ? v : 0.0f;
+                }
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split_bf16x2(pv[2 * q], pv[2 * q + 1], hw[q], lw[q]);
+                uint16_t* pb = po + tblk(rt, sj) * kBlk;
+                *reinterpret_cast<u32x4_t*>(pb) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4_t*>(pb + 6 * kBlk) = u32x4_t{lw[0], lw[1], lw[2], lw[3]};
             }
         }
     }
     __syncthreads();
-    // ---- K image, Q blocks and P blocks (bf16 hi, lo) out ----------------------
+    // ---- K image and Q blocks (bf16 hi, lo) out ----------------------------------
     {
         uint16_t* ko = out.kimg + (static_cast<size_t>(c) * 16 + kh) * kKImg;
 #pragma unroll
@@ -474,19 +500,6 @@ __global__ __launch_bounds__(kLocalThreads) void dn_chunk_local_kernel(
             const u32x2_t l1 = *reinterpret_cast<const u32x2_t*>(Ql + row * kLD + k0 + 16);
             *reinterpret_cast<u32x4_t*>(qo + 8 * pc) = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
             *reinterpret_cast<u32x4_t*>(qo + 16 * kBlk + 8 * pc) = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
-        }
-        for (int pc = t; pc < 2 * 6 * 64; pc += kLocalThreads) {   // [hh][block][lane]
-            const int hh = pc / 384, blk = (pc >> 6) % 6, l = pc & 63;
-            const int tt = blk < 2 ? blk : 2 + ((blk - 2) >> 1), j = blk < 2 ? 0 : (blk - 2) & 1;
-            const int row = 16 * tt + (l & 15), k0 = 32 * j + 4 * (l >> 4);
-            const int so = hh * kC * kLP + row * kLP + k0;
-            const u32x2_t h0 = *reinterpret_cast<const u32x2_t*>(Pfh + so);
-            const u32x2_t h1 = *reinterpret_cast<const u32x2_t*>(Pfh + so + 16);
-            const u32x2_t l0 = *reinterpret_cast<const u32x2_t*>(Pfl + so);
-            const u32x2_t l1 = *reinterpret_cast<const u32x2_t*>(Pfl + so + 16);
-            uint16_t* po = out.pop + (static_cast<size_t>(c) * 32 + 2 * kh + hh) * kPOp + 8 * (pc % 384);
-            *reinterpret_cast<u32x4_t*>(po) = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
-            *reinterpret_cast<u32x4_t*>(po + 6 * kBlk) = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
         }
     }
     __syncthreads();   // Q consumed: its region holds T from here on
