@@ -1,17 +1,19 @@
 """qff_gqa_decode_static, the allocation-free variant of qff_gqa_decode
 (split-KV partials in the library's fixed device array instead of a
-context's workspace), against qff_gqa_decode through the C ABI: two calls in
-a row, the second with a smaller batch and context, each bit-identical with
-the context entry point (same kernels; the context is sized so both split
-the positions the same way), the caches included; oversized batches are
-rejected before anything is launched."""
+context's workspace), against qff_gqa_decode through the C ABI: calls in a
+row, each with a smaller batch and context than the last (batch 1 takes the
+single-sequence split), each bit-identical with the context entry point
+(same kernels; the context is sized so both split the positions the same
+way), the caches included, on bf16 and on fp16 caches; oversized batches
+are rejected before anything is launched."""
 import ctypes
 
 import numpy as np
 import pytest
 import torch
 
-from gpu_util import DEV, bf16_tensor, f32_tensor
+from gpu_util import DEV, bf16_tensor, f16_tensor, f32_tensor
+from oracle import oracle as O
 from qff import synth
 
 pytestmark = pytest.mark.gpu
@@ -25,21 +27,26 @@ def _call_static(prm, qg, kn, vn, kc, vc, pos, out, B, max_ctx):
                                        0, B, max_ctx)
 
 
-def test_gqa_decode_static_matches_context_entry(hip):
+@pytest.mark.parametrize("kv_f16", [0, 1])
+def test_gqa_decode_static_matches_context_entry(hip, kv_f16):
     import qff
     from qff._lib import GqaParams
     p = {k: f32_tensor(v) for k, v in synth.gqa_params().items()}
-    prm = GqaParams(p["q_norm_w"].data_ptr(), p["k_norm_w"].data_ptr(), 1e7, 64, 1.0 / 16, 1e-6)
+    prm = GqaParams(p["q_norm_w"].data_ptr(), p["k_norm_w"].data_ptr(), 1e7, 64, 1.0 / 16, 1e-6, kv_f16)
     # 16 x 2 x 128 = 4096 partial slots: the static array's count, so both
     # entry points pick the same chunk length
     ctx = qff.Context(max_batch=16, max_ctx=8192, max_prefill_tokens=1)
-    for B, max_ctx, seed in ((8, 8192, 1), (3, 2048, 2)):
-        print(f"gqa_decode_static B={B} max_ctx={max_ctx}", flush=True)
+    for B, max_ctx, seed in ((8, 8192, 1), (3, 2048, 2), (1, 1024, 3)):
+        print(f"gqa_decode_static B={B} max_ctx={max_ctx} kv_f16={kv_f16}", flush=True)
         rng = np.random.default_rng(seed)
         inp = synth.gqa_decode_inputs(B, max_ctx, seed=seed, lengths=rng.integers(1, max_ctx + 1, B))
         qg, kn, vn = (bf16_tensor(inp[k]) for k in ("q_gate", "k_new", "v_new"))
         pos = torch.from_numpy(inp["positions"]).to(DEV)
-        kc_a, vc_a = bf16_tensor(inp["k_cache"]), bf16_tensor(inp["v_cache"])
+        if kv_f16:
+            kc_a = f16_tensor(O.f32_to_f16(O.bf16_to_f32(inp["k_cache"])))
+            vc_a = f16_tensor(O.f32_to_f16(O.bf16_to_f32(inp["v_cache"])))
+        else:
+            kc_a, vc_a = bf16_tensor(inp["k_cache"]), bf16_tensor(inp["v_cache"])
         kc_b, vc_b = kc_a.clone(), vc_a.clone()
         ref = qff.gqa_decode(ctx, p, qg, kn, vn, kc_a, vc_a, pos, out_dtype=torch.float32)
         out = torch.full((B, 16, 256), float("nan"), device=DEV)
