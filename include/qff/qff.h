@@ -59,8 +59,10 @@ typedef struct qff_ctx_cfg {
     int max_batch;           /* largest decode batch                        */
     int max_ctx;             /* largest KV context a decode call may attend,
                                 and the largest start_pos + T of a prefill
-                                over a bf16 cache (whose fp16 copy, 2 KB per
-                                position, the workspace holds)              */
+                                (the workspace holds the copies of the cache
+                                that the prefill attention reads: V
+                                transposed, and the fp16 K of a bf16 cache;
+                                2 KB per position)                          */
     int max_prefill_tokens;  /* largest T of a prefill call                 */
 } qff_ctx_cfg;
 
@@ -312,9 +314,9 @@ int qff_gqa_decode_static(qff_stream_t stream, const qff_gqa_params* p, const vo
  *   k_cache, v_cache [max_ctx, 2, 256] bf16 (fp16 with p->kv_f16);
  *   out [T, 16, 256] (out_dtype).
  * QFF_ERR_INVALID_ARG when start_pos + T > max_ctx; QFF_ERR_WORKSPACE when T
- * exceeds the context's max_prefill_tokens, or, for a bf16 cache, when
- * start_pos + T exceeds the context's max_ctx (the attention reads an fp16
- * copy of the cache kept in the workspace). */
+ * exceeds the context's max_prefill_tokens or start_pos + T exceeds the
+ * context's max_ctx (the attention reads copies of the cache kept in the
+ * workspace: V transposed, and the fp16 K of a bf16 cache). */
 int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p,
                     const void* q_gate, const void* k, const void* v,
                     qff_dtype in_dtype, void* k_cache, void* v_cache,

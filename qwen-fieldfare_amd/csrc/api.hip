@@ -37,7 +37,8 @@ WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg) {
     L.gqa_d = take(S * 8 * sizeof(float));
     L.gqa_o = take(S * 8 * 256 * sizeof(float));
     L.gqa_qb = take(T * 16 * 256 * sizeof(uint16_t));
-    L.gqa_kv16 = take(static_cast<size_t>(cfg.max_ctx) * 2 * 512 * sizeof(uint16_t));
+    L.gqa_kv16 = take(static_cast<size_t>(cfg.max_ctx) * 512 * sizeof(uint16_t));
+    L.gqa_vt = take(static_cast<size_t>((cfg.max_ctx + 63) / 64) * 64 * 512 * sizeof(uint16_t));
     L.q4_x16 = take(static_cast<size_t>(q4_xs_tokens(cfg)) * 4096 * sizeof(uint16_t));
     L.q4_fm = take(static_cast<size_t>(q4_xs_tokens(cfg)) * sizeof(float));
     L.q4_sk_part = take(static_cast<size_t>(kQ4SkSlots) * 16 * 64 * sizeof(float));
@@ -163,6 +164,7 @@ int qff_ctx_create(qff_ctx** out, int device, const qff_ctx_cfg* cfg) {
     auto u16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(base + off); };
     c->gqa_qb = u16(L.gqa_qb);
     c->gqa_kv16 = u16(L.gqa_kv16);
+    c->gqa_vt = u16(L.gqa_vt);
     c->q4_x16 = reinterpret_cast<uint16_t*>(base + L.q4_x16);
     c->q4_fm = reinterpret_cast<float*>(base + L.q4_fm);
     c->q4_xs_tokens = q4_xs_tokens(c->cfg);
@@ -386,8 +388,9 @@ int qff_gqa_prefill(qff_ctx* ctx, qff_stream_t stream, const qff_gqa_params* p, 
     if (T <= 0 || start_pos < 0 || max_ctx <= 0) return QFF_ERR_INVALID_ARG;
     if (static_cast<long long>(start_pos) + T > max_ctx) return QFF_ERR_INVALID_ARG;
     if (T > ctx->cfg.max_prefill_tokens) return QFF_ERR_WORKSPACE;   // the staged q rows hold that many tokens
-    // the fp16 copy of a bf16 cache holds the context's max_ctx rows
-    if (!p->kv_f16 && static_cast<long long>(start_pos) + T > ctx->cfg.max_ctx) return QFF_ERR_WORKSPACE;
+    // the cache copies the attention reads (fp16 K of a bf16 cache, V
+    // transposed) hold the context's max_ctx rows
+    if (static_cast<long long>(start_pos) + T > ctx->cfg.max_ctx) return QFF_ERR_WORKSPACE;
     QFF_CHECK_HIP(launch_gqa_prefill(ctx, stream, p, q_gate, k, v, in_dtype, k_cache, v_cache, start_pos,
                                      out, out_dtype, T, max_ctx));
     return QFF_OK;

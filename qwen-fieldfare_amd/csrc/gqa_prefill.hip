@@ -9,31 +9,32 @@
 //          16 q heads (fp16, softmax scale folded in, to workspace: the
 //          reference also rounds q to half, Runner:1119-1126) and of the 2 k
 //          heads (appended to the cache, bf16 or fp16, together with v; a
-//          bf16 cache's new rows also go to its fp16 copy in workspace, whose
-//          older rows kv16_copy fills).
+//          bf16 cache's new k rows also go to its fp16 copy in workspace,
+//          whose older rows k16_copy fills).
+//   vt     the transposed fp16 copy of V (per kv head and 64-position tile,
+//          dims x positions), so that the attention's V operand is one
+//          16-byte LDS read per lane.
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; four wave pairs of 32 rows = 4 tokens
 //          x 8 heads, each wave scoring half of a tile's positions and
 //          accumulating half of the output dims, so accumulators and q stay
 //          in VGPRs and two waves share each SIMD) and walks 64-position
-//          K/V tiles copied from the fp16 cache (or the fp16 copy of a bf16
-//          one: exact for the cache's values) straight into LDS
-//          (double-buffered, XOR-swizzled rows, no registers),
-//          so both products run on fp16 operands: S^T = K Q^T on 16x16x32
-//          fp16 MFMAs (q keeps the 11-bit significand the reference gives
-//          it, where bf16 q puts rare outputs beyond the output tolerance
-//          once logits reach ~15); softmax in
-//          base 2 (q carries scale * log2 e), with the running max raised
-//          only when a tile exceeds it by more than 2^8, so the O rescale is
-//          rare; causal masking only on the tiles that reach past the
-//          block's first token. O += P V with 16x16x32 fp16 MFMAs (P in
-//          fp16, 8x finer than bf16) whose 32-deep k
-//          runs over the tile's positions in the order the S^T registers
-//          hold them; the V operand comes from the row-major tile through the
-//          LDS transpose read. The eight waves run as two groups one phase
-//          apart (MFMA phase / softmax phase, see the kernel). Query blocks
-//          are issued last-first so the longest rows start earliest. The
-//          epilogue divides by the row sums and applies the sigmoid gate.
+//          tiles of K (from the fp16 cache, or the fp16 copy of a bf16 one:
+//          exact for the cache's values) and of V^T, copied straight into
+//          LDS (double-buffered, XOR-swizzled rows, no registers), so both
+//          products run on fp16 operands in the transposed orientation on
+//          32x32x16 MFMAs: S^T = K Q^T (q keeps the 11-bit significand the
+//          reference gives it, where bf16 q puts rare outputs beyond the
+//          output tolerance once logits reach ~15) and O^T = V^T P^T (P in
+//          fp16, 8x finer than bf16), each lane owning one q row of both.
+//          Softmax in base 2 (q carries scale * log2 e), with the running
+//          max raised only when a tile exceeds it by more than 2^8, so the
+//          O rescale is rare; causal masking only on the tiles that reach
+//          past the block's first token. The eight waves run as two groups
+//          one phase apart (MFMA phase / softmax phase, see the kernel).
+//          Query blocks are issued last-first so the longest rows start
+//          earliest. The epilogue divides by the row sums and applies the
+//          sigmoid gate.
 #include "common.hpp"
 #include "internal.hpp"
 #include "mfma.hpp"
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, int start, int T, uint16_t* __restrict__ qb, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, uint16_t* __restrict__ k16, uint16_t* __restrict__ v16) {
+    uint16_t* __restrict__ v_cache, uint16_t* __restrict__ k16) {
     const int lane = threadIdx.x & 63;
     const int tok = blockIdx.x * kPrepWaves + (threadIdx.x >> 6);
     if (tok >= T) return;
@@ -131,56 +132,93 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
                     *reinterpret_cast<u32x2_t*>(v_cache + off) =
                         u32x2_t{pack_f16x2(vv[kvh][0], vv[kvh][1]), pack_f16x2(vv[kvh][2], vv[kvh][3])};
                 } else {
-                    // the bf16 entries, and their fp16 copy for the attention kernel
+                    // the bf16 entries, and the k entries' fp16 copy for the attention kernel
                     const u32x2_t kw2 = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-                    const u32x2_t vw2 = u32x2_t{pack_bf16x2(vv[kvh][0], vv[kvh][1]), pack_bf16x2(vv[kvh][2], vv[kvh][3])};
                     *reinterpret_cast<u32x2_t*>(k_cache + off) = kw2;
-                    *reinterpret_cast<u32x2_t*>(v_cache + off) = vw2;
+                    *reinterpret_cast<u32x2_t*>(v_cache + off) =
+                        u32x2_t{pack_bf16x2(vv[kvh][0], vv[kvh][1]), pack_bf16x2(vv[kvh][2], vv[kvh][3])};
                     *reinterpret_cast<u32x2_t*>(k16 + off) = u32x2_t{bf16x2_to_f16x2(kw2[0]), bf16x2_to_f16x2(kw2[1])};
-                    *reinterpret_cast<u32x2_t*>(v16 + off) = u32x2_t{bf16x2_to_f16x2(vw2[0]), bf16x2_to_f16x2(vw2[1])};
                 }
             }
         }
     }
 }
 
-// The fp16 copy of bf16 cache rows 0 .. n-1 (both kv heads, K and V): one
-// 16-byte piece of each per thread.
-__global__ __launch_bounds__(256) void kv16_copy_kernel(const uint16_t* __restrict__ kc,
-                                                        const uint16_t* __restrict__ vc, uint16_t* __restrict__ k16,
-                                                        uint16_t* __restrict__ v16, int pieces) {
+// The fp16 copy of bf16 K cache rows 0 .. n-1 (both kv heads): one 16-byte
+// piece per thread.
+__global__ __launch_bounds__(256) void k16_copy_kernel(const uint16_t* __restrict__ kc, uint16_t* __restrict__ k16,
+                                                       int pieces) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= pieces) return;
     const size_t o = static_cast<size_t>(i) * 8;
     *reinterpret_cast<u32x4_t*>(k16 + o) = bf16x8_to_f16x8(*reinterpret_cast<const u32x4_t*>(kc + o));
-    *reinterpret_cast<u32x4_t*>(v16 + o) = bf16x8_to_f16x8(*reinterpret_cast<const u32x4_t*>(vc + o));
+}
+
+// The transposed fp16 copy of V cache rows 0 .. n-1, per kv head and
+// 64-row tile a [256 dims][64 slots] block (the tile's 32 KB contiguous,
+// tiles of one kv head ntile_stride apart). Within each 16 slots, slot
+// 8h + 4j + i holds row 8j + 4h + i (bits 2 and 3 swapped): the order in
+// which the attention's O^T = V^T P^T operand runs over positions, so a
+// lane's eight positions are one 16-byte piece. Rows >= n are zero. A block
+// of 256 threads stages one tile through LDS.
+__device__ __forceinline__ int vt_slot_row(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
+
+template <int KV_F16>
+__global__ __launch_bounds__(256) void vt_copy_kernel(const uint16_t* __restrict__ vc, uint16_t* __restrict__ vt,
+                                                      int n, int ntile_stride) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64][264];   // rows x dims (+8 pad)
+    const int tl = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
+    const int p0 = tl * 64;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = t + 256 * i, row = q >> 5, pc = q & 31;
+        u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+        if (p0 + row < n) {
+            v = *reinterpret_cast<const u32x4_t*>(vc + (static_cast<size_t>(p0 + row) * 2 + kvh) * 256 + 8 * pc);
+            if (!KV_F16) v = bf16x8_to_f16x8(v);
+        }
+        *reinterpret_cast<u32x4_t*>(&tile[row][8 * pc]) = v;
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<size_t>(kvh) * ntile_stride + tl) * (256 * 64);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = t + 256 * i, d = q >> 3, sp = q & 7;   // dim d, slots 8 sp .. 8 sp + 7
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k)][d]) |
+                   (static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k + 1)][d]) << 16);
+        *reinterpret_cast<u32x4_t*>(dst + d * 64 + 8 * sp) = u32x4_t{w[0], w[1], w[2], w[3]};
+    }
 }
 
 constexpr int kPfThreads = 512;
 
-// K and V tiles in LDS: 64 rows of 256 fp16 (512 B) without padding, the
-// 16-byte pieces of row r XOR-permuted by swz(r): piece j of the row sits at
-// j ^ swz(r). A K operand read (16 rows x one piece) and a V transpose read
-// (16 rows x 2 pieces per 32 lanes) then each meet every bank group equally.
-__device__ __forceinline__ int kv_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// K tiles in LDS: 64 rows of 256 fp16 (512 B) without padding, piece j
+// (16 bytes) of row r at j ^ k_swz(r); V^T tiles: 256 rows (dims) of 64
+// slots (128 B), piece j of row d at j ^ vt_swz(d). A K operand read (32
+// rows x one piece per 32 lanes) and a V^T operand read (32 rows x one
+// piece) then each meet every bank group equally.
+__device__ __forceinline__ int k_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int vt_swz(int d) { return (d >> 1) & 7; }
 
-// One wave's 1-KB chunk c (rows 2c, 2c + 1) of a 64-row tile, copied from
+// One wave's 1-KB chunk c (rows 2c, 2c + 1) of a 64-row K tile, copied from
 // the fp16 cache rows p0 + 2c, p0 + 2c + 1 straight into LDS: lane l fills
 // LDS piece l % 32 of row 2c + h (h = l / 32) with global piece
-// (l % 32) ^ swz(2c + h) = (l % 32) ^ 2h ^ U(c), U(c) = swz(2c) (2c is even,
-// so swz(2c + h) = swz(2c) + 2h with bit 1 of swz(2c) clear): a lane term
-// XORed with a uniform one, added to the uniform row base. Only the tile
-// that reaches kv_end (tail) clamps rows at kv_end - 1 (finite data; their
-// scores are masked).
+// (l % 32) ^ k_swz(2c + h) = (l % 32) ^ 2h ^ k_swz(2c) (bit 1 of k_swz(2c) is
+// clear): a lane term XORed with a uniform one, added to the uniform row
+// base. Only the tile that reaches kv_end (tail) clamps rows at kv_end - 1
+// (finite data; their scores are masked).
 template <bool TAIL>
-__device__ __forceinline__ void kv_chunk_to_lds(const uint16_t* __restrict__ src, int kvh, int p0, int kv_end,
-                                                uint16_t* tile, int c, int lane) {
+__device__ __forceinline__ void k_chunk_to_lds(const uint16_t* __restrict__ src, int kvh, int p0, int kv_end,
+                                               uint16_t* tile, int c, int lane) {
     const int h = lane >> 5;
     // (redefined for the compiler at each chunk, so the offsets of all the
     // chunks are not formed ahead and held in registers)
     unsigned lt = 1024u * h + 16u * ((lane & 31) ^ (2 * h));
     asm volatile("" : "+v"(lt));
-    const unsigned poff = lt ^ (16u * kv_swz(2 * c));
+    const unsigned poff = lt ^ (16u * k_swz(2 * c));
     const char* g;
     if constexpr (TAIL) {
         const int p = min(p0 + 2 * c + h, kv_end - 1);
@@ -192,16 +230,35 @@ __device__ __forceinline__ void kv_chunk_to_lds(const uint16_t* __restrict__ src
                                      (__attribute__((address_space(3))) void*)(tile + 512 * c), 16, 0, 0);
 }
 
-// Chunks c0, c0 + step, ... (n of them) of the tile at rows p0 .. p0 + 63.
+// Chunks c0, c0 + step, ... (N of them) of the K tile at rows p0 .. p0 + 63.
 template <int N>
-__device__ __forceinline__ void kv_tile_to_lds(const uint16_t* __restrict__ src, int kvh, int p0, int kv_end,
-                                               uint16_t* tile, int c0, int step, int lane) {
+__device__ __forceinline__ void k_tile_to_lds(const uint16_t* __restrict__ src, int kvh, int p0, int kv_end,
+                                              uint16_t* tile, int c0, int step, int lane) {
     if (p0 + kPfKT > kv_end) {
 #pragma unroll
-        for (int i = 0; i < N; ++i) kv_chunk_to_lds<true>(src, kvh, p0, kv_end, tile, c0 + step * i, lane);
+        for (int i = 0; i < N; ++i) k_chunk_to_lds<true>(src, kvh, p0, kv_end, tile, c0 + step * i, lane);
     } else {
 #pragma unroll
-        for (int i = 0; i < N; ++i) kv_chunk_to_lds<false>(src, kvh, p0, kv_end, tile, c0 + step * i, lane);
+        for (int i = 0; i < N; ++i) k_chunk_to_lds<false>(src, kvh, p0, kv_end, tile, c0 + step * i, lane);
+    }
+}
+
+// Chunks c0, c0 + step, ... (N of them; chunk c = dims 8c .. 8c + 7) of the
+// V^T tile at src (32 KB), copied straight into LDS: lane l fills LDS piece
+// l % 8 of row 8c + l / 8 with global piece (l % 8) ^ vt_swz(8c + l / 8) =
+// (l % 8) ^ (l / 16) ^ 4 (c % 2). The copy is whole (rows past the cache
+// end are zero), so no clamping.
+template <int N>
+__device__ __forceinline__ void vt_tile_to_lds(const uint16_t* __restrict__ src, uint16_t* tile, int c0, int step,
+                                               int lane) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int c = c0 + step * i;
+        unsigned lt = 128u * (lane >> 3) + 16u * ((lane & 7) ^ (lane >> 4));
+        asm volatile("" : "+v"(lt));
+        const char* g = reinterpret_cast<const char*>(src) + 1024 * c + (lt ^ (64u * (c & 1)));
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)(tile + 512 * c), 16, 0, 0);
     }
 }
 
@@ -214,208 +271,190 @@ __device__ __forceinline__ void phase_barrier() {
 }
 
 // grid (ceil(T/16), 2 kv heads), 512 threads: four wave pairs, pair pr
-// owning the 32 rows of tokens t0 + 4 pr .. t0 + 4 pr + 3 (x the 8 q heads)
-// as two 16-row tiles. Wave e of a pair scores positions 32e .. 32e + 31 of
-// each K tile for both row tiles (each K operand read from LDS feeds two
-// MFMAs), the pair meets once for the row maxima and once for the P
-// operands (through LDS), and wave e accumulates output dims
-// 128e .. 128e + 127 over all 64 positions (each V operand feeds two MFMAs):
-// 34 KB of LDS reads per wave and tile instead of the 64 KB a wave of 16
-// rows scoring every position and accumulating every dim would need.
+// owning the 32 q rows r = 8 tt + hh (token t0 + 4 pr + tt, head hh of the
+// kv head's 8). Lane l holds row l % 32 throughout. Wave e of a pair scores
+// positions 32e .. 32e + 31 of each K tile, S^T = K Q^T on 32x32x16 fp16
+// MFMAs (A = 32 K rows x 16 dims from LDS, B = the row's q in registers),
+// the pair meets once for the row maxima and once for the P operands
+// (through LDS), and wave e accumulates output dims 128e .. 128e + 127 over
+// all 64 positions, O^T = V^T P^T (A = 32 dims x 16 positions of the V^T
+// tile in LDS, B = P^T straight from the S^T accumulators: a lane's
+// S^T registers and O^T registers belong to its one q row, so the rescale
+// needs no lane exchange). Each K operand read feeds 32 rows, each V
+// operand read 32 rows: 32 KB of LDS reads per wave and tile.
 //
 // Schedule: two phases per tile between workgroup barriers -- M(j), on the
-// MFMAs: S^T of tile j+1 interleaved with O += P V of tile j (20
-// independent accumulator chains, operands read two steps ahead); V(j+1),
-// on the VALU: the softmax of tile j+1 -- with waves 4-7 (group 1) one
-// phase behind waves 0-3 (group 0): group 1 passes one barrier more at the
-// start, group 0 one more at the end. Waves w and w + 4 share a SIMD, so
-// while one issues MFMAs the other runs its softmax. Slots: group 0
-// computes S_j in slot 2j and P V_j in slot 2j+2, group 1 one slot later, so
-// K_j is read in slots 2j, 2j+1 and V_j in 2j+2, 2j+3. The tiles go from the
-// fp16 cache (or its fp16 copy) straight into LDS, requested by group 1 in
-// its V(m) (slot 2m+2): K_{m+2} into the buffer whose K_m was last read in
-// 2m+1, V_{m+1} into the one whose V_{m-1} was last read in 2m+1; group 1
-// waits for them at the end of its next M phase (slot 2m+3), before both
-// are first read (slot 2m+4).
+// MFMAs: S^T of tile j+1 interleaved with O^T += V^T P^T of tile j
+// (operands read three steps ahead); V(j+1), on the VALU: the softmax of
+// tile j+1 -- with waves 4-7 (group 1) one phase behind waves 0-3 (group
+// 0): group 1 passes one barrier more at the start, group 0 one more at the
+// end. Waves w and w + 4 share a SIMD, so while one issues MFMAs the other
+// runs its softmax. Slots: group 0 computes S_j in slot 2j and P V_j in
+// slot 2j+2, group 1 one slot later, so K_j is read in slots 2j, 2j+1 and
+// V_j in 2j+2, 2j+3. The K tiles (from the fp16 cache or its fp16 copy)
+// and the V^T tiles (from the transposed copy) go straight into LDS,
+// requested by group 1 in its V(m) (slot 2m+2): K_{m+2}
+// into the buffer whose K_m was last read in 2m+1, V_{m+1} into the one
+// whose V_{m-1} was last read in 2m+1; group 1 waits for them at the end of
+// its next M phase (slot 2m+3), before both are first read (slot 2m+4).
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const uint16_t* __restrict__ qb, const void* __restrict__ q_gate, const uint16_t* __restrict__ k16,
-    const uint16_t* __restrict__ v16, int start, int T, void* __restrict__ out) {
+    const uint16_t* __restrict__ vt, int vt_stride, int start, int T, void* __restrict__ out) {
     __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][kPfKT * 256];
-    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][kPfKT * 256];
-    __shared__ float xrow[kPfThreads / 64][2][16];                              // per wave, row tile, row
-    __shared__ __attribute__((aligned(16))) u32x4_t xp[kPfThreads / 64][2][64];  // per wave, row tile, lane
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][kPfKT * 256];   // V^T tiles
+    __shared__ float xrow[kPfThreads / 64][32];                                  // per wave, q row
+    __shared__ __attribute__((aligned(16))) u32x4_t xp[kPfThreads / 64][2][64];  // per wave, chunk, lane
     const int nqb = (T + kPfQB - 1) / kPfQB;
     const int q_blk = nqb - 1 - static_cast<int>(blockIdx.x);
     const int kvh = blockIdx.y;
     const int t0 = q_blk * kPfQB;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = lane & 15, kb = lane >> 4;
-    const int pr = wave >> 1, e = wave & 1, partner = wave ^ 1;
     const int wv = __builtin_amdgcn_readfirstlane(wave);   // the same, known uniform
     const int grp = wv >> 2;
+    const int r = lane & 31, h = lane >> 5;
+    const int pr = wave >> 1, e = wave & 1, partner = wave ^ 1;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
 
-    // this lane's q rows: row tile rt = token t0 + 4 pr + 2 rt + n/8, head n%8
-    u32x4_t qreg[2][8];
-    int lim[2];
+    // the lane's q row: token t0 + 4 pr + r / 8, head r % 8; B operand of S
+    // step s = dims 16s + 8h .. +7
+    const int tok_q = min(t0 + 4 * pr + (r >> 3), T - 1);
+    const int lim = start + tok_q;
+    u32x4_t qreg[16];
+    {
+        const uint16_t* qrow = qb + (static_cast<size_t>(tok_q) * 16 + kvh * 8 + (r & 7)) * 256 + 8 * h;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int tok_q = min(t0 + 4 * pr + 2 * rt + (n >> 3), T - 1);
-        lim[rt] = start + tok_q;
-        const uint16_t* qrow = qb + (static_cast<size_t>(tok_q) * 16 + kvh * 8 + (n & 7)) * 256;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) qreg[rt][jj] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * jj + 8 * kb);
+        for (int s = 0; s < 16; ++s) qreg[s] = *reinterpret_cast<const u32x4_t*>(qrow + 16 * s);
         // consumed here (no instruction) so the loads are not sunk into the loop
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) asm volatile("" ::"v"(qreg[rt][jj]));
+        for (int s = 0; s < 16; ++s) asm volatile("" ::"v"(qreg[s]));
     }
     const int kv_end = start + min(T, t0 + kPfQB);
     const int ntiles = (kv_end + kPfKT - 1) / kPfKT;
     const int first_masked = (start + t0) / kPfKT;   // tiles before this need no causal mask
 
-    float m_run[2] = {-INFINITY, -INFINITY}, d_run[2] = {0.0f, 0.0f};
-    f32x4_t oacc[2][8];
+    float m_run = -INFINITY, d_run = 0.0f;   // of the lane's row (the same in lanes r, r + 32)
+    f32x16_t oacc[4];                        // O^T tile dt: dims 128e + 32dt + 8(i/4) + 4h + i%4
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int jd = 0; jd < 8; ++jd) oacc[rt][jd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.0f;
 
     // K_0, V_0 and K_1 by every wave (32 chunks each, 4 a wave)
-    kv_tile_to_lds<4>(k16, kvh, 0, kv_end, Ks[0], wv, 8, lane);
-    kv_tile_to_lds<4>(v16, kvh, 0, kv_end, Vs[0], wv, 8, lane);
-    if (ntiles > 1) kv_tile_to_lds<4>(k16, kvh, kPfKT, kv_end, Ks[1], wv, 8, lane);
+    // this kv head's V^T tiles (64 x 256 fp16 each)
+    const uint16_t* __restrict__ vth = vt + static_cast<size_t>(kvh) * vt_stride * (kPfKT * 256);
+    k_tile_to_lds<4>(k16, kvh, 0, kv_end, Ks[0], wv, 8, lane);
+    vt_tile_to_lds<4>(vth, Vs[0], wv, 8, lane);
+    if (ntiles > 1) k_tile_to_lds<4>(k16, kvh, kPfKT, kv_end, Ks[1], wv, 8, lane);
     // every load so far (q included) has landed
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (grp) phase_barrier();   // group 1 runs one phase behind
 
     const int kp = 32 * e;      // the wave's first scored position in a tile
-    f32x4_t s[2][2];            // S^T of the tile whose softmax comes next
-    u32x4_t pa[2];              // the wave's P operands of the current tile
+    f32x16_t sacc;              // S^T of the tile whose softmax comes next: position kp + 8(i/4) + 4h + i%4
+    u32x4_t pa[2];              // the wave's P^T operands of the current tile (positions kp + 16m ..)
 
-    // S^T = K Q^T of tile kt for the wave's two 16-position tiles x both row
-    // tiles (32 dims a step), optionally interleaved with O += P V of tile
-    // kt - 1 (four MFMAs of each a step); the masked row maxima of the
+    // M phase of tile kt: S^T of tile kt (16 steps of 16 dims, two
+    // accumulators so consecutive steps are independent) and O^T += V^T P^T
+    // of tile kt - 1 (16 steps: the wave's own chunks, then the partner's,
+    // c = v / 8, m = (v / 4) % 2, dt = v % 4); the masked row maxima of the
     // wave's 32 positions go to the partner
     auto mphase = [&](auto with_s, auto with_pv, int kt) {
         constexpr bool WS = decltype(with_s)::value, WPV = decltype(with_pv)::value;
-        // the lane's K rows kp + 16pt + n (swz = kv_swz(n)), piece 4st + kb:
-        // element (kp + n) 256 + 8 ((kb ^ swz) ^ 4st) = kidx ^ 32st
+        // K operand of step s: row kp + r, piece 2s + h -> element
+        // (kp + r) 256 + 8 ((h ^ k_swz(r)) ^ 2s) = kidx ^ 16s
         const uint16_t* kbuf = Ks[kt & 1];
-        const int kidx = (kp + n) * 256 + 8 * (kb ^ kv_swz(n));
-        // PV of tile kt - 1: B operand through the LDS transpose read, lane
-        // s of group kb at position 32c + 16h + 4kb + s/4, dims 128e + 16jd +
-        // 4(s%4); A = the wave's own P (c = e), then the partner's (c = 1-e)
-        // (rows 4kb + n/4 + 16h + 32c all permute by vr = kv_swz(4kb + n/4); the
-        // lane's 4 dims are piece 16e + 2jd + (n%4)/2, half n%2 of it)
-        // element (4kb + n/4) 256 + 128e + 8 (vx ^ 2jd) + 4 (n%2) = vidx ^ 16jd
+        const int kidx = (kp + r) * 256 + 8 * (h ^ k_swz(r));
+        // V^T operand of PV step v: row (dim) 128e + 32dt + r, slots
+        // 32c' + 16m + 8h .. +7 (c' = e for the own chunks, 1 - e for the
+        // partner's; positions 32c' + 16m + 8j + 4h + i for k = 8h + 4j + i),
+        // piece 4c' + 2m + h permuted by vt_swz(r) -> element
+        // (vidx ^ (32c' + 16m)) + 2048 dt
         const uint16_t* vbuf = Vs[(kt + 1) & 1];
-        const int vidx = (4 * kb + (n >> 2)) * 256 + 128 * e + 4 * (n & 1) +
-                         8 * (((n & 3) >> 1) ^ kv_swz(4 * kb + (n >> 2)));
-        u32x4_t A1[2];   // the partner's P operands, read for PV steps 4 .. 7
+        const int vidx = (128 * e + r) * 64 + 8 * (h ^ vt_swz(r));
+        u32x4_t A1[2];   // the partner's P^T operands, read for PV steps 8 .. 15
         auto load_a1 = [&]() {
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) A1[rt] = xp[partner][rt][lane];
+            for (int m = 0; m < 2; ++m) A1[m] = xp[partner][m][lane];
         };
-        // S step st: dims 32st .. 32st + 31; PV step st: c = st / 4 (the wave's
-        // own P, then the partner's), dims 16jd, jd = 2 (st % 4) + 0, 1. Each
-        // operand is read kLead steps before its MFMAs, into rings of kLead + 1.
-        // (The lane indices are redefined, as far as the compiler knows, at
-        // every step, so each step's XOR is formed next to its reads instead
-        // of all of them being held in registers across the loop.)
         constexpr int kLead = 3, kRing = kLead + 1;
-        u32x4_t ka[kRing][2];
-        u32x2_t va[kRing][4];
+        u32x4_t ka[kRing];
+        u32x4_t va[kRing];
+        // (the lane indices are redefined, as far as the compiler knows, at
+        // every step, so each step's XOR is formed next to its reads instead
+        // of all of them being held in registers across the loop)
         auto load_k = [&](int st) {
             int ki = kidx;
             asm volatile("" : "+v"(ki));
-            ki ^= 32 * st;
-#pragma unroll
-            for (int pt = 0; pt < 2; ++pt)
-                ka[st % kRing][pt] = *reinterpret_cast<const u32x4_t*>(kbuf + ki + 16 * pt * 256);
+            ka[st % kRing] = *reinterpret_cast<const u32x4_t*>(kbuf + (ki ^ (16 * st)));
         };
-        auto load_v = [&](int st) {
-            const int cc = st >> 2, jd0 = 2 * (st & 3);
-            const uint16_t* vb = vbuf + 32 * (cc == 0 ? e : 1 - e) * 256;
+        auto load_v = [&](int v) {
+            const int cc = v >> 3, m = (v >> 2) & 1, dt = v & 3;
             int vi = vidx;
             asm volatile("" : "+v"(vi));
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int o = vi ^ (16 * (jd0 + jj));
-                va[st % kRing][2 * jj] = lds_read_tr16(vb + o);
-                va[st % kRing][2 * jj + 1] = lds_read_tr16(vb + 16 * 256 + o);
-            }
+            vi ^= 32 * (cc == 0 ? e : 1 - e) + 16 * m;
+            va[v % kRing] = *reinterpret_cast<const u32x4_t*>(vbuf + vi + 2048 * dt);
         };
+        f32x16_t s1;
         auto mfma_s = [&](int st) {
-#pragma unroll
-            for (int pt = 0; pt < 2; ++pt)
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) s[rt][pt] = mfma_16x16x32_f16(ka[st % kRing][pt], qreg[rt][st], s[rt][pt]);
+            if (st & 1) s1 = mfma_32x32x16_f16(ka[st % kRing], qreg[st], s1);
+            else sacc = mfma_32x32x16_f16(ka[st % kRing], qreg[st], sacc);
         };
-        auto mfma_pv = [&](int st) {
-            const int cc = st >> 2, jd0 = 2 * (st & 3);
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const u32x4_t B = u32x4_t{va[st % kRing][2 * jj][0], va[st % kRing][2 * jj][1], va[st % kRing][2 * jj + 1][0],
-                                          va[st % kRing][2 * jj + 1][1]};
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-                    oacc[rt][jd0 + jj] = mfma_16x16x32_f16(cc == 0 ? pa[rt] : A1[rt], B, oacc[rt][jd0 + jj]);
-            }
+        auto mfma_pv = [&](int v) {
+            const int cc = v >> 3, m = (v >> 2) & 1, dt = v & 3;
+            oacc[dt] = mfma_32x32x16_f16(va[v % kRing], cc == 0 ? pa[m] : A1[m], oacc[dt]);
         };
         // masked row maxima of S^T over the wave's 32 positions, to the partner
         auto row_max = [&]() {
+            sacc += s1;
             if (kt >= first_masked) {   // (uniform) the tiles that reach the block's first token
-                const int p0 = kt * kPfKT;
+                const int p0 = kt * kPfKT + kp + 4 * h;
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                    for (int pt = 0; pt < 2; ++pt)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (p0 + kp + 16 * pt + 4 * kb + i > lim[rt]) s[rt][pt][i] = -INFINITY;
+                for (int i = 0; i < 16; ++i)
+                    if (p0 + 8 * (i >> 2) + (i & 3) > lim) sacc[i] = -INFINITY;
             }
-            // over the lanes n, n + 16, n + 32, n + 48 on the permlane swaps
-            // (VALU; an LDS permute would queue behind the operand reads)
+            float tm = sacc[0];
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                float tm = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
-                                 fmaxf(fmaxf(s[rt][1][0], s[rt][1][1]), fmaxf(s[rt][1][2], s[rt][1][3])));
-                const auto h16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tm), __float_as_uint(tm), false, false);
-                tm = fmaxf(__uint_as_float(h16[0]), __uint_as_float(h16[1]));
-                const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tm), __float_as_uint(tm), false, false);
-                tm = fmaxf(__uint_as_float(h32[0]), __uint_as_float(h32[1]));
-                if (kb == 0) xrow[wave][rt][n] = tm;
-            }
+            for (int i = 1; i < 16; ++i) tm = fmaxf(tm, sacc[i]);
+            // with the other half of the wave's positions (lane r + 32) on the
+            // permlane swap (VALU; an LDS permute would queue behind the
+            // operand reads)
+            const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tm), __float_as_uint(tm), false, false);
+            tm = fmaxf(__uint_as_float(h32[0]), __uint_as_float(h32[1]));
+            if (h == 0) xrow[wave][r] = tm;
         };
         if constexpr (WS) {
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int pt = 0; pt < 2; ++pt) s[rt][pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < 16; ++i) {
+                sacc[i] = 0.0f;
+                s1[i] = 0.0f;
+            }
         }
         if constexpr (WS && WPV) {
-            // step u: S_u (u < 8) and PV_{u-2} (u >= 2), so S is done two steps
-            // before the end and its row maxima run beside the last PV MFMAs;
-            // K of S_{u+3} and V of PV_{u+1} are read at step u
+            // step u: S step u (u < 16) and PV step u - 2 (u >= 2), so S is
+            // done two steps before the end and its row maxima run beside the
+            // last PV MFMAs; K of S step u + kLead and V of PV step
+            // u + kLead - 2 are read at step u
 #pragma unroll
             for (int st = 0; st < kLead; ++st) load_k(st);
-            load_v(0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLead + 4, 0);
 #pragma unroll
-            for (int u = 0; u < 10; ++u) {
-                if (u + kLead < 8) load_k(u + kLead);
-                if (u + 1 < 8) load_v(u + 1);
-                if (u == 4) load_a1();
-                if (u < 8) mfma_s(u);
+            for (int v = 0; v < kLead - 2; ++v) load_v(v);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLead - 2, 0);
+#pragma unroll
+            for (int u = 0; u < 18; ++u) {
+                const bool lk = u + kLead < 16, lv = u + kLead - 2 < 16;
+                if (lk) load_k(u + kLead);
+                if (lv) load_v(u + kLead - 2);
+                if (u == 6) load_a1();
+                if (u < 16) mfma_s(u);
                 if (u >= 2) mfma_pv(u - 2);
-                if (u == 4) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-                else if (u + kLead < 8) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-                else if (u + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                if (u < 2 || u >= 8) __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-                else __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-                if (u == 8) row_max();
+                if (u == 6) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                else if (lk && lv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                else if (lk || lv) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (u < 2 || u >= 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                if (u == 16) row_max();
             }
         } else {
             // a single product: operands kLead steps ahead
@@ -426,8 +465,8 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                 if constexpr (WPV) load_v(st);
             }
 #pragma unroll
-            for (int st = 0; st < 8; ++st) {
-                if (st + kLead < 8) {
+            for (int st = 0; st < 16; ++st) {
+                if (st + kLead < 16) {
                     if constexpr (WS) load_k(st + kLead);
                     if constexpr (WPV) load_v(st + kLead);
                 }
@@ -440,95 +479,98 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
         // has none in flight)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
-    // softmax (base 2) of tile kt's S^T into the wave's P operands (to the
+    // softmax (base 2) of tile kt's S^T into the wave's P^T operands (to the
     // partner too); group 1 then requests K_{kt+2} and V_{kt+1}
-    auto vphase = [&](bool with_softmax, int kt) {
-        if (with_softmax) {
-            // both waves of the pair take the same maxima and so keep the
-            // same running max (the lazy rule sees the same values in both)
+    auto vphase = [&](int kt) {
+        // both waves of the pair take the same maxima and so keep the same
+        // running max (the lazy rule sees the same values in both)
+        const float tm = fmaxf(xrow[wave][r], xrow[partner][r]);
+        if (__any(tm > m_run + kLazy)) {
+            const float m_new = tm > m_run + kLazy ? tm : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            d_run *= alpha;
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                float tm = fmaxf(xrow[wave][rt][n], xrow[partner][rt][n]);
-                if (__any(tm > m_run[rt] + kLazy)) {
-                    const float m_new = tm > m_run[rt] + kLazy ? tm : m_run[rt];
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
-                    m_run[rt] = m_new;
-                    d_run[rt] *= alpha;
-                    float al[4];
+            for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * kb + i, 64);
+                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        }
+        // chunk m: k = 8h + 4j + i of the B operand <-> S^T element 8m + 4j + i
+        // (position kp + 16m + 8j + 4h + i)
+        float pe[16];
 #pragma unroll
-                    for (int jd = 0; jd < 8; ++jd)
+        for (int i = 0; i < 16; ++i) {
+            pe[i] = __builtin_amdgcn_exp2f(sacc[i] - m_run);
+            d_run += pe[i];
+        }
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) oacc[rt][jd][i] *= al[i];
-                }
-            }
-            // k = 8kb + j of the A operand <-> position kp + 16(j/4) + 4kb + j%4
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                float pe[2][4];
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        pe[h][i] = __builtin_amdgcn_exp2f(s[rt][h][i] - m_run[rt]);
-                        d_run[rt] += pe[h][i];
-                    }
-                pa[rt] = u32x4_t{pack_f16x2(pe[0][0], pe[0][1]), pack_f16x2(pe[0][2], pe[0][3]),
-                                 pack_f16x2(pe[1][0], pe[1][1]), pack_f16x2(pe[1][2], pe[1][3])};
-                xp[wave][rt][lane] = pa[rt];
-            }
+        for (int m = 0; m < 2; ++m) {
+            pa[m] = u32x4_t{pack_f16x2(pe[8 * m], pe[8 * m + 1]), pack_f16x2(pe[8 * m + 2], pe[8 * m + 3]),
+                            pack_f16x2(pe[8 * m + 4], pe[8 * m + 5]), pack_f16x2(pe[8 * m + 6], pe[8 * m + 7])};
+            xp[wave][m][lane] = pa[m];
         }
         if (grp) {
             // K_{kt+2} over K_kt and V_{kt+1} over V_{kt-1}: 32 chunks each, 8 a wave
-            if (kt + 2 < ntiles) kv_tile_to_lds<8>(k16, kvh, (kt + 2) * kPfKT, kv_end, Ks[kt & 1], wv - 4, 4, lane);
-            if (kt + 1 < ntiles) kv_tile_to_lds<8>(v16, kvh, (kt + 1) * kPfKT, kv_end, Vs[(kt + 1) & 1], wv - 4, 4, lane);
+            if (kt + 2 < ntiles) k_tile_to_lds<8>(k16, kvh, (kt + 2) * kPfKT, kv_end, Ks[kt & 1], wv - 4, 4, lane);
+            if (kt + 1 < ntiles) vt_tile_to_lds<8>(vth + (kt + 1) * (kPfKT * 256), Vs[(kt + 1) & 1], wv - 4, 4, lane);
         }
     };
 
     mphase(std::true_type{}, std::false_type{}, 0);
     phase_barrier();
-    vphase(true, 0);
+    vphase(0);
     phase_barrier();
     for (int kt = 1; kt < ntiles; ++kt) {
         mphase(std::true_type{}, std::true_type{}, kt);
         phase_barrier();
-        vphase(true, kt);
+        vphase(kt);
         phase_barrier();
     }
     mphase(std::false_type{}, std::true_type{}, ntiles);
     phase_barrier();
     if (!grp) phase_barrier();   // group 0 passes group 1's last barrier
 
-    // epilogue: O / d * sigmoid(gate), d the pair's row sums;
-    // oacc[rt][jd][i] = O[row 4kb+i of row tile rt][dim 128e + 16jd + n]
-    float dt[2];
+    // epilogue: O / d * sigmoid(gate), d the row sum over the lane's 16
+    // positions, lane r + 32's and the partner's; four consecutive dims per
+    // (dt, j), so one 8- or 16-byte gate load and store
+    {
+        const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(d_run), __float_as_uint(d_run), false, false);
+        const float d = __uint_as_float(h32[0]) + __uint_as_float(h32[1]);
+        if (h == 0) xrow[wave][r] = d;
+        __syncthreads();
+        const float inv_d = 1.0f / (d + xrow[partner][r]);
+        const int tok = t0 + 4 * pr + (r >> 3);
+        if (tok < T) {
+            const size_t qi = static_cast<size_t>(tok) * 16 + kvh * 8 + (r & 7);
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        float d = d_run[rt];
-        d += __shfl_xor(d, 16, 64);
-        d += __shfl_xor(d, 32, 64);
-        dt[rt] = d;
-        if (kb == 0) xrow[wave][rt][n] = d;
-    }
-    __syncthreads();
+            for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const float d = dt[rt] + xrow[partner][rt][n];
+                for (int j = 0; j < 4; ++j) {
+                    const int dim = 128 * e + 32 * dt + 8 * j + 4 * h;
+                    float g[4], y[4];
+                    if constexpr (IN_DT == 1) {
+                        const u32x2_t w = *reinterpret_cast<const u32x2_t*>(
+                            static_cast<const uint16_t*>(q_gate) + qi * 512 + 256 + dim);
+                        g[0] = __uint_as_float(w[0] << 16);
+                        g[1] = __uint_as_float(w[0] & 0xffff0000u);
+                        g[2] = __uint_as_float(w[1] << 16);
+                        g[3] = __uint_as_float(w[1] & 0xffff0000u);
+                    } else {
+                        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(
+                            static_cast<const float*>(q_gate) + qi * 512 + 256 + dim);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 4 * kb + i;
-            const float inv_d = 1.0f / __shfl(d, row, 64);
-            const int tok = t0 + 4 * pr + 2 * rt + (row >> 3);
-            if (tok >= T) continue;
-            const int h = kvh * 8 + (row & 7);
-            const size_t qi = static_cast<size_t>(tok) * 16 + h;
+                        for (int i = 0; i < 4; ++i) g[i] = w[i];
+                    }
 #pragma unroll
-            for (int jd = 0; jd < 8; ++jd) {
-                const int dim = 128 * e + 16 * jd + n;
-                const float g = elem<IN_DT>::load(q_gate, qi * 512 + 256 + dim);
-                elem<OUT_DT>::store(out, qi * 256 + dim, oacc[rt][jd][i] * inv_d * sigmoid(g));
-            }
+                    for (int i = 0; i < 4; ++i) y[i] = oacc[dt][4 * j + i] * inv_d * sigmoid(g[i]);
+                    if constexpr (OUT_DT == 1) {
+                        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(out) + qi * 256 + dim) =
+                            u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                    } else {
+                        *reinterpret_cast<f32x4_t*>(static_cast<float*>(out) + qi * 256 + dim) =
+                            f32x4_t{y[0], y[1], y[2], y[3]};
+                    }
+                }
         }
     }
 }
@@ -542,15 +584,16 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
     uint16_t* kc = static_cast<uint16_t*>(k_cache);
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     const RopeFreqs rf = rope_freqs(p->rope_theta);
-    // the attention kernel reads fp16 K and V: an fp16 cache itself, else
-    // the fp16 copy in workspace ([max_ctx][2][256] K, then V), which the
-    // prep kernel extends by the new rows and kv16_copy fills below start_pos
+    // the attention kernel reads fp16 K (an fp16 cache itself, else the fp16
+    // copy in workspace, [max_ctx][2][256], which the prep kernel extends by
+    // the new rows and k16_copy fills below start_pos) and the transposed
+    // fp16 copy of V (vt_copy, after the prep kernel's append)
     uint16_t* k16 = p->kv_f16 ? kc : ctx->gqa_kv16;
-    uint16_t* v16 = p->kv_f16 ? vc : ctx->gqa_kv16 + static_cast<size_t>(ctx->cfg.max_ctx) * 512;
+    const int vt_stride = (ctx->cfg.max_ctx + kPfKT - 1) / kPfKT;   // tiles per kv head
     if (!p->kv_f16 && start_pos > 0) {
-        ProfScope prof(ctx, stream, "gqa_prefill_kv16");
+        ProfScope prof(ctx, stream, "gqa_prefill_k16");
         const int pieces = start_pos * 64;
-        kv16_copy_kernel<<<(pieces + 255) / 256, 256, 0, stream>>>(kc, vc, k16, v16, pieces);
+        k16_copy_kernel<<<(pieces + 255) / 256, 256, 0, stream>>>(kc, k16, pieces);
     }
     {
         ProfScope prof(ctx, stream, "gqa_prefill_prep");
@@ -558,7 +601,7 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
 #define QFF_PREP(I, F)                                                                                           \
     gqa_prefill_prep_kernel<I, F><<<pgrid, 64 * kPrepWaves, 0, stream>>>(q_gate, k, v, p->q_norm_w, p->k_norm_w, \
                                                                         rf, p->scale, p->eps, start_pos, T, qb, \
-                                                                        kc, vc, k16, v16)
+                                                                        kc, vc, k16)
         if (p->kv_f16) {
             if (in_dtype == QFF_BF16) QFF_PREP(1, 1); else QFF_PREP(0, 1);
         } else {
@@ -566,10 +609,20 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
         }
 #undef QFF_PREP
     }
+    {
+        ProfScope prof(ctx, stream, "gqa_prefill_vt");
+        const int n = start_pos + T;
+        const dim3 vgrid((n + kPfKT - 1) / kPfKT, 2);
+        if (p->kv_f16)
+            vt_copy_kernel<1><<<vgrid, 256, 0, stream>>>(vc, ctx->gqa_vt, n, vt_stride);
+        else
+            vt_copy_kernel<0><<<vgrid, 256, 0, stream>>>(vc, ctx->gqa_vt, n, vt_stride);
+    }
     const dim3 grid((T + kPfQB - 1) / kPfQB, 2);
     ProfScope prof(ctx, stream, "gqa_prefill_attn");
 #define QFF_PFA(I, O) \
-    gqa_prefill_attn_kernel<I, O><<<grid, kPfThreads, 0, stream>>>(qb, q_gate, k16, v16, start_pos, T, out)
+    gqa_prefill_attn_kernel<I, O><<<grid, kPfThreads, 0, stream>>>(qb, q_gate, k16, ctx->gqa_vt, vt_stride, \
+                                                                   start_pos, T, out)
     if (in_dtype == QFF_BF16) {
         if (out_dtype == QFF_BF16) QFF_PFA(1, 1); else QFF_PFA(1, 0);
     } else {

@@ -38,7 +38,8 @@ struct qff_ctx {
     float* gqa_o = nullptr;       // [gqa_slots(cfg) * 8 * 256]
     // Full-attention prefill: normed, rotated q as bf16 [T][16][256].
     uint16_t* gqa_qb = nullptr;
-    uint16_t* gqa_kv16 = nullptr;   // fp16 copy of a bf16 KV cache for prefill: [max_ctx][2][256] K, then V
+    uint16_t* gqa_kv16 = nullptr;   // fp16 copy of a bf16 K cache for prefill: [max_ctx][2][256]
+    uint16_t* gqa_vt = nullptr;     // transposed fp16 copy of the V cache for prefill: [2][max_ctx / 64][256][64]
     // Many-token Q4 products, per slice of q4_xs_tokens tokens: the fp16
     // activations x16 [q4_xs_tokens][<= 4096] and each token's output factor.
     uint16_t* q4_x16 = nullptr;
@@ -77,7 +78,7 @@ constexpr int kSchedChunkLocal = 0;    // slot of the DeltaNet chunk-local pass
 
 struct WorkspaceLayout {
     size_t gqa_m, gqa_d, gqa_o;
-    size_t gqa_qb, gqa_kv16, q4_x16, q4_fm, q4_sk_part, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
+    size_t gqa_qb, gqa_kv16, gqa_vt, q4_x16, q4_fm, q4_sk_part, pf_o, dn_arrive, sched, kimg, qop, top, pop, gates, bv;
     size_t total;
 };
 WorkspaceLayout workspace_layout(const qff_ctx_cfg& cfg);

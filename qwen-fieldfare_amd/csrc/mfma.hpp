@@ -7,6 +7,9 @@
 //   16x16x16 bf16 / f16: A[16 x 16]: lane l holds row l%16, k = 4*(l/16) .. +3
 //                  B[16 x 16]: lane l holds col l%16, k = 4*(l/16) .. +3
 //   C/D[16 x 16] fp32: lane l holds col l%16, rows 4*(l/16) .. +3
+//   32x32x16 f16: A[32 x 16]: lane l holds row l%32, k = 8*(l/32) .. +7
+//                 B[16 x 32]: lane l holds col l%32, k = 8*(l/32) .. +7
+//   C/D[32 x 32] fp32: lane l holds col l%32, element i row 8*(i/4) + 4*(l/32) + i%4
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,6 +41,12 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32_f16(u32x4_t a, u32x4_t b, f32x4
 }
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16_t mfma_32x32x16_f16(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
 
 __device__ __forceinline__ f32x4_t mfma_16x16x16_f16(u32x2_t a, u32x2_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,

@@ -250,16 +250,17 @@ def test_gqa_rejects_bad_calls(hip):
     with pytest.raises(qff.QffError) as e:       # past the end of the cache
         prefill(8, 60)
     assert e.value.status == -1
-    # a longer cache than the context's max_ctx: refused for a bf16 cache (its
-    # fp16 copy lives in the workspace), accepted for an fp16 one
-    kc_long = torch.zeros(2 * max_ctx, 2, 256, dtype=torch.bfloat16, device=DEV)
+    # a longer cache than the context's max_ctx, written past it: refused for
+    # either cache type (the attention's copies of the cache live in the
+    # workspace); up to it: accepted
     qg8 = torch.zeros(8, 16, 512, dtype=torch.bfloat16, device=DEV)
     kv8 = torch.zeros(8, 2, 256, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(qff.QffError) as e:
-        qff.gqa_prefill(ctx, pg, qg8, kv8, kv8, kc_long, kc_long.clone(), max_ctx)
-    assert e.value.status == -4
-    kc_long16 = kc_long.to(torch.float16)
-    qff.gqa_prefill(ctx, pg, qg8, kv8, kv8, kc_long16, kc_long16.clone(), max_ctx)
+    for dt in (torch.bfloat16, torch.float16):
+        kc_long = torch.zeros(2 * max_ctx, 2, 256, dtype=dt, device=DEV)
+        with pytest.raises(qff.QffError) as e:
+            qff.gqa_prefill(ctx, pg, qg8, kv8, kv8, kc_long, kc_long.clone(), max_ctx - 4)
+        assert e.value.status == -4
+        qff.gqa_prefill(ctx, pg, qg8, kv8, kv8, kc_long, kc_long.clone(), max_ctx - 8)
     torch.cuda.synchronize()
     qg = torch.zeros(3, 16, 512, dtype=torch.bfloat16, device=DEV)
     kn = torch.zeros(3, 2, 256, dtype=torch.bfloat16, device=DEV)
