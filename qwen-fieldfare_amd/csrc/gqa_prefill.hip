@@ -200,6 +200,20 @@ constexpr int kPfThreads = 512;
 // slots (128 B), piece j of row d at j ^ vt_swz(d). A K operand read (32
 // rows x one piece per 32 lanes) and a V^T operand read (32 rows x one
 // piece) then each meet every bank group equally.
+// 32-bit LDS byte address of a shared-memory element; a b128 read at one;
+// a ^ x in one VALU instruction that the compiler neither hoists nor merges.
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint16_t*)(p)));
+}
+__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t a) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(static_cast<uintptr_t>(a));
+}
+__device__ __forceinline__ uint32_t lds_xor(uint32_t a, uint32_t x) {
+    uint32_t r;
+    asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(x), "v"(a));
+    return r;
+}
+
 __device__ __forceinline__ int k_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 __device__ __forceinline__ int vt_swz(int d) { return (d >> 1) & 7; }
 
@@ -381,20 +395,16 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
         constexpr int kLead = 3, kRing = kLead + 1;
         u32x4_t ka[kRing];
         u32x4_t va[kRing];
-        // (the lane indices are redefined, as far as the compiler knows, at
-        // every step, so each step's XOR is formed next to its reads instead
-        // of all of them being held in registers across the loop)
-        auto load_k = [&](int st) {
-            int ki = kidx;
-            asm volatile("" : "+v"(ki));
-            ka[st % kRing] = *reinterpret_cast<const u32x4_t*>(kbuf + (ki ^ (16 * st)));
-        };
+        // (the buffers are 1-KB aligned, so XOR of an element offset's low
+        // bits is XOR of the LDS byte address's; each step's XOR is one VALU
+        // instruction, formed next to its read in an asm statement the
+        // compiler cannot hoist, instead of all of them being held in
+        // registers across the loop)
+        const uint32_t kaddr = lds_addr(kbuf + kidx), vaddr = lds_addr(vbuf + vidx);
+        auto load_k = [&](int st) { ka[st % kRing] = lds_read_b128(lds_xor(kaddr, 32 * st)); };
         auto load_v = [&](int v) {
             const int cc = v >> 3, m = (v >> 2) & 1, dt = v & 3;
-            int vi = vidx;
-            asm volatile("" : "+v"(vi));
-            vi ^= 32 * (cc == 0 ? e : 1 - e) + 16 * m;
-            va[v % kRing] = *reinterpret_cast<const u32x4_t*>(vbuf + vi + 2048 * dt);
+            va[v % kRing] = lds_read_b128(lds_xor(vaddr, 64 * (cc == 0 ? e : 1 - e) + 32 * m) + 4096 * dt);
         };
         f32x16_t s1;
         auto mfma_s = [&](int st) {
