@@ -217,31 +217,35 @@ __device__ __forceinline__ uint32_t lds_xor(uint32_t a, uint32_t x) {
 __device__ __forceinline__ int k_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 __device__ __forceinline__ int vt_swz(int d) { return (d >> 1) & 7; }
 
+// global_load_lds_dwordx4 from base + voff (base uniform, voff a 32-bit lane
+// offset) to the LDS address in M0, lane l's 16 bytes at M0 + 16 l (the
+// s_nop is the wait state an M0 write needs before an LDS DMA).
+__device__ __forceinline__ void dma16(const char* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+
 // One wave's 1-KB chunk c (rows 2c, 2c + 1) of a 64-row K tile, copied from
 // the fp16 cache rows p0 + 2c, p0 + 2c + 1 straight into LDS: lane l fills
 // LDS piece l % 32 of row 2c + h (h = l / 32) with global piece
 // (l % 32) ^ k_swz(2c + h) = (l % 32) ^ 2h ^ k_swz(2c) (bit 1 of k_swz(2c) is
-// clear): a lane term XORed with a uniform one, added to the uniform row
-// base. Only the tile that reaches kv_end (tail) clamps rows at kv_end - 1
-// (finite data; their scores are masked).
+// clear): a lane term XORed with a uniform one (one VALU instruction), as
+// the 32-bit offset from a uniform row base. Only the tile that reaches
+// kv_end (tail) clamps rows at kv_end - 1 (finite data; their scores are
+// masked).
 template <bool TAIL>
 __device__ __forceinline__ void k_chunk_to_lds(const uint16_t* __restrict__ src, int kvh, int p0, int kv_end,
                                                uint16_t* tile, int c, int lane) {
     const int h = lane >> 5;
-    // (redefined for the compiler at each chunk, so the offsets of all the
-    // chunks are not formed ahead and held in registers)
-    unsigned lt = 1024u * h + 16u * ((lane & 31) ^ (2 * h));
-    asm volatile("" : "+v"(lt));
-    const unsigned poff = lt ^ (16u * k_swz(2 * c));
-    const char* g;
+    const uint32_t lt = 1024u * h + 16u * ((lane & 31) ^ (2 * h));
+    const uint32_t poff = lds_xor(lt, 16u * k_swz(2 * c));
     if constexpr (TAIL) {
         const int p = min(p0 + 2 * c + h, kv_end - 1);
-        g = reinterpret_cast<const char*>(src) + (static_cast<size_t>(p) * 2 + kvh) * 512 + (poff & 1023u);
+        dma16(reinterpret_cast<const char*>(src) + (static_cast<size_t>(p0) * 2 + kvh) * 512,
+              static_cast<uint32_t>(p - p0) * 1024u + (poff & 1023u), lds_addr(tile + 512 * c));
     } else {
-        g = reinterpret_cast<const char*>(src) + (static_cast<size_t>(p0 + 2 * c) * 2 + kvh) * 512 + poff;
+        dma16(reinterpret_cast<const char*>(src) + (static_cast<size_t>(p0 + 2 * c) * 2 + kvh) * 512, poff,
+              lds_addr(tile + 512 * c));
     }
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)(tile + 512 * c), 16, 0, 0);
 }
 
 // Chunks c0, c0 + step, ... (N of them) of the K tile at rows p0 .. p0 + 63.
@@ -265,14 +269,11 @@ __device__ __forceinline__ void k_tile_to_lds(const uint16_t* __restrict__ src, 
 template <int N>
 __device__ __forceinline__ void vt_tile_to_lds(const uint16_t* __restrict__ src, uint16_t* tile, int c0, int step,
                                                int lane) {
+    const uint32_t lt = 128u * (lane >> 3) + 16u * ((lane & 7) ^ (lane >> 4));
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const int c = c0 + step * i;
-        unsigned lt = 128u * (lane >> 3) + 16u * ((lane & 7) ^ (lane >> 4));
-        asm volatile("" : "+v"(lt));
-        const char* g = reinterpret_cast<const char*>(src) + 1024 * c + (lt ^ (64u * (c & 1)));
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                         (__attribute__((address_space(3))) void*)(tile + 512 * c), 16, 0, 0);
+        dma16(reinterpret_cast<const char*>(src) + 1024 * c, lds_xor(lt, 64u * (c & 1)), lds_addr(tile + 512 * c));
     }
 }
 
