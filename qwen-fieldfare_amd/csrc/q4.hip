@@ -927,19 +927,22 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
 //
 // q4_x16_kernel forms x16 and f_m (one wave per token). q4_gemm_kernel: one
 // workgroup per 256 rows x 128 tokens, four waves of 64 rows x 128 tokens
-// (4 x 8 MFMA tiles, C rows = weight rows so each lane's four outputs are
-// adjacent in y). A wave loads its own rows' nibbles straight into registers
-// (8 B per lane and row tile per group: it alone uses them) and converts them
-// there; the token tile's x16 group goes through LDS, double-buffered, one
-// barrier per group, loaded straight from global memory into LDS. The packed fp16 (256 s, 256 b) of the tile's rows sit in
-// LDS for the whole K loop.
+// (2 x 4 tiles of 32x32x16 fp16 MFMAs, C rows = weight rows so each lane's
+// four consecutive outputs are adjacent in y; a 32x32x16 MFMA runs long
+// enough that the wave's next LDS operand reads issue under it). A wave loads
+// its own rows' nibbles straight into registers (16 B per lane and row tile
+// per group: it alone uses them) and converts them there; the token tile's
+// x16 group goes through LDS, double-buffered, one barrier per group, loaded
+// straight from global memory into LDS. The packed fp16 (256 s, 256 b) of
+// the tile's rows sit in LDS for the whole K loop.
 //
 // Within each 8-column word the matrix-core k order is (c0, c4, c1, c5, c2,
 // c6, c3, c7): dword j of the converted word is then the fp16 pair
 // ((w >> 4j) & 0x000F000F) | 0x64006400 = (1024 + q_j, 1024 + q_j+4), exact,
-// minus 1024 (exact), then the FMA; x16 is stored in the same order. A lane
-// with k-block kb of a 32-wide MFMA step ks takes word 2 kb + ks of the group,
-// so its two words of a group are one 8-byte load.
+// minus 1024 (exact), then the FMA; x16 is stored in the same order. The
+// lanes of half h (k slots 8h .. 8h + 7) of a 16-deep MFMA step ks take word
+// 4h + ks of the group, so a lane's four words of a group are one 16-byte
+// load, and the x16 piece 4h + ks.
 constexpr int kQ4GemmRows = 256;   // weight rows per workgroup
 constexpr int kQ4GemmToks = 128;   // tokens per workgroup
 
@@ -1014,15 +1017,19 @@ __global__ __launch_bounds__(256) void q4_x16_kernel(const void* __restrict__ x,
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 // One nibble word -> four fp16 pairs 256 (s q + b) in the k order above;
-// sb = packed fp16 (256 s, 256 b).
-__device__ __forceinline__ u32x4_t q4_to_f16_scaled(uint32_t w, uint32_t sb) {
+// sb = packed fp16 (256 s, 256 b); e1024 = 0x64006400 held in a VGPR, so the
+// extraction of each pair is one v_and_or_b32 (its other constant the one
+// scalar operand a VOP3 instruction may read) after the shift.
+__device__ __forceinline__ u32x4_t q4_to_f16_scaled(uint32_t w, uint32_t sb, uint32_t e1024) {
     const f16x2_t sbv = __builtin_bit_cast(f16x2_t, sb);
     const f16x2_t s2 = {sbv[0], sbv[0]}, b2 = {sbv[1], sbv[1]};
     const f16x2_t k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     u32x4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const f16x2_t q = __builtin_bit_cast(f16x2_t, ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - k1024;
+        uint32_t e;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(e) : "v"(w >> (4 * j)), "s"(0x000F000Fu), "v"(e1024));
+        const f16x2_t q = __builtin_bit_cast(f16x2_t, e) - k1024;
         r[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
     }
     return r;
@@ -1043,7 +1050,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const bool ybf = parts.ybf16[pp];
     const int G = cols / 64;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = lane & 15, kb = lane >> 4;
     const int R0 = (blockIdx.x - parts.blk0[pp]) * kQ4GemmRows, M0 = blockIdx.y * kQ4GemmToks;
 
     __shared__ __attribute__((aligned(16))) uint16_t Xl[2][kQ4GemmToks * 64];
@@ -1058,23 +1064,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     // x16 staging straight from global memory into LDS: wave w's load i fills
     // tokens 8 (4w + i) .. +7 of the [128][64] tile, lane l the 16-byte
     // piece l & 7 of token l >> 3, which holds the token's 8-column block
-    // (l & 7) ^ ((token >> 1) & 7) of the group (the swizzle puts the 16 rows
-    // of an operand read on different banks)
+    // (l & 7) ^ ((token >> 1) & 7) of the group (the swizzle spreads the 32
+    // rows of an operand read over the bank groups)
     const uint16_t* xsrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 8 * (4 * wave + i) + (lane >> 3);
         xsrc[i] = x16 + static_cast<size_t>(min(M0 + tok, batch - 1)) * cols + 8 * ((lane & 7) ^ ((tok >> 1) & 7));
     }
-    // weight words: lane -> rows 64 wave + 16 rt + n, words 2 kb, 2 kb + 1 of each group
+    // weight words: lane -> rows 64 wave + 32 rt + r, words 4h .. 4h + 3 of each group
     // (rows past the part's end read its last row; their outputs are not stored)
-    const int wrow = R0 + 64 * wave + n;
-    const uint32_t* wsrc = w + static_cast<size_t>(min(wrow, rows - 1)) * (cols / 8) + 2 * kb;
-    int wstep[4];   // word offset of row tile rt from row tile 0
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) wstep[rt] = (min(wrow + 16 * rt, rows - 1) - min(wrow, rows - 1)) * (cols / 8);
+    const int r = lane & 31, h = lane >> 5;
+    const int wrow = R0 + 64 * wave + r;
+    const uint32_t* wsrc = w + static_cast<size_t>(min(wrow, rows - 1)) * (cols / 8) + 4 * h;
+    const int wstep1 = (min(wrow + 32, rows - 1) - min(wrow, rows - 1)) * (cols / 8);   // row tile 1's word offset
 
-    u32x2_t wa[2][4];
+    u32x4_t wa[2][2];
     auto stage_x = [&](int buf, int g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -1082,21 +1087,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                                              (__attribute__((address_space(3))) void*)&Xl[buf][8 * (4 * wave + i) * 64],
                                              16, 0, 0);
     };
-    auto fetch_w = [&](u32x2_t (&dst)[4], int g) {
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) dst[rt] = *reinterpret_cast<const u32x2_t*>(wsrc + wstep[rt] + 8 * g);
+    auto fetch_w = [&](u32x4_t (&dst)[2], int g) {
+        dst[0] = *reinterpret_cast<const u32x4_t*>(wsrc + 8 * g);
+        dst[1] = *reinterpret_cast<const u32x4_t*>(wsrc + wstep1 + 8 * g);
     };
 
-    f32x4_t acc[4][8];
+    f32x16_t acc[2][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 8; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
     // group g: x16 in LDS buffer g & 1, its weight words in wa[s]; on the
     // way, group g + 1's x16 is requested into the other buffer and its
     // weight words into wa[s ^ 1] (clamped, so every load is unconditional)
-    const int sw = (n >> 1) & 7;
+    uint32_t e1024 = 0x64006400u;
+    asm volatile("" : "+v"(e1024));   // kept in a VGPR
     auto step = [&](int s, int g) {
         // (the two unrolled steps are kept apart: interleaved by the
         // scheduler they would not fit the registers)
@@ -1106,33 +1114,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         stage_x((g + 1) & 1, min(g + 1, G - 1));
-        const u32x2_t (&cur)[4] = wa[s];
+        const u32x4_t (&cur)[2] = wa[s];
         fetch_w(wa[s ^ 1], min(g + 1, G - 1));
         // the loads stay at the top of the step, a whole group's work ahead
         // of their use (the scheduler would sink them next to it)
         __builtin_amdgcn_sched_barrier(0);
-        uint32_t sb[4];
+        uint32_t sb[2];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) sb[rt] = sbl[g * kQ4GemmRows + 64 * wave + 16 * rt + n];
-        const uint16_t* xb = &Xl[g & 1][n * 64];
+        for (int rt = 0; rt < 2; ++rt) sb[rt] = sbl[g * kQ4GemmRows + 64 * wave + 32 * rt + r];
+        // B operand of token tile mt, step ks: token 32 mt + r, x16 piece
+        // 4h + ks (swizzled by (token / 2) % 8, so the 32 rows of a read
+        // meet every bank group twice)
+        const uint16_t* xb = &Xl[g & 1][r * 64];
+        const int sw = (r >> 1) & 7;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            u32x4_t A[4];
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4_t A[2], B[4];
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) A[rt] = q4_to_f16_scaled(cur[rt][ks], sb[rt]);
-            const int off = 8 * ((2 * kb + ks) ^ sw);
+            for (int rt = 0; rt < 2; ++rt) A[rt] = q4_to_f16_scaled(cur[rt][ks], sb[rt], e1024);
 #pragma unroll
-            for (int mh = 0; mh < 2; ++mh) {
-                u32x4_t B[4];
+            for (int mt = 0; mt < 4; ++mt)
+                B[mt] = *reinterpret_cast<const u32x4_t*>(xb + 32 * mt * 64 + 8 * ((4 * h + ks) ^ sw));
 #pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-                    B[mi] = *reinterpret_cast<const u32x4_t*>(xb + 16 * (4 * mh + mi) * 64 + off);
+            for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                    for (int mi = 0; mi < 4; ++mi)
-                        acc[rt][4 * mh + mi] = mfma_16x16x32_f16(A[rt], B[mi], acc[rt][4 * mh + mi]);
-            }
+                for (int mt = 0; mt < 4; ++mt) acc[rt][mt] = mfma_32x32x16_f16(A[rt], B[mt], acc[rt][mt]);
         }
     };
     stage_x(0, 0);
@@ -1144,37 +1150,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     }
     if (g < G) step(0, g);
 
-    // lane: token 16mt + n, rows 64 wave + 16 rt + 4 kb .. +3 (adjacent in y)
+    // lane: token 32 mt + r, rows 64 wave + 32 rt + 8 j + 4 h .. +3 (adjacent in y)
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-        const int m = M0 + 16 * mt + n;
+    for (int mt = 0; mt < 4; ++mt) {
+        const int m = M0 + 32 * mt + r;
         if (m >= batch) continue;
         const float f = fm[m];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const int r = R0 + 64 * wave + 16 * rt + 4 * kb;
-            const size_t o = static_cast<size_t>(m) * rows + r;
-            f32x4_t v = acc[rt][mt];
+        for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] *= f;
-                if (res && r + i < rows) v[i] += ybf ? elem<1>::load(res, o + i) : elem<0>::load(res, o + i);
-            }
-            if (r + 3 < rows && (rows & 3) == 0) {
-                if (ybf)
-                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
-                        u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                else
-                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = v;
-            } else {
+            for (int j = 0; j < 4; ++j) {
+                const int rr = R0 + 64 * wave + 32 * rt + 8 * j + 4 * h;
+                const size_t o = static_cast<size_t>(m) * rows + rr;
+                f32x4_t v = f32x4_t{acc[rt][mt][4 * j], acc[rt][mt][4 * j + 1], acc[rt][mt][4 * j + 2],
+                                    acc[rt][mt][4 * j + 3]};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (r + i >= rows) continue;
-                    if (ybf) elem<1>::store(y, o + i, v[i]);
-                    else elem<0>::store(y, o + i, v[i]);
+                    v[i] *= f;
+                    if (res && rr + i < rows) v[i] += ybf ? elem<1>::load(res, o + i) : elem<0>::load(res, o + i);
+                }
+                if (rr + 3 < rows && (rows & 3) == 0) {
+                    if (ybf)
+                        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(y) + o) =
+                            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    else
+                        *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + o) = v;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (rr + i >= rows) continue;
+                        if (ybf) elem<1>::store(y, o + i, v[i]);
+                        else elem<0>::store(y, o + i, v[i]);
+                    }
                 }
             }
-        }
     }
 }
 
