@@ -16,9 +16,10 @@
 //          16-byte LDS read per lane.
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; four wave pairs of 32 rows = 4 tokens
-//          x 8 heads, each wave scoring half of a tile's positions and
-//          accumulating half of the output dims, so accumulators and q stay
-//          in VGPRs and two waves share each SIMD) and walks 64-position
+//          x 8 heads, each wave running its own flash attention over half of
+//          every tile's positions with O^T over all 256 dims, the pair's
+//          halves merged once at the end, so accumulators and q stay in
+//          VGPRs and two waves share each SIMD) and walks 64-position
 //          tiles of K (from the fp16 cache, or the fp16 copy of a bf16 one:
 //          exact for the cache's values) and of V^T, copied straight into
 //          LDS (double-buffered, XOR-swizzled rows, no registers), so both
@@ -30,11 +31,11 @@
 //          Softmax in base 2 (q carries scale * log2 e), with the running
 //          max raised only when a tile exceeds it by more than 2^8, so the
 //          O rescale is rare; causal masking only on the tiles that reach
-//          past the block's first token. The eight waves run as two groups
-//          one phase apart (MFMA phase / softmax phase, see the kernel).
-//          Query blocks are issued last-first so the longest rows start
-//          earliest. The epilogue divides by the row sums and applies the
-//          sigmoid gate.
+//          past the block's first token. One barrier per tile; the next
+//          tiles' copies are requested inside the MFMA stream. Query blocks
+//          are issued last-first so the longest rows start earliest. The
+//          epilogue merges each pair's halves, divides by the row sums and
+//          applies the sigmoid gate.
 #include "common.hpp"
 #include "internal.hpp"
 #include "mfma.hpp"
@@ -261,24 +262,18 @@ __device__ __forceinline__ void k_tile_to_lds(const uint16_t* __restrict__ src, 
     }
 }
 
-// Chunks c0, c0 + step, ... (N of them; chunk c = dims 8c .. 8c + 7) of the
-// V^T tile at src (32 KB), copied straight into LDS: lane l fills LDS piece
+// Chunk c (dims 8c .. 8c + 7) of the V^T tile at src (32 KB), copied
+// straight into LDS: lane l fills LDS piece
 // l % 8 of row 8c + l / 8 with global piece (l % 8) ^ vt_swz(8c + l / 8) =
 // (l % 8) ^ (l / 16) ^ 4 (c % 2). The copy is whole (rows past the cache
 // end are zero), so no clamping.
-template <int N>
-__device__ __forceinline__ void vt_tile_to_lds(const uint16_t* __restrict__ src, uint16_t* tile, int c0, int step,
-                                               int lane) {
+__device__ __forceinline__ void vt_chunk_to_lds(const uint16_t* __restrict__ src, uint16_t* tile, int c, int lane) {
     const uint32_t lt = 128u * (lane >> 3) + 16u * ((lane & 7) ^ (lane >> 4));
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const int c = c0 + step * i;
-        dma16(reinterpret_cast<const char*>(src) + 1024 * c, lds_xor(lt, 64u * (c & 1)), lds_addr(tile + 512 * c));
-    }
+    dma16(reinterpret_cast<const char*>(src) + 1024 * c, lds_xor(lt, 64u * (c & 1)), lds_addr(tile + 512 * c));
 }
 
-// A workgroup barrier between two phases of a wave's schedule; nothing
-// (MFMAs included, which touch no memory) is moved across it.
+// A workgroup barrier that nothing (MFMAs included, which touch no memory)
+// is moved across.
 __device__ __forceinline__ void phase_barrier() {
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -287,46 +282,40 @@ __device__ __forceinline__ void phase_barrier() {
 
 // grid (ceil(T/16), 2 kv heads), 512 threads: four wave pairs, pair pr
 // owning the 32 q rows r = 8 tt + hh (token t0 + 4 pr + tt, head hh of the
-// kv head's 8). Lane l holds row l % 32 throughout. Wave e of a pair scores
-// positions 32e .. 32e + 31 of each K tile, S^T = K Q^T on 32x32x16 fp16
-// MFMAs (A = 32 K rows x 16 dims from LDS, B = the row's q in registers),
-// the pair meets once for the row maxima and once for the P operands
-// (through LDS), and wave e accumulates output dims 128e .. 128e + 127 over
-// all 64 positions, O^T = V^T P^T (A = 32 dims x 16 positions of the V^T
-// tile in LDS, B = P^T straight from the S^T accumulators: a lane's
-// S^T registers and O^T registers belong to its one q row, so the rescale
-// needs no lane exchange). Each K operand read feeds 32 rows, each V
-// operand read 32 rows: 32 KB of LDS reads per wave and tile.
+// kv head's 8). Lane l holds row l % 32 throughout. Wave e of a pair runs
+// flash attention on its own over positions 32e .. 32e + 31 of every tile
+// (its own running max and row sum, O^T over all 256 dims), and the pair
+// merges its two halves once, at the end. Per tile a wave computes
+// S^T = K Q^T on 32x32x16 fp16 MFMAs (A = 32 K rows x 16 dims from LDS, B
+// = the row's q in registers; 16 steps) and O^T += V^T P^T (A = 32 dims x
+// 16 positions of the V^T tile, B = P^T straight from the S^T accumulator:
+// a lane's S^T and O^T registers belong to its one q row, so neither the
+// softmax nor the rescale needs a lane exchange beyond the permlane swap
+// of the two 16-position halves; 8 dim tiles x 2 steps). Each K or V
+// operand read feeds 32 rows: 32 KB of LDS reads per wave and tile.
 //
-// Schedule: two phases per tile between workgroup barriers -- M(j), on the
-// MFMAs: S^T of tile j+1 interleaved with O^T += V^T P^T of tile j
-// (operands read three steps ahead); V(j+1), on the VALU: the softmax of
-// tile j+1 -- with waves 4-7 (group 1) one phase behind waves 0-3 (group
-// 0): group 1 passes one barrier more at the start, group 0 one more at the
-// end. Waves w and w + 4 share a SIMD, so while one issues MFMAs the other
-// runs its softmax. Slots: group 0 computes S_j in slot 2j and P V_j in
-// slot 2j+2, group 1 one slot later, so K_j is read in slots 2j, 2j+1 and
-// V_j in 2j+2, 2j+3. The K tiles (from the fp16 cache or its fp16 copy)
-// and the V^T tiles (from the transposed copy) go straight into LDS,
-// requested by group 1 in its V(m) (slot 2m+2): K_{m+2}
-// into the buffer whose K_m was last read in 2m+1, V_{m+1} into the one
-// whose V_{m-1} was last read in 2m+1; group 1 waits for them at the end of
-// its next M phase (slot 2m+3), before both are first read (slot 2m+4).
+// Schedule: one workgroup barrier per tile. Iteration kt runs S^T of tile
+// kt interleaved with O^T += V^T P^T of tile kt - 1 (operands read kLead
+// steps ahead), then the softmax of tile kt; it reads K_kt and V_{kt-1},
+// and right after its barrier every wave requests its share of K_{kt+1}
+// (into the buffer K_{kt-1} left) and of V_kt (into the one V_{kt-2}
+// left), straight into LDS, waiting for them before the next barrier.
+// All eight waves run the same schedule, two per SIMD, so one wave's
+// operand reads and softmax overlap the other's MFMAs.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const uint16_t* __restrict__ qb, const void* __restrict__ q_gate, const uint16_t* __restrict__ k16,
     const uint16_t* __restrict__ vt, int vt_stride, int start, int T, void* __restrict__ out) {
-    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][kPfKT * 256];
-    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][kPfKT * 256];   // V^T tiles
-    __shared__ float xrow[kPfThreads / 64][32];                                  // per wave, q row
-    __shared__ __attribute__((aligned(16))) u32x4_t xp[kPfThreads / 64][2][64];  // per wave, chunk, lane
+    // K tiles 0, 1 and V^T tiles 0, 1 (kvs[2], kvs[3]); after the loop,
+    // each wave's 16 KB hand-over of O^T to its partner
+    __shared__ __attribute__((aligned(1024))) uint16_t kvs[4][kPfKT * 256];
+    __shared__ float xm[kPfThreads / 64][32], xd[kPfThreads / 64][32];   // per wave, q row
     const int nqb = (T + kPfQB - 1) / kPfQB;
     const int q_blk = nqb - 1 - static_cast<int>(blockIdx.x);
     const int kvh = blockIdx.y;
     const int t0 = q_blk * kPfQB;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wv = __builtin_amdgcn_readfirstlane(wave);   // the same, known uniform
-    const int grp = wv >> 2;
     const int r = lane & 31, h = lane >> 5;
     const int pr = wave >> 1, e = wave & 1, partner = wave ^ 1;
     constexpr float kLazy = 8.0f;   // raise the running max only past 2^8
@@ -349,127 +338,103 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const int first_masked = (start + t0) / kPfKT;   // tiles before this need no causal mask
 
     float m_run = -INFINITY, d_run = 0.0f;   // of the lane's row (the same in lanes r, r + 32)
-    f32x16_t oacc[4];                        // O^T tile dt: dims 128e + 32dt + 8(i/4) + 4h + i%4
+    f32x16_t oacc[8];                        // O^T tile dt: dims 32dt + 8(i/4) + 4h + i%4
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.0f;
 
-    // K_0, V_0 and K_1 by every wave (32 chunks each, 4 a wave)
     // this kv head's V^T tiles (64 x 256 fp16 each)
     const uint16_t* __restrict__ vth = vt + static_cast<size_t>(kvh) * vt_stride * (kPfKT * 256);
-    k_tile_to_lds<4>(k16, kvh, 0, kv_end, Ks[0], wv, 8, lane);
-    vt_tile_to_lds<4>(vth, Vs[0], wv, 8, lane);
-    if (ntiles > 1) k_tile_to_lds<4>(k16, kvh, kPfKT, kv_end, Ks[1], wv, 8, lane);
-    // every load so far (q included) has landed
+    // K_0 by every wave (32 chunks, 4 a wave); every load so far (q
+    // included) has landed at the first barrier
+    k_tile_to_lds<4>(k16, kvh, 0, kv_end, kvs[0], wv, 8, lane);
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (grp) phase_barrier();   // group 1 runs one phase behind
 
-    const int kp = 32 * e;      // the wave's first scored position in a tile
-    f32x16_t sacc;              // S^T of the tile whose softmax comes next: position kp + 8(i/4) + 4h + i%4
-    u32x4_t pa[2];              // the wave's P^T operands of the current tile (positions kp + 16m ..)
+    const int kp = 32 * e;   // the wave's first position in a tile
+    f32x16_t sacc;           // S^T: position kp + 8(i/4) + 4h + i%4
+    u32x4_t pa[2];           // P^T operands of the previous tile (positions kp + 16m ..)
 
-    // M phase of tile kt: S^T of tile kt (16 steps of 16 dims, two
-    // accumulators so consecutive steps are independent) and O^T += V^T P^T
-    // of tile kt - 1 (16 steps: the wave's own chunks, then the partner's,
-    // c = v / 8, m = (v / 4) % 2, dt = v % 4); the masked row maxima of the
-    // wave's 32 positions go to the partner
-    auto mphase = [&](auto with_s, auto with_pv, int kt) {
+    // iteration kt: S^T of tile kt (WS) and O^T += V^T P^T of tile kt - 1
+    // (WPV, step v: m = v / 8, dt = v % 8), then the softmax of tile kt
+    auto iter = [&](auto with_s, auto with_pv, int kt) {
         constexpr bool WS = decltype(with_s)::value, WPV = decltype(with_pv)::value;
+        phase_barrier();
+        // K_{kt+1} (K_{ntiles-1} again in the last iteration, into the free
+        // buffer) and V_kt: 32 chunks each, 4 a wave, one request per MFMA
+        // step in the first half of the stream, so the requests queue while
+        // the MFMAs run (the lane terms derived anew each time from an
+        // opaque copy of the lane index, rather than held in registers
+        // across the loop; the K rows clamped at kv_end - 1 in every tile,
+        // so no branch splits the stream)
+        int ln = static_cast<int>(threadIdx.x);
+        asm volatile("" : "+v"(ln));
+        ln &= 63;
+        // the stream at a raised wave priority, the softmax at the normal one
+        // (the SIMD's other wave then takes the MFMA issue slots it leaves)
+        __builtin_amdgcn_s_setprio(1);
+        const int kn = min(kt + 1, ntiles - 1);
+        auto dma = [&](int i) {
+            if constexpr (WS) {
+                const int c = wv + 8 * (i >> 1);
+                if (i & 1) vt_chunk_to_lds(vth + kt * (kPfKT * 256), kvs[2 + (kt & 1)], c, ln);
+                else k_chunk_to_lds<true>(k16, kvh, kn * kPfKT, kv_end, kvs[(kt + 1) & 1], c, ln);
+            }
+        };
         // K operand of step s: row kp + r, piece 2s + h -> element
         // (kp + r) 256 + 8 ((h ^ k_swz(r)) ^ 2s) = kidx ^ 16s
-        const uint16_t* kbuf = Ks[kt & 1];
         const int kidx = (kp + r) * 256 + 8 * (h ^ k_swz(r));
-        // V^T operand of PV step v: row (dim) 128e + 32dt + r, slots
-        // 32c' + 16m + 8h .. +7 (c' = e for the own chunks, 1 - e for the
-        // partner's; positions 32c' + 16m + 8j + 4h + i for k = 8h + 4j + i),
-        // piece 4c' + 2m + h permuted by vt_swz(r) -> element
-        // (vidx ^ (32c' + 16m)) + 2048 dt
-        const uint16_t* vbuf = Vs[(kt + 1) & 1];
-        const int vidx = (128 * e + r) * 64 + 8 * (h ^ vt_swz(r));
-        u32x4_t A1[2];   // the partner's P^T operands, read for PV steps 8 .. 15
-        auto load_a1 = [&]() {
-#pragma unroll
-            for (int m = 0; m < 2; ++m) A1[m] = xp[partner][m][lane];
-        };
-        constexpr int kLead = 3, kRing = kLead + 1;
+        // V^T operand of PV step (m, dt): row (dim) 32dt + r, slots
+        // kp + 16m + 8h .. +7 (positions kp + 16m + 8j + 4h + i for
+        // k = 8h + 4j + i), piece 4e + 2m + h permuted by vt_swz(r) ->
+        // element (vidx ^ (kp + 16m)) + 2048 dt
+        const int vidx = r * 64 + 8 * (h ^ vt_swz(r));
+        constexpr int kLead = 2, kRing = kLead + 1;
         u32x4_t ka[kRing];
         u32x4_t va[kRing];
         // (the buffers are 1-KB aligned, so XOR of an element offset's low
-        // bits is XOR of the LDS byte address's; each step's XOR is one VALU
-        // instruction, formed next to its read in an asm statement the
+        // bits is XOR of the LDS byte address's; each K step's XOR is one
+        // VALU instruction, formed next to its read in an asm statement the
         // compiler cannot hoist, instead of all of them being held in
         // registers across the loop)
-        const uint32_t kaddr = lds_addr(kbuf + kidx), vaddr = lds_addr(vbuf + vidx);
+        const uint32_t kaddr = lds_addr(kvs[kt & 1] + kidx);
+        const uint32_t vaddr = lds_addr(kvs[2 + ((kt + 1) & 1)] + vidx) ^ (64u * e);
         auto load_k = [&](int st) { ka[st % kRing] = lds_read_b128(lds_xor(kaddr, 32 * st)); };
         auto load_v = [&](int v) {
-            const int cc = v >> 3, m = (v >> 2) & 1, dt = v & 3;
-            va[v % kRing] = lds_read_b128(lds_xor(vaddr, 64 * (cc == 0 ? e : 1 - e) + 32 * m) + 4096 * dt);
+            const int m = v >> 3, dt = v & 7;
+            va[v % kRing] = lds_read_b128((m ? (vaddr ^ 32u) : vaddr) + 4096 * dt);
         };
-        f32x16_t s1;
-        auto mfma_s = [&](int st) {
-            if (st & 1) s1 = mfma_32x32x16_f16(ka[st % kRing], qreg[st], s1);
-            else sacc = mfma_32x32x16_f16(ka[st % kRing], qreg[st], sacc);
-        };
+        auto mfma_s = [&](int st) { sacc = mfma_32x32x16_f16(ka[st % kRing], qreg[st], sacc); };
         auto mfma_pv = [&](int v) {
-            const int cc = v >> 3, m = (v >> 2) & 1, dt = v & 3;
-            oacc[dt] = mfma_32x32x16_f16(va[v % kRing], cc == 0 ? pa[m] : A1[m], oacc[dt]);
-        };
-        // masked row maxima of S^T over the wave's 32 positions, to the partner
-        auto row_max = [&]() {
-            sacc += s1;
-            if (kt >= first_masked) {   // (uniform) the tiles that reach the block's first token
-                const int p0 = kt * kPfKT + kp + 4 * h;
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (p0 + 8 * (i >> 2) + (i & 3) > lim) sacc[i] = -INFINITY;
-            }
-            float tm = sacc[0];
-#pragma unroll
-            for (int i = 1; i < 16; ++i) tm = fmaxf(tm, sacc[i]);
-            // with the other half of the wave's positions (lane r + 32) on the
-            // permlane swap (VALU; an LDS permute would queue behind the
-            // operand reads)
-            const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tm), __float_as_uint(tm), false, false);
-            tm = fmaxf(__uint_as_float(h32[0]), __uint_as_float(h32[1]));
-            if (h == 0) xrow[wave][r] = tm;
+            const int m = v >> 3, dt = v & 7;
+            oacc[dt] = mfma_32x32x16_f16(va[v % kRing], pa[m], oacc[dt]);
         };
         if constexpr (WS) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sacc[i] = 0.0f;
-                s1[i] = 0.0f;
-            }
+            for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
         }
         if constexpr (WS && WPV) {
-            // step u: S step u (u < 16) and PV step u - 2 (u >= 2), so S is
-            // done two steps before the end and its row maxima run beside the
-            // last PV MFMAs; K of S step u + kLead and V of PV step
-            // u + kLead - 2 are read at step u
 #pragma unroll
-            for (int st = 0; st < kLead; ++st) load_k(st);
+            for (int st = 0; st < kLead; ++st) {
+                load_k(st);
+                load_v(st);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLead, 0);
 #pragma unroll
-            for (int v = 0; v < kLead - 2; ++v) load_v(v);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLead - 2, 0);
-#pragma unroll
-            for (int u = 0; u < 18; ++u) {
-                const bool lk = u + kLead < 16, lv = u + kLead - 2 < 16;
-                if (lk) load_k(u + kLead);
-                if (lv) load_v(u + kLead - 2);
-                if (u == 6) load_a1();
-                if (u < 16) mfma_s(u);
-                if (u >= 2) mfma_pv(u - 2);
-                if (u == 6) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                else if (lk && lv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                else if (lk || lv) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                if (u < 2 || u >= 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                else __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                if (u == 16) row_max();
+            for (int u = 0; u < 16; ++u) {
+                const bool ld = u + kLead < 16;
+                if (ld) {
+                    load_k(u + kLead);
+                    load_v(u + kLead);
+                }
+                if (u < 8) dma(u);
+                mfma_s(u);
+                mfma_pv(u);
+                if (ld) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             }
         } else {
             // a single product: operands kLead steps ahead
-            if constexpr (WPV) load_a1();
 #pragma unroll
             for (int st = 0; st < kLead; ++st) {
                 if constexpr (WS) load_k(st);
@@ -481,83 +446,105 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                     if constexpr (WS) load_k(st + kLead);
                     if constexpr (WPV) load_v(st + kLead);
                 }
+                if (st < 8) dma(st);
                 if constexpr (WS) mfma_s(st);
                 if constexpr (WPV) mfma_pv(st);
             }
-            if constexpr (WS) row_max();
         }
-        // group 1's tile requests of its last V phase have landed (group 0
-        // has none in flight)
+        __builtin_amdgcn_s_setprio(0);
+        if constexpr (WS) {
+            // softmax (base 2) of tile kt's S^T, masked, into the P^T operands
+            if (kt >= first_masked) {   // (uniform) the tiles that reach the block's first token
+                const int rel = lim - (kt * kPfKT + kp + 4 * h);
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i >> 2) + (i & 3) > rel) sacc[i] = -INFINITY;
+            }
+            float tm = sacc[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) tm = fmaxf(tm, sacc[i]);
+            // with the other 16 positions (lane r + 32) on the permlane swap
+            const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tm), __float_as_uint(tm), false, false);
+            tm = fmaxf(__uint_as_float(h32[0]), __uint_as_float(h32[1]));
+            // a row whose positions so far are all masked keeps m_run = -inf
+            // and alpha 1 (its O^T and sum are zero), its P entries exp2(-inf)
+            if (__any(tm > m_run + kLazy)) {
+                const bool up = tm > m_run + kLazy;
+                const float alpha = up ? __builtin_amdgcn_exp2f(m_run - tm) : 1.0f;
+                if (up) m_run = tm;
+                d_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+            }
+            const float mb = m_run == -INFINITY ? 0.0f : m_run;
+            // chunk m: k = 8h + 4j + i of the B operand <-> S^T element
+            // 8m + 4j + i (position kp + 16m + 8j + 4h + i)
+            float pe[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pe[i] = __builtin_amdgcn_exp2f(sacc[i] - mb);
+                d_run += pe[i];
+            }
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                pa[m] = u32x4_t{pack_f16x2(pe[8 * m], pe[8 * m + 1]), pack_f16x2(pe[8 * m + 2], pe[8 * m + 3]),
+                                pack_f16x2(pe[8 * m + 4], pe[8 * m + 5]), pack_f16x2(pe[8 * m + 6], pe[8 * m + 7])};
+        }
+        // this iteration's tile requests have landed
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
-    // softmax (base 2) of tile kt's S^T into the wave's P^T operands (to the
-    // partner too); group 1 then requests K_{kt+2} and V_{kt+1}
-    auto vphase = [&](int kt) {
-        // both waves of the pair take the same maxima and so keep the same
-        // running max (the lazy rule sees the same values in both)
-        const float tm = fmaxf(xrow[wave][r], xrow[partner][r]);
-        if (__any(tm > m_run + kLazy)) {
-            const float m_new = tm > m_run + kLazy ? tm : m_run;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            d_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
-        }
-        // chunk m: k = 8h + 4j + i of the B operand <-> S^T element 8m + 4j + i
-        // (position kp + 16m + 8j + 4h + i)
-        float pe[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            pe[i] = __builtin_amdgcn_exp2f(sacc[i] - m_run);
-            d_run += pe[i];
-        }
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            pa[m] = u32x4_t{pack_f16x2(pe[8 * m], pe[8 * m + 1]), pack_f16x2(pe[8 * m + 2], pe[8 * m + 3]),
-                            pack_f16x2(pe[8 * m + 4], pe[8 * m + 5]), pack_f16x2(pe[8 * m + 6], pe[8 * m + 7])};
-            xp[wave][m][lane] = pa[m];
-        }
-        if (grp) {
-            // K_{kt+2} over K_kt and V_{kt+1} over V_{kt-1}: 32 chunks each, 8 a wave
-            if (kt + 2 < ntiles) k_tile_to_lds<8>(k16, kvh, (kt + 2) * kPfKT, kv_end, Ks[kt & 1], wv - 4, 4, lane);
-            if (kt + 1 < ntiles) vt_tile_to_lds<8>(vth + (kt + 1) * (kPfKT * 256), Vs[(kt + 1) & 1], wv - 4, 4, lane);
-        }
-    };
 
-    mphase(std::true_type{}, std::false_type{}, 0);
-    phase_barrier();
-    vphase(0);
-    phase_barrier();
-    for (int kt = 1; kt < ntiles; ++kt) {
-        mphase(std::true_type{}, std::true_type{}, kt);
-        phase_barrier();
-        vphase(kt);
-        phase_barrier();
-    }
-    mphase(std::false_type{}, std::true_type{}, ntiles);
-    phase_barrier();
-    if (!grp) phase_barrier();   // group 0 passes group 1's last barrier
+    iter(std::true_type{}, std::false_type{}, 0);
+    for (int kt = 1; kt < ntiles; ++kt) iter(std::true_type{}, std::true_type{}, kt);
+    iter(std::false_type{}, std::true_type{}, ntiles);
 
-    // epilogue: O / d * sigmoid(gate), d the row sum over the lane's 16
-    // positions, lane r + 32's and the partner's; four consecutive dims per
-    // (dt, j), so one 8- or 16-byte gate load and store
+    // epilogue: merge the pair's halves, O = (O_0 f_0 + O_1 f_1) / (d_0 f_0 +
+    // d_1 f_1) with f_e = exp2(m_e - max(m_0, m_1)), d_e the row sums (the
+    // lane's 16 positions plus lane r + 32's), then * sigmoid(gate). Wave e
+    // finishes dims 128e .. 128e + 127 and hands the other half of its O^T
+    // (dim tiles 4(1 - e) ..) to the partner through LDS (lane-major, one
+    // 16-byte piece per lane and index).
     {
         const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(d_run), __float_as_uint(d_run), false, false);
         const float d = __uint_as_float(h32[0]) + __uint_as_float(h32[1]);
-        if (h == 0) xrow[wave][r] = d;
+        if (h == 0) {
+            xm[wave][r] = m_run;
+            xd[wave][r] = d;
+        }
+        f32x4_t* const xo = reinterpret_cast<f32x4_t*>(kvs[0]) + wave * 1024;   // 16 KB a wave
+        phase_barrier();   // every wave is done with the tiles
+        auto hand_over = [&](auto ev) {
+            constexpr int E = decltype(ev)::value;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xo[(4 * c + j) * 64 + lane] = f32x4_t{oacc[4 * (1 - E) + c][4 * j], oacc[4 * (1 - E) + c][4 * j + 1],
+                                                         oacc[4 * (1 - E) + c][4 * j + 2],
+                                                         oacc[4 * (1 - E) + c][4 * j + 3]};
+        };
+        if (e == 0) hand_over(std::integral_constant<int, 0>{});
+        else hand_over(std::integral_constant<int, 1>{});
         __syncthreads();
-        const float inv_d = 1.0f / (d + xrow[partner][r]);
+        const float mp = xm[partner][r], dp = xd[partner][r];
+        const float mx = fmaxf(m_run, mp);
+        const float fo = __builtin_amdgcn_exp2f(m_run - mx), fp = __builtin_amdgcn_exp2f(mp - mx);
+        const float inv_d = 1.0f / (d * fo + dp * fp);
+        const float so = fo * inv_d, sp = fp * inv_d;
+        const f32x4_t* const xq = reinterpret_cast<const f32x4_t*>(kvs[0]) + partner * 1024;
         const int tok = t0 + 4 * pr + (r >> 3);
-        if (tok < T) {
+        auto finish = [&](auto ev) {
+            constexpr int E = decltype(ev)::value;
+            if (tok >= T) return;
             const size_t qi = static_cast<size_t>(tok) * 16 + kvh * 8 + (r & 7);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int c = 0; c < 4; ++c)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int dim = 128 * e + 32 * dt + 8 * j + 4 * h;
+                    const int dim = 128 * E + 32 * c + 8 * j + 4 * h;
+                    const f32x4_t po = xq[(4 * c + j) * 64 + lane];
                     float g[4], y[4];
                     if constexpr (IN_DT == 1) {
                         const u32x2_t w = *reinterpret_cast<const u32x2_t*>(
@@ -573,7 +560,8 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                         for (int i = 0; i < 4; ++i) g[i] = w[i];
                     }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) y[i] = oacc[dt][4 * j + i] * inv_d * sigmoid(g[i]);
+                    for (int i = 0; i < 4; ++i)
+                        y[i] = (oacc[4 * E + c][4 * j + i] * so + po[i] * sp) * sigmoid(g[i]);
                     if constexpr (OUT_DT == 1) {
                         *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(out) + qi * 256 + dim) =
                             u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
@@ -582,7 +570,9 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                             f32x4_t{y[0], y[1], y[2], y[3]};
                     }
                 }
-        }
+        };
+        if (e == 0) finish(std::integral_constant<int, 0>{});
+        else finish(std::integral_constant<int, 1>{});
     }
 }
 
