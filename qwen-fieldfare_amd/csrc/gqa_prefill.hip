@@ -4,16 +4,16 @@
 // The reference has no prefill kernel: each prompt token runs the decode
 // path at its position (QwenQ4ActiveExpertStreamingRunner.swift:1545-1561,
 // 1076-1150), so token t attends to positions 0 .. start+t. This file
-// computes all T rows at once:
+// computes all T rows in two launches:
 //   prep   one wave per token: head RMSNorm + partial RoPE of the
 //          16 q heads (fp16, softmax scale folded in, to workspace: the
 //          reference also rounds q to half, Runner:1119-1126) and of the 2 k
 //          heads (appended to the cache, bf16 or fp16, together with v; a
-//          bf16 cache's new k rows also go to its fp16 copy in workspace,
-//          whose older rows k16_copy fills).
-//   vt     the transposed fp16 copy of V (per kv head and 64-position tile,
-//          dims x positions), so that the attention's V operand is one
-//          16-byte LDS read per lane.
+//          bf16 cache's new k rows also go to its fp16 copy in workspace).
+//          The same launch's other workgroups write the transposed fp16
+//          copy of V (per kv head and 64-position tile, dims x positions,
+//          so that the attention's V operand is one 16-byte LDS read per
+//          lane) and a bf16 cache's older k rows into the fp16 copy.
 //   attn   flash attention. A workgroup owns 16 query tokens x the 8 q heads
 //          of one kv head (128 rows; four wave pairs of 32 rows = 4 tokens
 //          x 8 heads, each wave running its own flash attention over half of
@@ -45,6 +45,71 @@ namespace qff {
 constexpr int kPfQB = 16;       // query tokens per workgroup
 constexpr int kPfKT = 64;       // K/V positions per tile
 
+// The transposed fp16 copy of V, per kv head and 64-position tile a
+// [256 dims][64 slots] block (the tile's 32 KB contiguous, tiles of one kv
+// head ntile_stride apart). Within each 16 slots, slot 8h + 4j + i holds
+// position 8j + 4h + i (bits 2 and 3 swapped): the order in which the
+// attention's O^T = V^T P^T operand runs over positions, so a lane's eight
+// positions are one 16-byte piece. Positions before start come from the
+// cache, start .. start + T - 1 from the step's v (rounded to the cache's
+// type first, exactly as the prep workgroups store them, so the copy holds
+// the cache's values), later ones are zero. A workgroup of 512 threads
+// stages one tile through LDS.
+__device__ __forceinline__ int vt_slot_row(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
+
+template <int IN_DT, int KV_F16>
+__device__ __forceinline__ void vt_tile_copy(const void* __restrict__ v, const uint16_t* __restrict__ vc,
+                                             uint16_t* __restrict__ vt, int tl, int kvh, int start, int n,
+                                             int ntile_stride) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64][264];   // positions x dims (+8 pad)
+    const int t = threadIdx.x;
+    const int p0 = tl * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = t + 512 * i, row = q >> 5, pc = q & 31, p = p0 + row;
+        u32x4_t w = u32x4_t{0u, 0u, 0u, 0u};
+        if (p < start) {
+            w = *reinterpret_cast<const u32x4_t*>(vc + (static_cast<size_t>(p) * 2 + kvh) * 256 + 8 * pc);
+            if (!KV_F16) w = bf16x8_to_f16x8(w);
+        } else if (p < n) {
+            const size_t src = (static_cast<size_t>(p - start) * 2 + kvh) * 256 + 8 * pc;
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = elem<IN_DT>::load(v, src + e);
+            if (KV_F16) {
+                w = u32x4_t{pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]), pack_f16x2(f[4], f[5]),
+                            pack_f16x2(f[6], f[7])};
+            } else {
+                w = bf16x8_to_f16x8(u32x4_t{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                                            pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])});
+            }
+        }
+        *reinterpret_cast<u32x4_t*>(&tile[row][8 * pc]) = w;
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<size_t>(kvh) * ntile_stride + tl) * (256 * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = t + 512 * i, d = q >> 3, sp = q & 7;   // dim d, slots 8 sp .. 8 sp + 7
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k)][d]) |
+                   (static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k + 1)][d]) << 16);
+        *reinterpret_cast<u32x4_t*>(dst + d * 64 + 8 * sp) = u32x4_t{w[0], w[1], w[2], w[3]};
+    }
+}
+
+// Launch layout of the prep kernel: vt_blocks workgroups of transposed-V
+// tiles (two per 64-position tile, one per kv head), then k16_blocks
+// workgroups copying a bf16 cache's K rows before start into the fp16 copy
+// (512 16-byte pieces each), then one workgroup per 8 tokens of the prep
+// proper. None depends on another: the copies read only rows the prep does
+// not write, or the step's inputs.
+struct PrepGrid {
+    int vt_blocks, k16_blocks, vt_stride;
+};
+
 // One wave per token, 8 per workgroup: the token's 32 RoPE angles are
 // evaluated once (lane i < 32: cos, sin of pos * f[i]) and shuffled to the
 // lanes that rotate, then the 18 head slots (0-15 the q heads, 16-17 the kv
@@ -59,9 +124,25 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
     const void* __restrict__ q_gate, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w, RopeFreqs rf, float scale,
     float eps, int start, int T, uint16_t* __restrict__ qb, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, uint16_t* __restrict__ k16) {
+    uint16_t* __restrict__ v_cache, uint16_t* __restrict__ k16, uint16_t* __restrict__ vt, PrepGrid pg) {
+    int blk = static_cast<int>(blockIdx.x);
+    if (blk < pg.vt_blocks) {
+        vt_tile_copy<IN_DT, KV_F16>(v, v_cache, vt, blk >> 1, blk & 1, start, start + T, pg.vt_stride);
+        return;
+    }
+    blk -= pg.vt_blocks;
+    if (blk < pg.k16_blocks) {
+        // the fp16 copy of bf16 K cache rows 0 .. start - 1 (both kv heads)
+        const int i = blk * 512 + static_cast<int>(threadIdx.x);
+        if (i < start * 64) {
+            const size_t o = static_cast<size_t>(i) * 8;
+            *reinterpret_cast<u32x4_t*>(k16 + o) = bf16x8_to_f16x8(*reinterpret_cast<const u32x4_t*>(k_cache + o));
+        }
+        return;
+    }
+    blk -= pg.k16_blocks;
     const int lane = threadIdx.x & 63;
-    const int tok = blockIdx.x * kPrepWaves + (threadIdx.x >> 6);
+    const int tok = blk * kPrepWaves + (threadIdx.x >> 6);
     if (tok >= T) return;
     const int pos = start + tok;
     float cs, sn;
@@ -142,55 +223,6 @@ __global__ __launch_bounds__(64 * kPrepWaves) void gqa_prefill_prep_kernel(
                 }
             }
         }
-    }
-}
-
-// The fp16 copy of bf16 K cache rows 0 .. n-1 (both kv heads): one 16-byte
-// piece per thread.
-__global__ __launch_bounds__(256) void k16_copy_kernel(const uint16_t* __restrict__ kc, uint16_t* __restrict__ k16,
-                                                       int pieces) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= pieces) return;
-    const size_t o = static_cast<size_t>(i) * 8;
-    *reinterpret_cast<u32x4_t*>(k16 + o) = bf16x8_to_f16x8(*reinterpret_cast<const u32x4_t*>(kc + o));
-}
-
-// The transposed fp16 copy of V cache rows 0 .. n-1, per kv head and
-// 64-row tile a [256 dims][64 slots] block (the tile's 32 KB contiguous,
-// tiles of one kv head ntile_stride apart). Within each 16 slots, slot
-// 8h + 4j + i holds row 8j + 4h + i (bits 2 and 3 swapped): the order in
-// which the attention's O^T = V^T P^T operand runs over positions, so a
-// lane's eight positions are one 16-byte piece. Rows >= n are zero. A block
-// of 256 threads stages one tile through LDS.
-__device__ __forceinline__ int vt_slot_row(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
-
-template <int KV_F16>
-__global__ __launch_bounds__(256) void vt_copy_kernel(const uint16_t* __restrict__ vc, uint16_t* __restrict__ vt,
-                                                      int n, int ntile_stride) {
-    __shared__ __attribute__((aligned(16))) uint16_t tile[64][264];   // rows x dims (+8 pad)
-    const int tl = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
-    const int p0 = tl * 64;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int q = t + 256 * i, row = q >> 5, pc = q & 31;
-        u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-        if (p0 + row < n) {
-            v = *reinterpret_cast<const u32x4_t*>(vc + (static_cast<size_t>(p0 + row) * 2 + kvh) * 256 + 8 * pc);
-            if (!KV_F16) v = bf16x8_to_f16x8(v);
-        }
-        *reinterpret_cast<u32x4_t*>(&tile[row][8 * pc]) = v;
-    }
-    __syncthreads();
-    uint16_t* dst = vt + (static_cast<size_t>(kvh) * ntile_stride + tl) * (256 * 64);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int q = t + 256 * i, d = q >> 3, sp = q & 7;   // dim d, slots 8 sp .. 8 sp + 7
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            w[k] = static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k)][d]) |
-                   (static_cast<uint32_t>(tile[vt_slot_row(8 * sp + 2 * k + 1)][d]) << 16);
-        *reinterpret_cast<u32x4_t*>(dst + d * 64 + 8 * sp) = u32x4_t{w[0], w[1], w[2], w[3]};
     }
 }
 
@@ -586,23 +618,26 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
     uint16_t* vc = static_cast<uint16_t*>(v_cache);
     const RopeFreqs rf = rope_freqs(p->rope_theta);
     // the attention kernel reads fp16 K (an fp16 cache itself, else the fp16
-    // copy in workspace, [max_ctx][2][256], which the prep kernel extends by
-    // the new rows and k16_copy fills below start_pos) and the transposed
-    // fp16 copy of V (vt_copy, after the prep kernel's append)
+    // copy in workspace, [max_ctx][2][256]) and the transposed fp16 copy of V
+    // ([2][max_ctx / 64][256][64] in workspace), both written by the prep
+    // launch
     uint16_t* k16 = p->kv_f16 ? kc : ctx->gqa_kv16;
-    const int vt_stride = (ctx->cfg.max_ctx + kPfKT - 1) / kPfKT;   // tiles per kv head
-    if (!p->kv_f16 && start_pos > 0) {
-        ProfScope prof(ctx, stream, "gqa_prefill_k16");
-        const int pieces = start_pos * 64;
-        k16_copy_kernel<<<(pieces + 255) / 256, 256, 0, stream>>>(kc, k16, pieces);
-    }
     {
+        // one launch: the transposed V copy (cache rows before start_pos and
+        // the step's v), the fp16 copy of a bf16 cache's K rows before
+        // start_pos, and the per-token prep (q to workspace, k / v appended,
+        // a bf16 cache's new k rows also to the fp16 copy)
         ProfScope prof(ctx, stream, "gqa_prefill_prep");
-        const int pgrid = (T + kPrepWaves - 1) / kPrepWaves;
-#define QFF_PREP(I, F)                                                                                           \
-    gqa_prefill_prep_kernel<I, F><<<pgrid, 64 * kPrepWaves, 0, stream>>>(q_gate, k, v, p->q_norm_w, p->k_norm_w, \
-                                                                        rf, p->scale, p->eps, start_pos, T, qb, \
-                                                                        kc, vc, k16)
+        PrepGrid pg;
+        pg.vt_stride = (ctx->cfg.max_ctx + kPfKT - 1) / kPfKT;   // tiles per kv head
+        pg.vt_blocks = 2 * ((start_pos + T + kPfKT - 1) / kPfKT);
+        pg.k16_blocks = p->kv_f16 ? 0 : (start_pos * 64 + 511) / 512;
+        const int grid = pg.vt_blocks + pg.k16_blocks + (T + kPrepWaves - 1) / kPrepWaves;
+#define QFF_PREP(I, F)                                                                                      \
+    gqa_prefill_prep_kernel<I, F><<<grid, 64 * kPrepWaves, 0, stream>>>(q_gate, k, v, p->q_norm_w,          \
+                                                                       p->k_norm_w, rf, p->scale, p->eps, \
+                                                                       start_pos, T, qb, kc, vc, k16,     \
+                                                                       ctx->gqa_vt, pg)
         if (p->kv_f16) {
             if (in_dtype == QFF_BF16) QFF_PREP(1, 1); else QFF_PREP(0, 1);
         } else {
@@ -610,15 +645,7 @@ hipError_t launch_gqa_prefill(qff_ctx* ctx, hipStream_t stream, const qff_gqa_pa
         }
 #undef QFF_PREP
     }
-    {
-        ProfScope prof(ctx, stream, "gqa_prefill_vt");
-        const int n = start_pos + T;
-        const dim3 vgrid((n + kPfKT - 1) / kPfKT, 2);
-        if (p->kv_f16)
-            vt_copy_kernel<1><<<vgrid, 256, 0, stream>>>(vc, ctx->gqa_vt, n, vt_stride);
-        else
-            vt_copy_kernel<0><<<vgrid, 256, 0, stream>>>(vc, ctx->gqa_vt, n, vt_stride);
-    }
+    const int vt_stride = (ctx->cfg.max_ctx + kPfKT - 1) / kPfKT;
     const dim3 grid((T + kPfQB - 1) / kPfQB, 2);
     ProfScope prof(ctx, stream, "gqa_prefill_attn");
 #define QFF_PFA(I, O) \
