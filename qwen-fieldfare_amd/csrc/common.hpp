@@ -148,4 +148,17 @@ __device__ __forceinline__ float dot4(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
+// 32-bit LDS byte address of a shared-memory element.
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint16_t*)(p)));
+}
+
+// global_load_lds_dwordx4 from base + voff (base uniform, voff a 32-bit lane
+// offset) to the LDS address in M0, lane l's 16 bytes at M0 + 16 l (the
+// s_nop is the wait state an M0 write needs before an LDS DMA). The copy
+// counts in vmcnt until its bytes are in LDS.
+__device__ __forceinline__ void dma16(const char* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+
 }  // namespace qff

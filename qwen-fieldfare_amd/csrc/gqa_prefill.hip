@@ -233,11 +233,8 @@ constexpr int kPfThreads = 512;
 // slots (128 B), piece j of row d at j ^ vt_swz(d). A K operand read (32
 // rows x one piece per 32 lanes) and a V^T operand read (32 rows x one
 // piece) then each meet every bank group equally.
-// 32-bit LDS byte address of a shared-memory element; a b128 read at one;
-// a ^ x in one VALU instruction that the compiler neither hoists nor merges.
-__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint16_t*)(p)));
-}
+// A b128 read at a 32-bit LDS byte address; a ^ x in one VALU instruction
+// that the compiler neither hoists nor merges.
 __device__ __forceinline__ u32x4_t lds_read_b128(uint32_t a) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(static_cast<uintptr_t>(a));
 }
@@ -249,13 +246,6 @@ __device__ __forceinline__ uint32_t lds_xor(uint32_t a, uint32_t x) {
 
 __device__ __forceinline__ int k_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 __device__ __forceinline__ int vt_swz(int d) { return (d >> 1) & 7; }
-
-// global_load_lds_dwordx4 from base + voff (base uniform, voff a 32-bit lane
-// offset) to the LDS address in M0, lane l's 16 bytes at M0 + 16 l (the
-// s_nop is the wait state an M0 write needs before an LDS DMA).
-__device__ __forceinline__ void dma16(const char* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
-}
 
 // One wave's 1-KB chunk c (rows 2c, 2c + 1) of a 64-row K tile, copied from
 // the fp16 cache rows p0 + 2c, p0 + 2c + 1 straight into LDS: lane l fills
