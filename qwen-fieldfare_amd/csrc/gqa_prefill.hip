@@ -317,13 +317,14 @@ __device__ __forceinline__ void phase_barrier() {
 // operand read feeds 32 rows: 32 KB of LDS reads per wave and tile.
 //
 // Schedule: one workgroup barrier per tile. Iteration kt runs S^T of tile
-// kt interleaved with O^T += V^T P^T of tile kt - 1 (operands read kLead
-// steps ahead), then the softmax of tile kt; it reads K_kt and V_{kt-1},
-// and right after its barrier every wave requests its share of K_{kt+1}
-// (into the buffer K_{kt-1} left) and of V_kt (into the one V_{kt-2}
-// left), straight into LDS, waiting for them before the next barrier.
-// All eight waves run the same schedule, two per SIMD, so one wave's
-// operand reads and softmax overlap the other's MFMAs.
+// kt interleaved step by step with O^T += V^T P^T of tile kt - 1 (operands
+// read kLead steps ahead; the wave at a raised priority), then the softmax
+// of tile kt; it reads K_kt and V_{kt-1}, and during the first half of its
+// MFMA stream (one request per step) every wave requests its share of
+// K_{kt+1} (into the buffer K_{kt-1} left) and of V_kt (into the one
+// V_{kt-2} left), straight into LDS, waiting for them before the next
+// barrier. All eight waves run the same schedule, two per SIMD, so one
+// wave's operand reads and softmax overlap the other's MFMAs.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
     const uint16_t* __restrict__ qb, const void* __restrict__ q_gate, const uint16_t* __restrict__ k16,
