@@ -515,7 +515,9 @@ __global__ __launch_bounds__(kPfThreads) void gqa_prefill_attn_kernel(
                 pa[m] = u32x4_t{pack_f16x2(pe[8 * m], pe[8 * m + 1]), pack_f16x2(pe[8 * m + 2], pe[8 * m + 3]),
                                 pack_f16x2(pe[8 * m + 4], pe[8 * m + 5]), pack_f16x2(pe[8 * m + 6], pe[8 * m + 7])};
         }
-        // this iteration's tile requests have landed
+        // this iteration's tile requests have landed (the softmax stays
+        // ahead of the wait, which it would otherwise follow)
+        __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
 
