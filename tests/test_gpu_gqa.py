@@ -217,7 +217,8 @@ def _prefill_case(hip, T, start, max_ctx, rows=None, out_dtype=torch.bfloat16, s
             assert_f32_output_close(got[t], ref)
 
 
-@pytest.mark.parametrize("T,start", [(1, 0), (17, 0), (100, 0), (64, 37), (300, 1000)])
+@pytest.mark.parametrize("T,start", [(1, 0), (17, 0), (100, 0), (64, 0), (64, 37), (128, 64), (300, 1000),
+                                     (16, 2032)])
 def test_gqa_prefill_matches_token_by_token(hip, T, start):
     _prefill_case(hip, T, start, max_ctx=2048, out_dtype=torch.float32 if T == 17 else torch.bfloat16)
 

@@ -101,7 +101,8 @@ def test_gqa_decode_f16_cache_long_context(hip):
 
 
 @pytest.mark.parametrize("T,start,out_dtype", [(1, 0, torch.bfloat16), (100, 0, torch.float32),
-                                               (64, 37, torch.bfloat16), (300, 1000, torch.bfloat16)])
+                                               (64, 37, torch.bfloat16), (128, 64, torch.bfloat16),
+                                               (300, 1000, torch.bfloat16), (16, 2032, torch.bfloat16)])
 def test_gqa_prefill_f16_cache_matches_token_by_token(hip, T, start, out_dtype):
     import qff
     max_ctx = 2048
