@@ -825,7 +825,7 @@ def main():
             configs[f"c2_gqa_decode_b{B}"] = bench_c2(ctx, B, max(args.steps * 10, 200), args.warmup)
     if "c3" in only:
         log("config 3: GQA prefill T=8192 + Q4 projections")
-        configs["c3_gqa_prefill_t8192"] = bench_c3(ctx, max(2, args.steps // 4), 1)
+        configs["c3_gqa_prefill_t8192"] = bench_c3(ctx, max(5, args.steps // 2), 3)
     if "c4" in only:
         for B, L in ((16, 32768), (1, 65536)):
             log(f"config 4: 40-layer stack decode B={B} L={L}")
