@@ -524,3 +524,54 @@ def test_gqa_prefill_config3_from_x_end_to_end(hip):
           f"max {errs.max():.3g}", flush=True)
     assert np.median(errs) <= 1.0
     ctx.close()
+
+
+def test_gqa_prefill_graph_replay(hip):
+    """qff_gqa_prefill captured in a HIP graph (T = 100 at start 37 on a bf16
+    cache, so the prep launch writes the fp16 K copy of the 37 older rows and
+    the transposed V copy beside the per-token prep) and replayed three
+    times, with an eager prefill of another shape on the same context (which
+    rewrites the workspace copies) between replays: every replay's output
+    and caches equal an eager call's on the same inputs, bit for bit."""
+    import qff
+    rng = np.random.default_rng(77)
+    p = synth.gqa_params()
+    pg = {k: f32_tensor(v) for k, v in p.items()}
+    T, start, max_ctx = 100, 37, 1024
+    qg = bf16_tensor(O.f32_to_bf16(rng.standard_normal((T, 16, 512)).astype(np.float32)))
+    kk = bf16_tensor(O.f32_to_bf16(rng.standard_normal((T, 2, 256)).astype(np.float32)))
+    vv = bf16_tensor(O.f32_to_bf16(rng.standard_normal((T, 2, 256)).astype(np.float32)))
+    kc0 = bf16_tensor(O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32)))
+    vc0 = bf16_tensor(O.f32_to_bf16(rng.standard_normal((max_ctx, 2, 256)).astype(np.float32)))
+    ctx = qff.Context(max_batch=1, max_ctx=max_ctx, max_prefill_tokens=256)
+    # the eager reference
+    kc_ref, vc_ref = kc0.clone(), vc0.clone()
+    ref = qff.gqa_prefill(ctx, pg, qg, kk, vv, kc_ref, vc_ref, start_pos=start)
+    torch.cuda.synchronize()
+    ref = ref.clone()
+    # another shape on the same context, run eagerly between replays
+    T2 = 70
+    o_args = [bf16_tensor(O.f32_to_bf16(rng.standard_normal(s).astype(np.float32)))
+              for s in ((T2, 16, 512), (T2, 2, 256), (T2, 2, 256))]
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    kc, vc = kc0.clone(), vc0.clone()
+    out = torch.empty(T, 16, 256, dtype=torch.bfloat16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        qff.gqa_prefill(ctx, pg, qg, kk, vv, kc.clone(), vc.clone(), start_pos=start, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    print(f"gqa_prefill graph capture T={T} start={start}", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qff.gqa_prefill(ctx, pg, qg, kk, vv, kc, vc, start_pos=start, out=out)
+    for rep in range(3):
+        print(f"gqa_prefill graph replay {rep}", flush=True)
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}: output"
+        assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), f"replay {rep}: caches"
+        qff.gqa_prefill(ctx, pg, *o_args, kc2, vc2, start_pos=500)
+        torch.cuda.synchronize()
