@@ -342,3 +342,44 @@ def test_q4_norm_matmul_parts_rejects_bad_calls(hip):
                                       96, 1) == -2
     with pytest.raises(ValueError):
         qff.q4_norm_matmul_parts(ctx, [(w, s, b)], x, torch.ones(64, device=DEV))
+
+
+@pytest.mark.parametrize("batch", [16, 200])
+def test_q4_matmul_parts_graph_replay(hip, batch):
+    """The three GQA in-projections (8192 + 512 + 512 rows x 2048) in one
+    call, captured in a HIP graph and replayed three times with an eager
+    product of another batch on the same context between replays (which
+    rewrites the context's x16 and token factors, or the split's partials):
+    every replay equals an eager call on the same inputs, bit for bit.
+    batch 16 runs the decode-shaped kernel, 200 the prefill GEMM."""
+    import qff
+    print(f"q4_matmul_parts graph replay batch={batch}", flush=True)
+    cols = 2048
+    ws = [synth.q4_weight(r, cols, seed=500 + r) for r in (8192, 512, 512)]
+    parts = [_w_gpu(w, s, b, "f16") for w, s, b in ws]
+    rng = np.random.default_rng(600 + batch)
+    x = bf16_tensor(O.f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32)))
+    x2 = bf16_tensor(O.f32_to_bf16(rng.standard_normal((40, cols)).astype(np.float32)))
+    ctx = qff.Context(max_batch=32, max_ctx=64, max_prefill_tokens=256)
+    ref = [o.clone() for o in qff.q4_matmul_parts(ctx, parts, x)]
+    torch.cuda.synchronize()
+    outs = [torch.empty_like(o) for o in ref]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        qff.q4_matmul_parts(ctx, parts, x, outs=outs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qff.q4_matmul_parts(ctx, parts, x, outs=outs)
+    for rep in range(3):
+        print(f"q4_matmul_parts graph replay {rep}", flush=True)
+        for o in outs:
+            o.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o.view(torch.int16), r.view(torch.int16)), f"replay {rep}"
+        qff.q4_matmul_parts(ctx, parts, x2)
+        torch.cuda.synchronize()
