@@ -439,16 +439,25 @@ void gqa_decode_partial_kernel(
 // grid (16 q heads x DS dim blocks, batch), 512 threads: attention.metal
 // :342-377 merge, then the gate of deltanet.metal:700-708, for 256 / DS dims
 // per workgroup (DS = 4 at small batches, so more than 16 workgroups share
-// the partial reads). Chunk weights are formed one thread per chunk; then
-// the 8 DS chunk streams (stream s sums chunks s, s + 8 DS, ...; 64 / DS
-// lanes per stream, a float4 of dims per lane) keep few dependent loads in
-// flight per lane, and their sums are added in LDS in a fixed order.
+// the partial reads). Chunk weights are formed one thread per chunk; the
+// 8 DS chunk streams (stream s sums chunks s, s + 8 DS, ...; 64 / DS lanes
+// per stream, a float4 of dims per lane) add their chunks in order, and
+// their sums are added in LDS in a fixed order. The loads form a short
+// chain: the (m, d) of every slot of the (sequence, kv head) and the gate
+// are requested with the positions the split reads, and each stream's first
+// four partial rows as soon as the split gives the chunk count, before the
+// maxima and weights are known. Every load is unconditional, its index
+// clamped to the workspace's slots or the call's chunks (a clamped row gets
+// no weight): a load under a branch makes the compiler wait for all loads
+// in flight where the branch ends. (Requesting the rows before the split,
+// clamped to the workspace's slots, was slower: slots past the call's
+// chunks hold rows this call did not write, which come from HBM.)
 template <int IN_DT, int OUT_DT, int DS>
 __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const void* __restrict__ q_gate, const int32_t* __restrict__ positions, int batch, int max_ctx, int target,
     int cstride, const float* __restrict__ pm, const float* __restrict__ pd, const float* __restrict__ po,
     void* __restrict__ out) {
-    constexpr int kDims = 256 / DS, kLanes = 64 / DS, kStreams = 8 * DS;
+    constexpr int kDims = 256 / DS, kLanes = 64 / DS, kStreams = 8 * DS, kRound = 4;
     __shared__ float es[kGqaMaxChunks], red[16];
     __shared__ __attribute__((aligned(16))) float osum[kStreams][kDims];
     const int h = blockIdx.x / DS, dblk = blockIdx.x % DS, seq = blockIdx.y, t = threadIdx.x;
@@ -456,6 +465,13 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const int kvh = h >> 3, hl = h & 7;
     const int d0 = dblk * kDims;
     const size_t qi = (static_cast<size_t>(seq) * 16 + h);
+    const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * cstride;
+    // every slot of this (sequence, kv head) lies in the workspace (cstride
+    // <= 512 threads); slots past the call's chunk count are masked below
+    const int ts = min(t, cstride - 1);
+    const float m_slot = pm[(base + ts) * 8 + hl];
+    const float d_slot = pd[(base + ts) * 8 + hl];
+    const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + d0 + min(t, kDims - 1));
     const int pos = positions[seq];
     if (pos < 0 || pos >= max_ctx) {
         if (t < kDims) elem<OUT_DT>::store(out, qi * 256 + d0 + t, __builtin_nanf(""));
@@ -464,10 +480,16 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     int chunk_len, unused_seq, unused_c, unused_len;
     gqa_split(positions, batch, max_ctx, target, cstride, 0, lane, chunk_len, unused_seq, unused_c, unused_len);
     const int L = pos + 1;
-    const int nc = (L + chunk_len - 1) / chunk_len;
-    const size_t base = (static_cast<size_t>(seq) * 2 + kvh) * cstride;
-    const float m = t < nc ? pm[(base + t) * 8 + hl] : -INFINITY;
-    const float d = t < nc ? pd[(base + t) * 8 + hl] : 0.0f;
+    const int nc = (L + chunk_len - 1) / chunk_len;   // <= cstride
+    const int sid = wave * DS + lane / kLanes, f = lane % kLanes;
+    // chunk c of this head at pr[c * 512]
+    const float4* pr = reinterpret_cast<const float4*>(po + (base * 8 + hl) * 256 + d0) + f;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v[kRound];
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) v[u] = pr[static_cast<size_t>(min(sid + kStreams * u, nc - 1)) * 512];
+    const float m = t < nc ? m_slot : -INFINITY;
+    const float d = t < nc ? d_slot : 0.0f;
     const float wmax = group_max<64>(m);
     if (lane == 0) red[wave] = wmax;
     __syncthreads();
@@ -479,25 +501,23 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
     const float wd = group_sum<64>(d * e);
     if (lane == 0) red[8 + wave] = wd;
     __syncthreads();
-    const int sid = wave * DS + lane / kLanes, f = lane % kLanes;
-    // chunk c of this head at pr[c * 512]
-    const float4* pr = reinterpret_cast<const float4*>(po + (base * 8 + hl) * 256 + d0) + f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int c = sid;
-    for (; c + 3 * kStreams < nc; c += 4 * kStreams) {
-        float4 v[4];
+    float4 acc = zero;
+    for (int c = sid; c < nc; c += kRound * kStreams) {
+        float4 cur[kRound];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = pr[static_cast<size_t>(c + kStreams * u) * 512];
+        for (int u = 0; u < kRound; ++u) cur[u] = v[u];
+        // the next round's rows, requested before this round's sums
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float w = es[c + kStreams * u];
-            acc.x += v[u].x * w; acc.y += v[u].y * w; acc.z += v[u].z * w; acc.w += v[u].w * w;
+        for (int u = 0; u < kRound; ++u)
+            v[u] = pr[static_cast<size_t>(min(c + kStreams * (kRound + u), nc - 1)) * 512];
+#pragma unroll
+        for (int u = 0; u < kRound; ++u) {
+            const int cc = c + kStreams * u;
+            const float w = es[min(cc, kGqaMaxChunks - 1)];
+            if (cc < nc) {
+                acc.x += cur[u].x * w; acc.y += cur[u].y * w; acc.z += cur[u].z * w; acc.w += cur[u].w * w;
+            }
         }
-    }
-    for (; c < nc; c += kStreams) {
-        const float4 v = pr[static_cast<size_t>(c) * 512];
-        const float w = es[c];
-        acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
     }
     reinterpret_cast<float4*>(osum[sid])[f] = acc;
     __syncthreads();
@@ -507,7 +527,6 @@ __global__ __launch_bounds__(512) void gqa_decode_combine_kernel(
         for (int w = 0; w < 8; ++w) D += red[8 + w];
 #pragma unroll
         for (int s2 = 0; s2 < kStreams; ++s2) O += osum[s2][t];
-        const float gate = elem<IN_DT>::load(q_gate, qi * 512 + 256 + d0 + t);
         elem<OUT_DT>::store(out, qi * 256 + d0 + t, (O / D) * sigmoid(gate));
     }
 }
