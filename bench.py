@@ -304,12 +304,16 @@ def bench_c3(ctx, steps, warmup):
         qff.q4_matmul_parts(ctx, wts, X, outs=(qg, k, v))
         qff.gqa_prefill(ctx, p, qg.view(T, 16, 512), k.view(T, 2, 256), v.view(T, 2, 256), kc, vc, 0, out=out)
 
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    # the step captured once in a HIP graph and replayed back-to-back, as the
+    # DeltaNet prefill and the 40-layer stack are timed (a prefill server
+    # replays captured steps); the eager one-call-per-launch time rides beside
+    ms_eager = timed(step, steps, warmup, torch.cuda.current_stream())
+    ms = timed_graph(step, 1, steps, warmup)
     kt, cnt = kernel_times(ctx, step, max(2, min(steps, 5)))
     # one x16 pass and one GEMM launch per step
     proj_ms = sum(v for k_, v in kt.items() if k_.startswith("q4_"))
     attn_ms = sum(v for k_, v in kt.items() if k_.startswith("gqa_prefill"))
-    return {"ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "kernels_ms": kt,
+    return {"ms_per_step": ms, "ms_per_step_eager": ms_eager, "tokens_per_s": T / (ms * 1e-3), "kernels_ms": kt,
             "roofline": mfma_roof(C3_ATTN_FLOPS + C3_PROJ_FLOPS, ms, "whole step, canonical flops"),
             "roofline_attention": mfma_roof(C3_ATTN_FLOPS, attn_ms, "attention kernels (event-timed)"),
             "roofline_projections": mfma_roof(C3_PROJ_FLOPS, proj_ms, "Q4 projection kernels (event-timed)")}
