@@ -13,10 +13,13 @@
 // w[r * cols/4 + c/4]; value = byte * scale[r, c/64] + bias[r, c/64].
 //
 // Two kernels:
-//   router_logits_kernel  one wave per (expert row, 8-token block): lane l
+//   router_logits_kernel  one wave per (expert row, block of NT tokens): lane l
 //       holds bytes 32l .. 32l+31 of each 2048-column piece (two 16-B loads),
 //       converts them with v_cvt_f32_ubyte and accumulates in fp32 in the
-//       factored form; a lane-group sum per token. x stays fp32.
+//       factored form; a lane-group sum per token. x stays fp32. All NT
+//       tokens' x loads are issued together and the logits stored at the
+//       end (a store between tokens would hold the next token's loads:
+//       vmcnt counts stores too).
 //   router_top8_kernel    one wave per token: the logits in registers (up to
 //       4 per lane), eight rounds of a wave maximum (DPP) and a ballot for
 //       the lowest index holding it, then the reference's softmax and
@@ -27,13 +30,17 @@
 
 namespace qff {
 
-constexpr int kRtTokens = 8;   // tokens per logits workgroup
+// tokens per logits workgroup: 1 for a single token, else 4 (at batch 16,
+// 4 tokens a wave: logits 7.7-7.8 us event-timed, against 11.3 with 8 and
+// 7.9-8.0 with 2; 12.3 with 8 tokens a wave each waiting for the previous
+// one's store)
+static int rt_tokens(int batch) { return batch <= 1 ? 1 : 4; }
 
 template <int I>
 __device__ __forceinline__ float rt_ubyte(uint32_t v) { return static_cast<float>((v >> (8 * I)) & 0xffu); }
 
-// grid (ceil(E / 4), ceil(batch / kRtTokens)), 256 threads; KW = 2048-column pieces
-template <int SB_DT, int X_DT, int KW>
+// grid (ceil(E / 4), ceil(batch / NT)), 256 threads; KW = 2048-column pieces
+template <int SB_DT, int X_DT, int KW, int NT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint32_t* __restrict__ w,
                                                             const uint16_t* __restrict__ scales,
                                                             const uint16_t* __restrict__ biases,
@@ -42,7 +49,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint32_t* __re
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e = blockIdx.x * 4 + wave;
     const int ec = min(e, experts - 1);
-    const int m0 = blockIdx.y * kRtTokens;
+    const int m0 = blockIdx.y * NT;
     const int G = cols / 64, W4 = cols / 4, npc = cols / 32;   // 32-byte pieces per row
     u32x4_t wq[KW][2];
     float sv[KW], bv[KW];
@@ -58,9 +65,12 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint32_t* __re
         sv[k] = elem<SB_DT>::load(scales, static_cast<size_t>(ec) * G + pcc / 2);
         bv[k] = elem<SB_DT>::load(biases, static_cast<size_t>(ec) * G + pcc / 2);
     }
-    for (int mi = 0; mi < kRtTokens; ++mi) {
-        const int m = m0 + mi;
-        if (m >= batch) break;   // wave-uniform
+    // every token of the block, its index clamped into the batch, so no load
+    // waits behind a branch or a store
+    float accs[NT];
+#pragma unroll
+    for (int mi = 0; mi < NT; ++mi) {
+        const int m = min(m0 + mi, batch - 1);
         float acc = 0.0f;
 #pragma unroll
         for (int k = 0; k < KW; ++k) {
@@ -104,8 +114,12 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint32_t* __re
             acc = fmaf(sk, dot, acc);
             acc = fmaf(bk, sum, acc);
         }
-        acc = group_sum<64>(acc);
-        if (lane == 0 && e < experts) logits[static_cast<size_t>(m) * experts + e] = acc;
+        accs[mi] = group_sum<64>(acc);
+    }
+    if (lane == 0 && e < experts) {
+#pragma unroll
+        for (int mi = 0; mi < NT; ++mi)
+            if (m0 + mi < batch) logits[static_cast<size_t>(m0 + mi) * experts + e] = accs[mi];
     }
 }
 
@@ -210,18 +224,23 @@ hipError_t launch_router_top8(qff_ctx* ctx, hipStream_t stream, const uint32_t* 
                               float* logits, int32_t* indices, float* scores, int experts, int cols, int batch) {
     const uint16_t* s = static_cast<const uint16_t*>(scales);
     const uint16_t* b = static_cast<const uint16_t*>(biases);
-    const dim3 grid((experts + 3) / 4, (batch + kRtTokens - 1) / kRtTokens);
+    const int nt = rt_tokens(batch);
+    const dim3 grid((experts + 3) / 4, (batch + nt - 1) / nt);
     const bool k2 = cols > 2048;
     {
         ProfScope prof(ctx, stream, "router_logits");
-#define QFF_RL(S, X)                                                                                              \
-    if (k2) router_logits_kernel<S, X, 2><<<grid, 256, 0, stream>>>(w, s, b, x, logits, experts, cols, batch); \
-    else router_logits_kernel<S, X, 1><<<grid, 256, 0, stream>>>(w, s, b, x, logits, experts, cols, batch)
+#define QFF_RL_NT(S, X, K)                                                                                     \
+    if (nt == 1) router_logits_kernel<S, X, K, 1><<<grid, 256, 0, stream>>>(w, s, b, x, logits, experts, cols, batch); \
+    else router_logits_kernel<S, X, K, 4><<<grid, 256, 0, stream>>>(w, s, b, x, logits, experts, cols, batch)
+#define QFF_RL(S, X)                   \
+    if (k2) { QFF_RL_NT(S, X, 2); }     \
+    else { QFF_RL_NT(S, X, 1); }
 #define QFF_RL_X(S) \
     if (x_dtype == QFF_BF16) { QFF_RL(S, 1); } else { QFF_RL(S, 0); }
         if (sb_dtype == QFF_BF16) { QFF_RL_X(1); } else { QFF_RL_X(2); }
 #undef QFF_RL_X
 #undef QFF_RL
+#undef QFF_RL_NT
     }
     ProfScope prof(ctx, stream, "router_top8");
     router_top8_kernel<<<(batch + 3) / 4, 256, 0, stream>>>(logits, indices, scores, experts, batch);
