@@ -14,6 +14,7 @@
 // 5.1 us at batch 1, where 32 workgroups cannot fill the chip.
 #include "common.hpp"
 #include "internal.hpp"
+#include "mfma.hpp"
 
 namespace qff {
 
@@ -76,7 +77,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 
     float4* S = reinterpret_cast<float4*>(ssm_state) + (static_cast<size_t>(seq) * 32 + h) * (128 * 32);
     float4 s[kNS];
 #pragma unroll
-    for (int i = 0; i < kNS; ++i) s[i] = S[(rbase + 2 * i) * 32 + col4];
+    for (int i = 0; i < kNS; ++i) {
+        // the state streams through once a step: non-temporal loads and
+        // stores (`nt`) keep it from displacing the caches' other contents
+        // (batch 32: 27.2 against 31.6 us a step; batch 16: 15.3 against 17.8)
+        const f32x4_t u = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(S) + (rbase + 2 * i) * 32 + col4);
+        s[i] = make_float4(u[0], u[1], u[2], u[3]);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const float4 ns = make_float4(st.y, st.z, st.w, xin);
     const float y = silu(ns.x * w4.x + ns.y * w4.y + ns.z * w4.z + ns.w * w4.w);
@@ -114,7 +121,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 
         const float delta = (v_s[r] - kv) * beta;
         v.x = fmaf(k4.x, delta, v.x); v.y = fmaf(k4.y, delta, v.y);
         v.z = fmaf(k4.z, delta, v.z); v.w = fmaf(k4.w, delta, v.w);
-        S[r * 32 + col4] = v;
+        __builtin_nontemporal_store(f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4_t*>(S) + r * 32 + col4);
         const float o = group_sum<32>(dot4(v, q4));
         if (col4 == 0) o_s[r] = o;
     }
