@@ -231,7 +231,9 @@ __global__ __launch_bounds__(64 * kQ4GemvMaxWaves) void q4_gemv_kernel(Q4Parts p
     for (int i = 0; i < PPT; ++i) {
         const int q = min(t + NT * i, npieces - 1);
         const int r = q / ppr, c4 = q - r * ppr;
-        wp[i] = *reinterpret_cast<const u32x4_t*>(w + static_cast<size_t>(min(R0 + r, rows - 1)) * W8 + 4 * c4);
+        // weights stream through once a call: non-temporal loads (`nt`)
+        wp[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(w + static_cast<size_t>(min(R0 + r, rows - 1)) * W8 + 4 * c4));
     }
     // scales/biases: at most SBT entries per thread
     float sreg[SBT], breg[SBT];
@@ -547,7 +549,7 @@ __global__ __launch_bounds__(256) void q4_gemv_sk_kernel(Q4Parts parts, const vo
     u32x4_t wq[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-        wq[j] = *reinterpret_cast<const u32x4_t*>(P.w + wrow * W8 + k0 / 8 + 16 * j + 4 * kb);
+        wq[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(P.w + wrow * W8 + k0 / 8 + 16 * j + 4 * kb));
     // x: token 4 i + wave, columns k0 + 8 lane .. +7
     u32x4_t xr[4][HILO ? 2 : 1];
 #pragma unroll
@@ -755,7 +757,7 @@ __global__ __launch_bounds__(64 * kQ4VecWaves) void q4_gemv1_kernel(Q4Parts part
 #pragma unroll
         for (int k = 0; k < KW; ++k) {
             const int pc = min(lane + 64 * k, npc - 1);
-            wq[r][k] = *reinterpret_cast<const u32x4_t*>(w + row * W8 + 4 * pc);
+            wq[r][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(w + row * W8 + 4 * pc));   // read once: `nt`
             sv[r][k] = elem<SB_DT>::load(scales, row * G + pc / 2);
             bv[r][k] = elem<SB_DT>::load(biases, row * G + pc / 2);
         }
